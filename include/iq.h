@@ -1,0 +1,128 @@
+/*
+ * iq.h -- C ABI of the MI355X (gfx950) quantized-weight matrix path.
+ *
+ * Drop-in boundary for the quantised part of the reference's device ABI
+ * (RyanXiaoo/infer kernels/ops/ops.cuh:165-178).  Plain C: no HIP, CUDA or
+ * torch types; device memory is passed as plain pointers owned by the caller,
+ * the stream as an opaque pointer (a hipStream_t; NULL = the null stream).
+ *
+ * Layout (the reference's src/quant.h:34-58, produced by src/quant.cpp and
+ * tools/quantize.cpp), one [rows x cols] matrix, row-major, groups of
+ * IQ_GROUP consecutive columns along a row:
+ *   q       int8: rows*cols bytes (two's complement codes -127..127)
+ *           int4: rows*cols/2 bytes, element (r,c) in byte (r*cols+c)/2,
+ *                 low nibble when c is even (codes 0..15)
+ *   scales  bf16 bits, rows x ceil(cols/128)
+ *   zeros   int4 only: u8 zero points, rows x ceil(cols/128); NULL for int8
+ *   dequant: int8 w = s*q ; int4 w = s*(q - z)          (src/quant.cpp:86-93)
+ *
+ * Every entry point enqueues work on `stream` and returns without
+ * synchronising.  Return value: 0 on success, a negative IQ_E* code when the
+ * arguments are rejected on the host (nothing was enqueued), or a positive
+ * hipError_t when the HIP runtime reported an error.  No exception crosses
+ * this boundary.  Calls that share a device share one workspace: calls on
+ * different streams of one device must not overlap in time.
+ */
+#ifndef IQ_H
+#define IQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IQ_GROUP 128
+
+/* gpu::QuantKind (kernels/ops/ops.cuh:165): kInt8 = 0, kInt4 = 1. */
+enum { IQ_INT8 = 0, IQ_INT4 = 1 };
+
+/* Error codes (negative). */
+enum {
+    IQ_OK = 0,
+    IQ_EKIND = -1,      /* kind is neither IQ_INT8 nor IQ_INT4 */
+    IQ_ESHAPE = -2,     /* inconsistent or unsupported sizes */
+    IQ_ENULL = -3,      /* a required pointer is NULL */
+    IQ_ETOOLARGE = -4,  /* problem exceeds the workspace limits */
+    IQ_ENOMEM = -5,     /* workspace allocation failed */
+    IQ_EDEVICE = -6     /* no usable gfx950 device */
+};
+
+/* gpu::QuantView (kernels/ops/ops.cuh:166-172), byte-compatible on LP64:
+ * a 4-byte kind, 4 bytes padding, then rows/cols/groups and three pointers. */
+typedef struct iq_view {
+    int32_t kind;
+    int64_t rows, cols, groups;  /* groups = ceil(cols / 128) */
+    const uint8_t* q;
+    const uint16_t* scales;
+    const uint8_t* zeros;        /* int4: rows*groups bytes; int8: NULL */
+} iq_view;
+
+/* y[b, o] = sum_c dequant(W, o, c) * x[b, c] (+ bf16 bias[o]), b < B, o < out.
+ * Replaces launch_gemv_batched_q (kernels/ops/ops.cuh:173-174,
+ * kernels/ops/quant.cu:312-345).  1 <= B <= 32.  x is fp32 [B][in]
+ * (only B rows are read; the reference reads up to 32), y fp32 [B][out]
+ * (only B rows are written).  in == W->cols, out == W->rows.  bias may be NULL. */
+int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64_t in,
+            int64_t out, float* y, void* stream);
+
+/* The two halves of iq_gemv, for callers that multiply one activation
+ * block by several matrices (q/k/v, gate/up share their input):
+ * iq_gemv_prep converts x [B][in] (fp32) once into the device workspace
+ * (fp16 hi/lo pairs with a power-of-two scale per row and 128-column group,
+ * in the column order that `kind`'s dequantisation produces);
+ * iq_gemv_prepped then runs the GEMV of any matrix of that kind and width on
+ * the prepared block.  A prepared block stays valid until the next
+ * iq_gemv / iq_gemv_prep on the device (stream order).  iq_gemv_prepped
+ * returns IQ_ESHAPE when (B, in, kind) differ from the last preparation.
+ * No reference counterpart: the reference's launcher re-reads x per matrix. */
+int iq_gemv_prep(const float* x, int B, int64_t in, int kind, void* stream);
+int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
+                    float* y, void* stream);
+
+/* Same contract for any T >= 1 (fp32 activations).  Replaces
+ * launch_gemm_tiled_q (kernels/ops/ops.cuh:175-176, kernels/ops/quant.cu:347-351).
+ * Runs the MFMA prefill GEMM with the activations split into bf16 hi + lo. */
+int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,
+            int64_t out, float* y, void* stream);
+
+/* Prefill GEMM with bf16 activations x [T][in] (bf16 bits), fp32 output.
+ * No reference counterpart (the reference's activations are fp32); it is the
+ * bf16-activation form of iq_gemm used for the Qwen2.5-7B prefill shapes. */
+int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int64_t T,
+                  int64_t in, int64_t out, float* y, void* stream);
+
+/* The quantised linear call site, GpuBatch::Impl::linear_b
+ * (kernels/batch_gpu.cu:137-147): T <= 32 -> iq_gemv, T > 32 -> iq_gemm. */
+int iq_linear(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,
+              int64_t out, float* y, void* stream);
+
+/* out[t, i] = dequant(table, ids[t], i), exactly.  Replaces launch_embedding_q
+ * (kernels/ops/ops.cuh:177-178, kernels/ops/quant.cu:304-309,353-357).
+ * H == table->cols.  An id outside [0, rows) yields a row of NaN (the
+ * reference reads out of bounds). */
+int iq_embedding(const iq_view* table, const int64_t* ids, int64_t T, int64_t H, float* out,
+                 void* stream);
+
+/* On-device quantize + pack of a bf16 [rows x cols] matrix, bit-exact to
+ * llm::quantize (src/quant.cpp:34-84, src/quant.h:61), which the reference
+ * runs on the CPU only (tools/quantize.cpp:30-49).  Writes q, scales and (int4)
+ * zeros in the layout above.  int4 needs even cols (as the reference). */
+int iq_quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, int kind, uint8_t* q,
+                uint16_t* scales, uint8_t* zeros, void* stream);
+
+/* Reserve the per-device workspace (done lazily by the first call that needs
+ * it).  Call before capturing a graph.  Returns 0 or an error code. */
+int iq_init(int device);
+
+/* Static description of an error code (never NULL). */
+const char* iq_error_string(int code);
+
+/* Library version string. */
+const char* iq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IQ_H */

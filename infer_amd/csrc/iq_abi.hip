@@ -1,0 +1,228 @@
+// iq_abi.hip -- the extern "C" boundary (include/iq.h): argument validation,
+// the per-device workspace, and dispatch to the gfx950 kernels.
+//
+// Validation mirrors what the reference rejects on the host
+// (src/quant.cpp:35-36 kind / odd int4 cols; src/quant.cpp:204-205 shape
+// mismatch) and adds the checks a C boundary needs (null pointers, sizes the
+// kernels assume).  Nothing is enqueued when a check fails.
+#include <mutex>
+
+#include "../../include/iq.h"
+#include "iq_internal.h"
+
+namespace iq {
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+Workspace g_ws[kMaxDevices];
+int g_cus[kMaxDevices];
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+hipError_t create_workspace(int dev, Workspace* ws) {
+    const size_t cnt = align256(sizeof(int) * kMaxCounters);
+    const size_t inv = align256(sizeof(float) * kMaxRowsGemv * (kMaxKp / kGroup));
+    const size_t xb = align256(sizeof(_Float16) * kMaxRowsGemv * kMaxKp);
+    const size_t part = align256(sizeof(float) * kPartialFloats);
+    const size_t total = cnt + inv + 2 * xb + part;
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, total);
+    if (e != hipSuccess) return e;
+    // Counters start at zero; each split-K launch leaves them at zero.
+    e = hipMemset(base, 0, cnt);
+    if (e != hipSuccess) { (void)hipFree(base); return e; }
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) { (void)hipFree(base); return e; }
+    char* p = static_cast<char*>(base);
+    ws->base = base;
+    ws->bytes = total;
+    ws->counters = reinterpret_cast<int*>(p);
+    ws->xinv = reinterpret_cast<float*>(p + cnt);
+    ws->xh = reinterpret_cast<_Float16*>(p + cnt + inv);
+    ws->xl = reinterpret_cast<_Float16*>(p + cnt + inv + xb);
+    ws->partials = reinterpret_cast<float*>(p + cnt + inv + 2 * xb);
+    (void)dev;
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t get_workspace(Workspace** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_ws[dev].base) {
+        e = create_workspace(dev, &g_ws[dev]);
+        if (e != hipSuccess) return e;
+    }
+    *out = &g_ws[dev];
+    return hipSuccess;
+}
+
+int device_cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int v = __atomic_load_n(&g_cus[dev], __ATOMIC_RELAXED);
+    if (v > 0) return v;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    __atomic_store_n(&g_cus[dev], cus, __ATOMIC_RELAXED);
+    return cus;
+}
+
+}  // namespace iq
+
+namespace {
+
+int from_hip(hipError_t e) { return e == hipSuccess ? IQ_OK : int(e); }
+
+// Shared view checks; `in`/`out` must match the matrix (quant.cpp:204-205).
+int check_view(const iq_view* W, int64_t in, int64_t out) {
+    if (!W) return IQ_ENULL;
+    if (W->kind != IQ_INT8 && W->kind != IQ_INT4) return IQ_EKIND;
+    if (W->rows <= 0 || W->cols <= 0) return IQ_ESHAPE;
+    if (W->groups != (W->cols + IQ_GROUP - 1) / IQ_GROUP) return IQ_ESHAPE;
+    if (in != W->cols || out != W->rows) return IQ_ESHAPE;
+    if (W->kind == IQ_INT4 && (W->cols % 2)) return IQ_ESHAPE;
+    if (!W->q || !W->scales) return IQ_ENULL;
+    if (W->kind == IQ_INT4 && !W->zeros) return IQ_ENULL;
+    return IQ_OK;
+}
+
+iq::QView to_qview(const iq_view* W) {
+    iq::QView v;
+    v.kind = W->kind;
+    v.rows = W->rows;
+    v.cols = W->cols;
+    v.groups = W->groups;
+    v.q = W->q;
+    v.scales = W->scales;
+    v.zeros = W->kind == IQ_INT4 ? W->zeros : nullptr;
+    return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+int iq_init(int device) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return from_hip(e);
+    if (device != cur) {
+        e = hipSetDevice(device);
+        if (e != hipSuccess) return from_hip(e);
+    }
+    iq::Workspace* ws = nullptr;
+    e = iq::get_workspace(&ws);
+    (void)iq::device_cu_count();
+    if (device != cur) (void)hipSetDevice(cur);
+    return from_hip(e);
+}
+
+int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
+            float* y, void* stream) {
+    int rc = check_view(W, in, out);
+    if (rc) return rc;
+    if (!x || !y) return IQ_ENULL;
+    if (B < 1 || B > iq::kMaxRowsGemv) return IQ_ESHAPE;
+    if (W->groups * IQ_GROUP > iq::kMaxKp) return IQ_ETOOLARGE;
+    iq::Workspace* ws = nullptr;
+    hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    return from_hip(iq::launch_gemv(x, to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
+}
+
+int iq_gemv_prep(const float* x, int B, int64_t in, int kind, void* stream) {
+    if (kind != IQ_INT8 && kind != IQ_INT4) return IQ_EKIND;
+    if (!x) return IQ_ENULL;
+    if (B < 1 || B > iq::kMaxRowsGemv || in < 1) return IQ_ESHAPE;
+    if (kind == IQ_INT4 && (in % 2)) return IQ_ESHAPE;
+    if ((in + IQ_GROUP - 1) / IQ_GROUP * IQ_GROUP > iq::kMaxKp) return IQ_ETOOLARGE;
+    iq::Workspace* ws = nullptr;
+    hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    return from_hip(iq::launch_xprep(x, B, in, kind, ws, static_cast<hipStream_t>(stream)));
+}
+
+int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
+                    float* y, void* stream) {
+    int rc = check_view(W, in, out);
+    if (rc) return rc;
+    if (!y) return IQ_ENULL;
+    iq::Workspace* ws = nullptr;
+    hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    if (B != ws->prep_M || in != ws->prep_K || W->kind != ws->prep_kind) return IQ_ESHAPE;
+    return from_hip(iq::launch_gemv_prepped(to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
+}
+
+int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,
+            int64_t out, float* y, void* stream) {
+    int rc = check_view(W, in, out);
+    if (rc) return rc;
+    if (!x || !y) return IQ_ENULL;
+    if (T < 1) return IQ_ESHAPE;
+    if ((T + 127) / 128 * ((out + 127) / 128) > 0x7fffffff) return IQ_ETOOLARGE;
+    return from_hip(iq::launch_gemm(x, nullptr, to_qview(W), bias, T, y, static_cast<hipStream_t>(stream)));
+}
+
+int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int64_t T,
+                  int64_t in, int64_t out, float* y, void* stream) {
+    int rc = check_view(W, in, out);
+    if (rc) return rc;
+    if (!x || !y) return IQ_ENULL;
+    if (T < 1) return IQ_ESHAPE;
+    if ((T + 127) / 128 * ((out + 127) / 128) > 0x7fffffff) return IQ_ETOOLARGE;
+    return from_hip(iq::launch_gemm(nullptr, x, to_qview(W), bias, T, y, static_cast<hipStream_t>(stream)));
+}
+
+int iq_linear(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,
+              int64_t out, float* y, void* stream) {
+    if (T >= 1 && T <= iq::kMaxRowsGemv) return iq_gemv(x, W, bias, int(T), in, out, y, stream);
+    return iq_gemm(x, W, bias, T, in, out, y, stream);
+}
+
+int iq_embedding(const iq_view* table, const int64_t* ids, int64_t T, int64_t H, float* out,
+                 void* stream) {
+    if (!table) return IQ_ENULL;
+    int rc = check_view(table, H, table->rows);
+    if (rc) return rc;
+    if (!ids || !out) return IQ_ENULL;
+    if (T < 1) return IQ_ESHAPE;
+    return from_hip(iq::launch_embedding(to_qview(table), ids, T, H, out, static_cast<hipStream_t>(stream)));
+}
+
+int iq_quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, int kind, uint8_t* q,
+                uint16_t* scales, uint8_t* zeros, void* stream) {
+    if (kind != IQ_INT8 && kind != IQ_INT4) return IQ_EKIND;
+    if (rows <= 0 || cols <= 0) return IQ_ESHAPE;
+    if (kind == IQ_INT4 && (cols % 2)) return IQ_ESHAPE;
+    if (!w_bf16 || !q || !scales || (kind == IQ_INT4 && !zeros)) return IQ_ENULL;
+    const int64_t waves = rows * (((cols + IQ_GROUP - 1) / IQ_GROUP + 3) / 4);
+    if ((waves + 3) / 4 > 0x7fffffff) return IQ_ETOOLARGE;
+    return from_hip(iq::launch_quantize(w_bf16, rows, cols, kind, q, scales, zeros, static_cast<hipStream_t>(stream)));
+}
+
+const char* iq_error_string(int code) {
+    switch (code) {
+        case IQ_OK: return "ok";
+        case IQ_EKIND: return "iq: quant kind must be IQ_INT8 (0) or IQ_INT4 (1)";
+        case IQ_ESHAPE: return "iq: inconsistent or unsupported shape";
+        case IQ_ENULL: return "iq: required pointer is NULL";
+        case IQ_ETOOLARGE: return "iq: problem exceeds workspace limits";
+        case IQ_ENOMEM: return "iq: workspace allocation failed";
+        case IQ_EDEVICE: return "iq: no usable device";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "iq: unknown error";
+}
+
+const char* iq_version(void) { return "iq 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,305 @@
+// iq_gemm.hip -- quantised prefill GEMM on gfx950 MFMA (bf16 in, fp32 out).
+//
+// Replaces gemm_tiled_q_kernel (kernels/ops/quant.cu:254-302, fp32 SIMT
+// 64x64 tiles).  y[t,n] = sum_k x[t,k] * dequant(W,n,k) (+ bias[n]).
+//
+// Tiling: a 256-thread workgroup (4 waves, 2x2) owns a 128 (activation rows)
+// x 128 (output features) tile; each wave a 64x64 block = 2x2 MFMA
+// f32_32x32x16_bf16 tiles.  K advances 64 columns per step through
+// double-buffered LDS: the next step's activation and weight bytes are
+// loaded into registers while the current step's MFMAs run, then written to
+// the other buffer -- the weights dequantised on the way in (int8 code, or
+// int4 q - z, as an exact bf16 integer).  The bf16 scale of each 128-column
+// group multiplies the fp32 MFMA partial of that group (acc += s * P_g), so
+// the matrix core only ever sees exact integers on the weight side.
+// Activations: bf16 as given (iq_gemm_bf16x), or fp32 split on the way into
+// LDS into bf16 hi + lo (x = hi + lo + O(2^-16 |x|)), two MFMAs per step.
+// Block order is XCD-aware: consecutive tiles along the activation rows of
+// one weight-column block land on the same XCD, so a weight tile is fetched
+// from HBM once per XCD and re-read from that XCD's L2.
+#include "iq_internal.h"
+
+namespace iq {
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64, LDSW = BK + 8;  // LDS row pitch (bf16)
+constexpr int kThreads = 256;
+
+struct GemmParams {
+    const float* xf;      // fp32 activations [T][K] or null
+    const uint16_t* xb;   // bf16 activations [T][K] or null
+    const uint8_t* q;
+    const uint16_t* scales;
+    const uint8_t* zeros;
+    const uint16_t* bias;
+    float* y;
+    int64_t T, N, K, G;
+    int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ uint32_t bf16_pair_from_f32(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+// Exact bf16 of a small integer (|v| < 256).
+__device__ __forceinline__ uint32_t bf16_pair_int(int a, int b) {
+    return bf16_pair_from_f32(float(a), float(b));
+}
+
+template <int KIND, bool XF32, bool FASTW, bool FASTX>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDSW];
+    __shared__ __attribute__((aligned(16))) uint16_t Al[XF32 ? 2 : 1][XF32 ? BM : 1][LDSW];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][LDSW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
+    // contiguous run of tiles (a bijection on [0, ntiles)).
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int b = blockIdx.x;
+    const int xcd = b % 8, base = ntiles / 8, extra = ntiles % 8;
+    const int t = xcd * base + (xcd < extra ? xcd : extra) + b / 8;
+    const int tm = t % p.tiles_m, tn = t / p.tiles_m;
+    const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
+
+    const int64_t row_bytes = KIND == 1 ? p.K / 2 : p.K;
+    const int nk = int((p.K + BK - 1) / BK);
+
+    // ---- register staging of one K step
+    constexpr int XCH = XF32 ? 8 : 4;           // 16-byte activation chunks per thread
+    constexpr int WCH = KIND == 1 ? 1 : 2;      // 16-byte weight chunks per thread
+    uint4 xr[XCH];
+    uint4 wr[WCH];
+    uint32_t zr = 0;
+
+    auto load_step = [&](int kt) {
+        const int64_t k0 = int64_t(kt) * BK;
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            const int c = tid + kThreads * i;
+            if (XF32) {
+                const int row = c >> 4, kc = c & 15;  // 16 chunks of 4 floats per row
+                const int64_t m = m0 + row, k = k0 + kc * 4;
+                if (m < p.T && FASTX) {
+                    xr[i] = *reinterpret_cast<const uint4*>(p.xf + m * p.K + k);
+                } else {
+                    float f[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) f[e] = (m < p.T && k + e < p.K) ? p.xf[m * p.K + k + e] : 0.0f;
+                    xr[i] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+                }
+            } else {
+                const int row = c >> 3, kc = c & 7;  // 8 chunks of 8 bf16 per row
+                const int64_t m = m0 + row, k = k0 + kc * 8;
+                if (m < p.T && FASTX) {
+                    xr[i] = *reinterpret_cast<const uint4*>(p.xb + m * p.K + k);
+                } else {
+                    uint32_t h[4] = {0, 0, 0, 0};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (m < p.T && k + e < p.K) h[e / 2] |= uint32_t(p.xb[m * p.K + k + e]) << (16 * (e & 1));
+                    xr[i] = make_uint4(h[0], h[1], h[2], h[3]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < WCH; i++) {
+            const int c = tid + kThreads * i;
+            int row, kc;
+            int64_t off;
+            if (KIND == 1) { row = c >> 1; kc = c & 1; off = (k0 + kc * 32) / 2; }
+            else { row = c >> 2; kc = c & 3; off = k0 + kc * 16; }
+            const int64_t n = n0 + row;
+            if (n < p.N) {
+                const uint8_t* qr = p.q + n * row_bytes;
+                if (FASTW) {
+                    wr[i] = *reinterpret_cast<const uint4*>(qr + off);
+                } else {
+                    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        if (off + e < row_bytes) w[e / 4] |= uint32_t(qr[off + e]) << (8 * (e % 4));
+                    wr[i] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+                if (KIND == 1) zr = p.zeros[n * p.G + k0 / kGroup];
+            } else {
+                wr[i] = make_uint4(0, 0, 0, 0);
+                zr = 0;
+            }
+        }
+    };
+
+    auto store_step = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            const int c = tid + kThreads * i;
+            if (XF32) {
+                const int row = c >> 4, kc = c & 15;
+                const float f[4] = {__uint_as_float(xr[i].x), __uint_as_float(xr[i].y),
+                                    __uint_as_float(xr[i].z), __uint_as_float(xr[i].w)};
+                uint32_t hi[2], lo[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint16_t h0 = f32_to_bf16(f[2 * e]), h1 = f32_to_bf16(f[2 * e + 1]);
+                    const float r0 = f[2 * e] - bf16_to_f32(h0), r1 = f[2 * e + 1] - bf16_to_f32(h1);
+                    hi[e] = uint32_t(h0) | (uint32_t(h1) << 16);
+                    lo[e] = uint32_t(f32_to_bf16(r0)) | (uint32_t(f32_to_bf16(r1)) << 16);
+                }
+                *reinterpret_cast<uint2*>(&As[buf][row][kc * 4]) = make_uint2(hi[0], hi[1]);
+                *reinterpret_cast<uint2*>(&Al[XF32 ? buf : 0][XF32 ? row : 0][kc * 4]) = make_uint2(lo[0], lo[1]);
+            } else {
+                const int row = c >> 3, kc = c & 7;
+                *reinterpret_cast<uint4*>(&As[buf][row][kc * 8]) = xr[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < WCH; i++) {
+            const int c = tid + kThreads * i;
+            const uint32_t d[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+            if (KIND == 1) {
+                const int row = c >> 1, kc = c & 1;
+                const int z = int(zr);
+                uint32_t o[16];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t byte = (d[j] >> (8 * e)) & 0xFF;
+                        o[j * 4 + e] = bf16_pair_int(int(byte & 0xF) - z, int(byte >> 4) - z);
+                    }
+                }
+                uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][row][kc * 32]);
+                dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+                dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+                dst[2] = make_uint4(o[8], o[9], o[10], o[11]);
+                dst[3] = make_uint4(o[12], o[13], o[14], o[15]);
+            } else {
+                const int row = c >> 2, kc = c & 3;
+                uint32_t o[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int8_t b0 = int8_t(d[j] & 0xFF), b1 = int8_t((d[j] >> 8) & 0xFF);
+                    const int8_t b2 = int8_t((d[j] >> 16) & 0xFF), b3 = int8_t(d[j] >> 24);
+                    o[2 * j] = bf16_pair_int(b0, b1);
+                    o[2 * j + 1] = bf16_pair_int(b2, b3);
+                }
+                uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][row][kc * 16]);
+                dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+                dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+            }
+        }
+    };
+
+    float16_t acc[2][2], P[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) { acc[i][j][r] = 0.0f; P[i][j][r] = 0.0f; }
+
+    // Scale row pointers of this lane's two output columns.
+    int64_t ncol[2];
+    bool nval[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        ncol[j] = n0 + wn * 64 + j * 32 + (lane & 31);
+        nval[j] = ncol[j] < p.N;
+    }
+
+    load_step(0);
+    store_step(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load_step(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ks++) {
+            const int kof = ks * 16 + 8 * (lane >> 5);
+            bf16x8_t a[2], al[2], bw[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * 64 + i * 32 + (lane & 31)][kof]);
+                if (XF32) al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[XF32 ? buf : 0][XF32 ? wm * 64 + i * 32 + (lane & 31) : 0][kof]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bw[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][wn * 64 + j * 32 + (lane & 31)][kof]);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    P[i][j] = mfma32_bf16(a[i], bw[j], P[i][j]);
+                    if (XF32) P[i][j] = mfma32_bf16(al[i], bw[j], P[i][j]);
+                }
+        }
+        // Close the 128-column group after its second 64-column step (or at the end).
+        if ((kt & 1) || kt + 1 == nk) {
+            const int64_t g = kt / 2;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const float s = nval[j] ? bf16_to_f32(p.scales[ncol[j] * p.G + g]) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        acc[i][j][r] = __builtin_fmaf(s, P[i][j][r], acc[i][j][r]);
+                        P[i][j][r] = 0.0f;
+                    }
+            }
+        }
+        if (kt + 1 < nk) store_step(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds rows m = 8*(r/4) + 4*(lane/32) + r%4 of each 32x32 tile.
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        if (!nval[j]) continue;
+        const float bv = p.bias ? bf16_to_f32(p.bias[ncol[j]]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                if (m < p.T) p.y[m * p.N + ncol[j]] = acc[i][j][r] + bv;
+            }
+    }
+}
+
+template <int KIND, bool XF32>
+void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
+    const unsigned grid = unsigned(p.tiles_m * p.tiles_n);
+    if (fastw && fastx) gemm_kernel<KIND, XF32, true, true><<<grid, kThreads, 0, stream>>>(p);
+    else if (fastw) gemm_kernel<KIND, XF32, true, false><<<grid, kThreads, 0, stream>>>(p);
+    else if (fastx) gemm_kernel<KIND, XF32, false, true><<<grid, kThreads, 0, stream>>>(p);
+    else gemm_kernel<KIND, XF32, false, false><<<grid, kThreads, 0, stream>>>(p);
+}
+
+}  // namespace
+
+hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
+                       const uint16_t* bias, int64_t T, float* y, hipStream_t stream) {
+    GemmParams p;
+    p.xf = x_f32; p.xb = x_bf16;
+    p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
+    p.T = T; p.N = W.rows; p.K = W.cols; p.G = W.groups;
+    p.tiles_m = int((T + BM - 1) / BM);
+    p.tiles_n = int((p.N + BN - 1) / BN);
+    const bool fastw = (p.K % kGroup == 0);
+    const uintptr_t xa = x_f32 ? reinterpret_cast<uintptr_t>(x_f32) : reinterpret_cast<uintptr_t>(x_bf16);
+    const bool fastx = (p.K % BK == 0) && (xa % 16 == 0);
+    if (x_f32) {
+        if (W.kind == 1) launch_gemm_t<1, true>(p, fastw, fastx, stream);
+        else launch_gemm_t<0, true>(p, fastw, fastx, stream);
+    } else {
+        if (W.kind == 1) launch_gemm_t<1, false>(p, fastw, fastx, stream);
+        else launch_gemm_t<0, false>(p, fastw, fastx, stream);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace iq

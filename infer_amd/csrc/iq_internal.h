@@ -1,0 +1,61 @@
+// iq_internal.h -- declarations shared by the HIP translation units of
+// libiq.so (kernel launchers and the per-device workspace).  Not installed;
+// the public boundary is include/iq.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "iq_device.h"
+
+namespace iq {
+
+// Kernel-argument copy of iq_view / gpu::QuantView (kernels/ops/ops.cuh:166-172).
+struct QView {
+    int32_t kind;  // 0 int8, 1 int4
+    int64_t rows, cols, groups;
+    const uint8_t* q;
+    const uint16_t* scales;
+    const uint8_t* zeros;
+};
+
+// Per-device scratch used by the GEMV: fp16 hi/lo activations, per-row
+// power-of-two prescale, split-K partial sums and split-K arrival counters.
+struct Workspace {
+    void* base = nullptr;
+    size_t bytes = 0;
+    int* counters = nullptr;   // kMaxCounters ints, zero between launches
+    float* xinv = nullptr;     // kMaxRowsGemv floats
+    _Float16* xh = nullptr;    // kMaxRowsGemv * kMaxKp
+    _Float16* xl = nullptr;
+    float* partials = nullptr; // kPartialFloats
+    // Shape of the activations last prepared into xh/xl/xinv (host-side record).
+    int prep_M = 0;
+    int64_t prep_K = 0;
+    int prep_kind = -1;
+};
+
+constexpr int kMaxRowsGemv = 32;            // GpuBatch::kMaxRows (kernels/batch_gpu.h:80)
+constexpr int64_t kMaxKp = 131072;          // padded K limit of the GEMV
+constexpr int64_t kMaxCounters = 65536;
+constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K partials
+
+// Returns the workspace of the current device, allocating it on first use.
+hipError_t get_workspace(Workspace** ws);
+
+hipError_t launch_quantize(const uint16_t* w, int64_t rows, int64_t cols, int kind, uint8_t* q,
+                           uint16_t* scales, uint8_t* zeros, hipStream_t stream);
+hipError_t launch_embedding(const QView& t, const int64_t* ids, int64_t T, int64_t H, float* out,
+                            hipStream_t stream);
+hipError_t launch_gemv(const float* x, const QView& W, const uint16_t* bias, int M, float* y,
+                       Workspace* ws, hipStream_t stream);
+hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream);
+hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
+                               hipStream_t stream);
+hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
+                       const uint16_t* bias, int64_t T, float* y, hipStream_t stream);
+
+// Device properties used by the dispatch heuristics.
+int device_cu_count();
+
+}  // namespace iq

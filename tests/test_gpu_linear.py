@@ -1,0 +1,122 @@
+"""GEMV / GEMM / embedding parity through the C ABI against the oracle:
+float64 over dequant() (tests/test_ops_gpu.cu:664-692), conditioning-normalised
+error <= 5e-6 and max|y-ref|/max|ref| <= 1e-3, canaries past y, ragged shapes."""
+import numpy as np
+import pytest
+import torch
+
+from infer_amd import ops
+from oracle import oracle as O
+from tests.gpu_util import QFix, bias_of, check_linear, out_buffer, say, CANARY
+
+pytestmark = pytest.mark.gpu
+
+# tests/test_ops_gpu.cu:886-893 shapes (in, out) and T values
+REF_SHAPES = [(128, 64), (130, 127), (896, 300), (1536, 65)]
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("T", [1, 5, 32, 70])
+@pytest.mark.parametrize("bias", [False, True])
+def test_reference_shapes(kind, T, bias):
+    rng = np.random.default_rng(20260919 + T + kind)
+    for K, N in REF_SHAPES:
+        W = QFix(rng, N, K, kind)
+        x = rng.standard_normal((T, K), dtype=np.float32)
+        bb, bd = bias_of(rng, N) if bias else (None, None)
+        y = out_buffer(T, N)
+        say("linear ref-shape", kind, T, K, N, bias)
+        ops.launch_linear_q(torch.from_numpy(x).cuda(), W.view, bd, T, K, N, y)
+        torch.cuda.synchronize()
+        check_linear(y, x, W, bb, T, f"kind={kind} T={T} {N}x{K}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 12, 16, 17, 32])
+def test_gemv_15b_mlp_shapes(kind, M):
+    rng = np.random.default_rng(77 + M)
+    for N, K in ((8960, 1536), (1536, 8960)):
+        W = QFix(rng, N, K, kind, sd=0.02)
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        y = out_buffer(M, N)
+        say("gemv 1.5B", kind, M, N, K)
+        ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+        torch.cuda.synchronize()
+        check_linear(y, x, W, None, M, f"gemv kind={kind} M={M} {N}x{K}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemv_7b_down_and_wide_activations(kind):
+    """K = 18944 (split-K path) and activations spanning many decades
+    (the per-group power-of-two prescale keeps fp16 in range)."""
+    rng = np.random.default_rng(3)
+    N, K = 3584, 18944
+    W = QFix(rng, N, K, kind, sd=0.02)
+    for M in (1, 16):
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        x *= np.float32(10.0) ** rng.integers(-6, 6, size=(M, K)).astype(np.float32)
+        x[0, :128] *= np.float32(1e6)  # beyond fp16 range without prescale
+        y = out_buffer(M, N)
+        say("gemv 7B down wide", kind, M)
+        ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+        torch.cuda.synchronize()
+        check_linear(y, x, W, None, M, f"gemv wide kind={kind} M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemv_deterministic(kind):
+    rng = np.random.default_rng(4)
+    N, K = 3584, 18944
+    W = QFix(rng, N, K, kind, sd=0.02)
+    x = torch.from_numpy(rng.standard_normal((4, K), dtype=np.float32)).cuda()
+    ys = []
+    for _ in range(3):
+        y = torch.empty(4, N, device="cuda")
+        ops.launch_gemv_batched_q(x, W.view, None, 4, K, N, y)
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2])
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("T", [33, 256, 300])
+def test_gemm_fp32(kind, T):
+    rng = np.random.default_rng(500 + T)
+    for N, K in ((640, 1536), (300, 896), (127, 130)):
+        W = QFix(rng, N, K, kind, sd=0.02)
+        x = rng.standard_normal((T, K), dtype=np.float32)
+        bb, bd = bias_of(rng, N)
+        y = out_buffer(T, N)
+        say("gemm fp32", kind, T, N, K)
+        ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, bd, T, K, N, y)
+        torch.cuda.synchronize()
+        check_linear(y, x, W, bb, T, f"gemm kind={kind} T={T} {N}x{K}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemm_bf16x(kind):
+    rng = np.random.default_rng(9)
+    for T, N, K in ((1024, 512, 3584), (200, 384, 18944), (37, 130, 130)):
+        W = QFix(rng, N, K, kind, sd=0.02)
+        xb = O.seeded_bf16(rng, (T, K), 1.0)
+        x = O.bf16_to_f32(xb)
+        y = out_buffer(T, N)
+        say("gemm bf16x", kind, T, N, K)
+        ops.launch_gemm_bf16x(torch.from_numpy(xb.view(np.int16)).cuda(), W.view, None, T, K, N, y)
+        torch.cuda.synchronize()
+        check_linear(y, x, W, None, T, f"gemm bf16x kind={kind} T={T} {N}x{K}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_embedding_exact(kind):
+    rng = np.random.default_rng(8)
+    W = QFix(rng, 50, 256, kind)
+    ids = np.array([0, 49, 7, 7], np.int64)
+    out = torch.full((len(ids) * 256 + 16,), CANARY, device="cuda")
+    say("embedding", kind)
+    ops.launch_embedding_q(W.view, torch.from_numpy(ids).cuda(), len(ids), 256, out)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    ref = O.embedding(W.q, W.s, W.z, kind, 256, ids)
+    assert np.array_equal(o[: ids.size * 256].reshape(len(ids), 256), ref)
+    assert np.all(o[ids.size * 256:] == CANARY)

@@ -1,0 +1,75 @@
+"""On-device quantize + pack (iq_quantize) is bit-exact to the reference's
+llm::quantize (src/quant.cpp:34-84): against the fixtures written by the
+reference's own compiled quantiser, and against the pinned oracle on random
+and full Qwen2.5-7B shapes."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from infer_amd import ops
+from oracle import oracle as O
+from tests.gpu_util import say
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
+
+
+def gpu_quantize(w_bits, kind):
+    rows, cols = w_bits.shape
+    if isinstance(w_bits, torch.Tensor):
+        w = w_bits.cuda()
+    else:
+        w = torch.from_numpy(np.ascontiguousarray(w_bits).view(np.int16)).cuda()
+    v = ops.quantize(w, kind)
+    torch.cuda.synchronize()
+    q = v.q.cpu().numpy()
+    s = v.scales.cpu().numpy().view(np.uint16).reshape(rows, -1)
+    z = v.zeros.cpu().numpy().reshape(rows, -1) if kind == 1 else None
+    return q, s, z
+
+
+def test_quantize_matches_reference_fixtures():
+    g = np.load(GOLD, allow_pickle=False)
+    keys = sorted({k.rsplit("_", 1)[0] for k in g.files})
+    for key in keys:
+        kind = 0 if key.startswith("int8") else 1
+        say("quantize fixture", key)
+        q, s, z = gpu_quantize(g[key + "_w"], kind)
+        assert np.array_equal(q, g[key + "_q"]), key
+        assert np.array_equal(s, g[key + "_s"]), key
+        if kind == 1:
+            assert np.array_equal(z, g[key + "_z"]), key
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("shape", [(1, 2), (3, 130), (7, 254), (64, 1536), (33, 8960), (5, 1000)])
+def test_quantize_random_vs_oracle(kind, shape):
+    rng = np.random.default_rng(100 + shape[1] + kind)
+    w = O.seeded_bf16(rng, shape, 0.05)
+    # sprinkle exact-tie and zero groups
+    w[0, : min(shape[1], 128)] = O.f32_to_bf16(np.zeros(min(shape[1], 128), np.float32))
+    say("quantize random", kind, shape)
+    q, s, z = gpu_quantize(w, kind)
+    rq, rs, rz = O.quantize(w, kind)
+    assert np.array_equal(q, rq)
+    assert np.array_equal(s, rs)
+    if kind == 1:
+        assert np.array_equal(z, rz)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_quantize_7b_shapes_bit_exact(kind):
+    """Full 7B matrices: gate/up 18944x3584 and down 3584x18944, plus q/k."""
+    for i, (rows, cols) in enumerate([(18944, 3584), (3584, 18944), (512, 3584)]):
+        gen = torch.Generator(device="cuda").manual_seed(1234 + i)
+        w = (torch.randn(rows, cols, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        say("quantize 7B", kind, rows, cols)
+        q, s, z = gpu_quantize(w.view(torch.int16), kind)
+        wb = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        rq, rs, rz = O.quantize(wb, kind)
+        assert np.array_equal(s, rs)
+        assert np.array_equal(q, rq)
+        if kind == 1:
+            assert np.array_equal(z, rz)
