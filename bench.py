@@ -1,0 +1,416 @@
+#!/usr/bin/env python3
+"""bench.py -- headline benchmark of the quantized-weight matrix path on one
+MI355X.
+
+Step (the timed unit): one decode step's worth of quantised linears of
+Qwen2.5-7B at 1 activation row: 28 layers x (q 3584x3584,
+k/v 512x3584, o 3584x3584, gate/up 18944x3584, down 3584x18944) in int4
+(group 128, bf16 scale, u8 zero point) plus the int8 lm_head 152064x3584,
+weights seeded ~N(0, 0.02) -> bf16 -> quantised on the device (bit-exact to
+src/quant.cpp), activations fp32 ~N(0, 1).  The step is issued the way a
+decode engine issues it -- activations prepared once per distinct input
+(attention input, attention context, MLP input, MLP hidden, final norm),
+then one GEMV per matrix -- and captured in one HIP graph, as the
+reference's engine captures its step (kernels/batch_gpu.cu:255-269).
+
+value = packed weight bytes + activation bytes read + output bytes written,
+per step, / time per step (GB/s).  All inputs are resident in HBM before the
+timed region; the 7B set is ~4 GB, far beyond the 256 MB MALL, so each step
+streams the weights from HBM.
+
+Also reported (measured after the timed region, outside it):
+  roofline   the GEMV kernel alone (int4, 1 row) from HIP events around each
+             launch on its stream, bytes-weighted over the 196 layer matrices;
+  cpu_baseline  the reference CPU path (src/forward.cpp linear over dequant(),
+             restated in oracle/iq_oracle.c) on a bounded sample, 1 thread;
+  detail     int4 at 16 rows, the int8 set at 1 and 16 rows, the prefill GEMM
+             (config 5), on-device quantize, configs 1-3.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "dequant-GEMV GB/s & % HBM peak, 7B int4/int8 at 1/16 rows; prefill TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+H7, I7, NH7, KV7, V7, L7 = 3584, 18944, 28, 4, 152064, 28
+H15, I15, L15 = 1536, 8960, 28
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_shapes(H, I, q_out, kv_out):
+    # (name, out, in, activation slot)
+    return [("q", q_out, H, "attn"), ("k", kv_out, H, "attn"), ("v", kv_out, H, "attn"),
+            ("o", H, q_out, "ctx"), ("gate", I, H, "mlp"), ("up", I, H, "mlp"), ("down", H, I, "hid")]
+
+
+class Model:
+    """Seeded quantised linears of one model, resident on the device."""
+
+    def __init__(self, torch, ops, kind, H, I, q_out, kv_out, layers, head=None, seed=0):
+        self.torch, self.ops = torch, ops
+        self.kind = kind
+        self.H, self.I = H, I
+        self.shapes = layer_shapes(H, I, q_out, kv_out)
+        self.layers = []
+        gen = torch.Generator(device="cuda")
+        for li in range(layers):
+            mats = {}
+            for j, (name, out, inn, slot) in enumerate(self.shapes):
+                gen.manual_seed(seed * 1000003 + li * 16 + j)
+                mats[name] = quantize_seeded(torch, ops, kind, out, inn, gen)
+            self.layers.append(mats)
+        self.head = None
+        if head is not None:
+            hk, V = head
+            gen.manual_seed(seed * 1000003 + 999)
+            self.head = quantize_seeded(torch, ops, hk, V, H, gen)
+
+    def weight_bytes(self):
+        n = sum(W.nbytes() for L in self.layers for W in L.values())
+        return n + (self.head.nbytes() if self.head is not None else 0)
+
+
+def quantize_seeded(torch, ops, kind, out, inn, gen):
+    w = (torch.randn(out, inn, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    W = ops.quantize(w.view(torch.int16), kind)
+    del w
+    return W
+
+
+class Step:
+    """One decode step over a Model at M rows: the op list and its bytes."""
+
+    def __init__(self, torch, ops, model, M, seed=1):
+        self.torch, self.ops, self.model, self.M = torch, ops, model, M
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        H, I = model.H, model.I
+        self.x = {"attn": torch.randn(M, H, generator=g, device="cuda"),
+                  "ctx": torch.randn(M, model.layers[0]["o"].cols, generator=g, device="cuda"),
+                  "mlp": torch.randn(M, H, generator=g, device="cuda"),
+                  "hid": torch.randn(M, I, generator=g, device="cuda"),
+                  "head": torch.randn(M, H, generator=g, device="cuda")}
+        self.y = {name: torch.empty(M, out, device="cuda") for name, out, _, _ in model.shapes}
+        if model.head is not None:
+            self.y["head"] = torch.empty(M, model.head.rows, device="cuda")
+        # op list: ("prep", slot, kind) | ("gemv", W, yname)
+        self.ops_list = []
+        for L in model.layers:
+            last = None
+            for name, out, inn, slot in model.shapes:
+                if slot != last:
+                    self.ops_list.append(("prep", slot, model.kind))
+                    last = slot
+                self.ops_list.append(("gemv", L[name], name))
+        if model.head is not None:
+            self.ops_list.append(("prep", "head", model.head.kind))
+            self.ops_list.append(("gemv", model.head, "head"))
+        self.bytes = 0
+        for op in self.ops_list:
+            if op[0] == "gemv":
+                W = op[1]
+                self.bytes += W.nbytes() + 4 * M * W.cols + 4 * M * W.rows
+
+    def run(self, timing=None):
+        ops, M = self.ops, self.M
+        cur = None
+        for op in self.ops_list:
+            if op[0] == "prep":
+                x = self.x[op[1]]
+                ops.gemv_prep(x, M, x.shape[1], op[2])
+            else:
+                W, yname = op[1], op[2]
+                if timing is not None:
+                    timing.append((W, self.torch.cuda.Event(enable_timing=True),
+                                   self.torch.cuda.Event(enable_timing=True)))
+                    timing[-1][1].record()
+                ops.gemv_prepped(W, None, M, W.cols, W.rows, self.y[yname])
+                if timing is not None:
+                    timing[-1][2].record()
+
+    def capture(self):
+        torch = self.torch
+        self.run()  # eager warm-up: workspace and code objects resident
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.run()
+        torch.cuda.synchronize()
+        return g
+
+
+def time_graph(torch, g, steps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+def kernel_roofline(torch, step, only_kind=None):
+    """Per-launch GEMV kernel durations from HIP events on the launch stream.
+    The queue is backed up with a device-side sleep first so that the events
+    bracket kernels that run back to back."""
+    timing = []
+    torch.cuda._sleep(int(2.4e9 * 0.05))
+    step.run(timing)
+    torch.cuda.synchronize()
+    tot_b, tot_ms, n = 0, 0.0, 0
+    for W, a, b in timing:
+        if only_kind is not None and W.kind != only_kind:
+            continue
+        ms = a.elapsed_time(b)
+        tot_b += W.nbytes() + 4 * step.M * W.cols + 4 * step.M * W.rows
+        tot_ms += ms
+        n += 1
+    return tot_b, tot_ms, n
+
+
+def cpu_baseline(torch, model, seconds=10.0):
+    """oracle/iq_oracle.c iqo_linear_q_f32 (= src/forward.cpp:35-47 over
+    dequant(), one thread) on layer matrices of the same model, until about
+    `seconds` of CPU work; returns (GB/s of packed weights, sample text)."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(0)
+    done_b, t_tot, n = 0, 0.0, 0
+    names = []
+    for li, L in enumerate(model.layers):
+        for name, out, inn, slot in model.shapes:
+            W = L[name]
+            q = W.q.cpu().numpy()
+            s = W.scales.cpu().numpy().view(np.uint16).reshape(W.rows, W.groups)
+            z = W.zeros.cpu().numpy().reshape(W.rows, W.groups) if W.zeros is not None else None
+            x = rng.standard_normal((1, W.cols), dtype=np.float32)
+            t0 = time.perf_counter()
+            O.linear_q_f32(x, q, s, z, int(W.kind), None, W.rows)
+            t_tot += time.perf_counter() - t0
+            done_b += W.nbytes()
+            n += 1
+            names.append(f"L{li}.{name}")
+            if t_tot >= seconds:
+                break
+        if t_tot >= seconds:
+            break
+    return done_b / t_tot / 1e9, f"{n} matrices ({names[0]}..{names[-1]}), {done_b / 1e6:.0f} MB packed, {t_tot:.1f} s"
+
+
+def bench_gemm(torch, ops, kind, T, N, K, reps=10, seed=5):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    W = quantize_seeded(torch, ops, kind, N, K, g)
+    x = torch.randn(T, K, generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty(T, N, device="cuda")
+    for _ in range(2):
+        ops.launch_gemm_bf16x(x.view(torch.int16), W, None, T, K, N, y)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ops.launch_gemm_bf16x(x.view(torch.int16), W, None, T, K, N, y)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return ms, 2.0 * T * N * K / (ms * 1e-3) / 1e12
+
+
+def bench_gemv_single(torch, ops, kind, N, K, M, copies, reps=200, seed=11):
+    """One matrix shape rotated over `copies` distinct weight copies (beyond the
+    MALL), iq_gemv per call, captured in a graph of `copies` launches."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Ws = [quantize_seeded(torch, ops, kind, N, K, g) for _ in range(copies)]
+    x = torch.randn(M, K, generator=g, device="cuda")
+    y = torch.empty(M, N, device="cuda")
+
+    def run():
+        for W in Ws:
+            ops.launch_gemv_batched_q(x, W, None, M, K, N, y)
+    run()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        run()
+    reps_g = max(1, reps // copies)
+    ms_step, _ = time_graph(torch, gr, reps_g, 2)
+    per_ms = ms_step / copies
+    nb = Ws[0].nbytes() + 4 * M * K + 4 * M * N
+    del Ws, gr
+    torch.cuda.empty_cache()
+    return per_ms * 1e3, nb / (per_ms * 1e-3) / 1e9
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline only (no detail / CPU baseline)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the quantized-weight path is single-GPU here, see DESIGN.md for how it would shard.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from infer_amd import ops
+    ops.init(0)
+    t_setup = time.perf_counter()
+
+    # ---- headline: 7B int4 set + int8 lm_head, 1 row
+    m4 = Model(torch, ops, 1, H7, I7, NH7 * 128, KV7 * 128, L7, head=(0, V7), seed=7)
+    torch.cuda.synchronize()
+    log(f"setup int4 7B: {m4.weight_bytes() / 1e9:.3f} GB packed in {time.perf_counter() - t_setup:.1f} s")
+    st = Step(torch, ops, m4, 1)
+    g = st.capture()
+    ms_wall, ms_ev = time_graph(torch, g, args.steps, args.warmup)
+    step_bytes = st.bytes
+    value = step_bytes / (ms_wall * 1e-3) / 1e9
+    log(f"int4 M=1: {ms_wall * 1e3:.1f} us/step wall, {ms_ev * 1e3:.1f} us events, {value:.0f} GB/s")
+
+    # roofline of the dominant kernel (int4 GEMV, 1 row)
+    rb, rms, rn = kernel_roofline(torch, st, only_kind=1)
+    achieved = rb / (rms * 1e-3) / 1e9
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "gemv_int4_7b_m1_traffic.json")
+    if os.path.exists(prof):
+        try:
+            traffic = json.load(open(prof)).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "gemv_kernel<int4, 1 row-tile, R=2> over the 196 int4 layer matrices",
+                "launches": rn, "avg_launch_us": round(rms * 1e3 / max(rn, 1), 3),
+                "algorithmic_bytes_per_launch": int(rb / max(rn, 1))}
+    del g
+
+    detail = {}
+    cpu = None
+    if not args.quick:
+        st16 = Step(torch, ops, m4, 16)
+        g16 = st16.capture()
+        ms16, _ = time_graph(torch, g16, args.steps, args.warmup)
+        detail["7b_int4_m16"] = {"us_per_step": round(ms16 * 1e3, 1),
+                                 "GBps": round(st16.bytes / (ms16 * 1e-3) / 1e9, 1),
+                                 "ratio_vs_m1": round(ms16 / ms_wall, 3)}
+        del g16, st16
+        cpu_gbs, cpu_sample = cpu_baseline(torch, m4, args.cpu_seconds)
+        cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "oracle iqo_linear_q_f32 (src/forward.cpp:35-47 over dequant(), scalar fp32, "
+                         "1 thread) on the 7B int4 layer matrices at 1 row: " + cpu_sample}
+        del m4, st
+        torch.cuda.empty_cache()
+
+        # int8 set
+        t0 = time.perf_counter()
+        m8 = Model(torch, ops, 0, H7, I7, NH7 * 128, KV7 * 128, L7, head=(0, V7), seed=8)
+        torch.cuda.synchronize()
+        tq = time.perf_counter() - t0
+        for M in (1, 16):
+            s8 = Step(torch, ops, m8, M)
+            g8 = s8.capture()
+            ms8, _ = time_graph(torch, g8, args.steps, args.warmup)
+            detail[f"7b_int8_m{M}"] = {"us_per_step": round(ms8 * 1e3, 1),
+                                       "GBps": round(s8.bytes / (ms8 * 1e-3) / 1e9, 1)}
+            del g8, s8
+        detail["7b_int8_setup_s"] = round(tq, 2)
+        del m8
+        torch.cuda.empty_cache()
+
+        # on-device quantize+pack throughput (gate/up shape, int8 and int4)
+        gq = torch.Generator(device="cuda").manual_seed(3)
+        w = (torch.randn(I7, H7, generator=gq, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+        for kind, kn in ((0, "int8"), (1, "int4")):
+            out = ops.alloc_quant(kind, I7, H7)
+            for _ in range(2):
+                ops.quantize(w, kind, out=out)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                ops.quantize(w, kind, out=out)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / 10
+            nb = 2 * I7 * H7 + out.nbytes()
+            detail[f"quantize_{kn}_18944x3584"] = {"us": round(ms * 1e3, 1), "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
+        del w
+        # prefill GEMM (config 5), int8, bf16 activations, T = 1024
+        for (N, K, nm) in ((I7, H7, "gate_up"), (H7, I7, "down")):
+            ms, tf = bench_gemm(torch, ops, 0, 1024, N, K)
+            detail[f"prefill_int8_{nm}_1024"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
+                                                 "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        # config 1: int8 8960x1536, 1 row, rotated over 64 copies
+        us, gbs = bench_gemv_single(torch, ops, 0, I15, H15, 1, copies=64)
+        detail["cfg1_int8_8960x1536_m1"] = {"us": round(us, 2), "GBps": round(gbs, 1)}
+        # config 2: 1.5B int4 layer set x 28, 1 row
+        m15 = Model(torch, ops, 1, H15, I15, 12 * 128, 2 * 128, L15, seed=15)
+        s15 = Step(torch, ops, m15, 1)
+        g15 = s15.capture()
+        ms15, _ = time_graph(torch, g15, args.steps, args.warmup)
+        detail["cfg2_1.5b_int4_28layers_m1"] = {"us_per_layer_set": round(ms15 * 1e3 / L15, 2),
+                                                "us_total": round(ms15 * 1e3, 1),
+                                                "GBps": round(s15.bytes / (ms15 * 1e-3) / 1e9, 1)}
+        del g15, s15, m15
+        torch.cuda.empty_cache()
+        # config 3: M sweep on the 1.5B MLP shapes
+        sweep = {}
+        for kind, kn in ((0, "int8"), (1, "int4")):
+            for (N, K, nm) in ((I15, H15, "gate"), (H15, I15, "down")):
+                base = None
+                row = {}
+                for M in (1, 2, 4, 5, 8, 12, 16, 32):
+                    us, gbs = bench_gemv_single(torch, ops, kind, N, K, M, copies=32, reps=128)
+                    base = base or us
+                    row[str(M)] = {"us": round(us, 2), "GBps": round(gbs, 1), "x_m1": round(us / base, 3)}
+                sweep[f"{kn}_{nm}_{N}x{K}"] = row
+        detail["cfg3_sweep"] = sweep
+
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-7B decode linear set, int4 group-128 (bf16 scale, u8 zero) x 28 layers "
+                        "(q,k,v,o,gate,up,down) + int8 lm_head 152064x3584, 1 activation row, HIP graph",
+            "rows": 1,
+            "bytes_per_step": int(step_bytes),
+            "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+            "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(rec), flush=True)
+
+if __name__ == "__main__":
+    main()

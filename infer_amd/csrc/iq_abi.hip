@@ -22,11 +22,12 @@ int g_cus[kMaxDevices];
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 hipError_t create_workspace(int dev, Workspace* ws) {
+    const int64_t gmax = kMaxKp / kGroup;
     const size_t cnt = align256(sizeof(int) * kMaxCounters);
-    const size_t inv = align256(sizeof(float) * kMaxRowsGemv * (kMaxKp / kGroup));
-    const size_t xb = align256(sizeof(_Float16) * kMaxRowsGemv * kMaxKp);
+    const size_t xq = align256(size_t(kMaxRowsGemv) * gmax * 3 * kGroup);
+    const size_t meta = align256(sizeof(int4) * gmax * kMaxRowsGemv);
     const size_t part = align256(sizeof(float) * kPartialFloats);
-    const size_t total = cnt + inv + 2 * xb + part;
+    const size_t total = cnt + xq + meta + part;
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, total);
     if (e != hipSuccess) return e;
@@ -39,10 +40,9 @@ hipError_t create_workspace(int dev, Workspace* ws) {
     ws->base = base;
     ws->bytes = total;
     ws->counters = reinterpret_cast<int*>(p);
-    ws->xinv = reinterpret_cast<float*>(p + cnt);
-    ws->xh = reinterpret_cast<_Float16*>(p + cnt + inv);
-    ws->xl = reinterpret_cast<_Float16*>(p + cnt + inv + xb);
-    ws->partials = reinterpret_cast<float*>(p + cnt + inv + 2 * xb);
+    ws->xq = reinterpret_cast<int8_t*>(p + cnt);
+    ws->xmeta = reinterpret_cast<int4*>(p + cnt + xq);
+    ws->partials = reinterpret_cast<float*>(p + cnt + xq + meta);
     (void)dev;
     return hipSuccess;
 }

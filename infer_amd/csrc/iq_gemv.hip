@@ -1,61 +1,89 @@
-// iq_gemv.hip -- dequant GEMV for 1..32 activation rows on gfx950 MFMA.
+// iq_gemv.hip -- dequant GEMV for 1..32 activation rows on gfx950 int8 MFMA.
 //
 // Replaces the reference's gemv_q_direct_kernel / gemv_batched_q_kernel
 // (kernels/ops/quant.cu:71-252) and their dispatch (quant.cu:312-345).
-// Semantics: y[m,n] = sum_k dequant(W,n,k) * x[m,k] (+ bias[n]).
+// Semantics: y[m,n] = sum_k dequant(W,n,k) * x[m,k] (+ bias[n]),
+// dequant = s * q (int8) or s * (q - z) (int4), s a bf16 scale per
+// 128-column group (src/quant.cpp:86-93).
 //
-// Two launches:
-//  1. xprep: the fp32 activations are cut into 128-column groups (the weight
-//     group size).  Each (row, group) is scaled by a power of two 2^e chosen
-//     from its absmax so that it fits fp16's range, then split exactly-ish
-//     into fp16 hi + lo (x*2^e = hi + lo + O(2^-22)).  hi/lo are written in
-//     the column order the weight dequantisation produces (see iq_device.h),
-//     2^-e is kept per (group, row).  Scaling by a power of two is exact.
-//  2. gemv: MFMA f32_16x16x32_f16 with the activations as the A operand
-//     (16 rows, zero beyond M) and the weights as B (16 output rows per
-//     tile).  Weight codes stream from HBM as 16-byte loads per lane (a wave
-//     reads 16 rows x 64 contiguous bytes per instruction) and are turned
-//     into exact fp16 integers in registers (q or q - z).  Per 128-column
-//     group the MFMA partial D_g = sum (q-z)*(hi+lo) is formed from zero and
-//     folded into the fp32 accumulator as acc += (s * 2^-e) * D_g, so the
-//     bf16 scale and the activation prescale are applied in fp32.  A wave
-//     owns R tiles of 16 rows (register tiling: the activation fragments
-//     are loaded once per group and reused by all R tiles) and one slice of
-//     the groups.  When the groups are split across waves (split-K, to put
-//     enough waves on the 256 CUs for short-and-wide matrices), every wave
-//     writes its partial sums, and the last wave to finish a row block
-//     (counted with a device-scope atomic) adds the S partials in slice order
-//     - deterministic - adds the bias and writes y.  The counter is reset by
-//     that wave, so the kernel needs no clearing between launches and can be
-//     captured in a graph.
+// The weight codes are integers, so the matrix core multiplies them as
+// integers: v_mfma_i32_16x16x64_i8.  The fp32 activations are turned into
+// integers once per call (xprep):
+//   per (activation row m, 128-column group g): 2^k with
+//   max|x| * 2^k in [2^21, 2^22), X = rint(x * 2^k) (exact scaling, one
+//   rounding: |x*2^k - X| <= 1/2, i.e. 2^-22 of the group's max), and X is
+//   written as three signed byte limbs, X = 2^16 X0 + 2^8 X1 + X2.
+// The GEMV then forms, per (row tile, group), three exact int32 sums
+//   S_L = sum_k q_k * X_L,k        (L = 0, 1, 2; 6 MFMAs per 128 columns)
+// and for int4 subtracts the zero point exactly in integers,
+//   T_L = S_L - z * sum_k X_L,k    (the limb sums come with the limbs),
+// so the only floating-point steps are
+//   acc += ldexp(s * (65536 T_0 + 256 T_1 + T_2), -k)       (fp32).
+// The int8 codes go to the MFMA untouched; int4 nibbles need one AND (even
+// columns) or one shift + AND (odd columns) per 4 codes.
 //
-// Accuracy: weight and activation fragments are exact up to the 2^-22
-// relative hi/lo residual; products are exact in the MFMA and accumulate in
-// fp32.  The result is within a few fp32 ulps of the conditioning
-// sum |w*x|, inside the reference test's 5e-6 (tests/test_ops_gpu.cu:199-206).
+// Accuracy: the activation rounding is at most 2^-22 of the group's largest
+// |x| per element, products and sums are exact integers, and the fp32
+// combination adds a few ulps: far inside the reference's 5e-6 of the
+// conditioning sum |w*x| (tests/test_ops_gpu.cu:199-206).  Non-finite
+// activations make the affected outputs NaN.
+//
+// Two kernels:
+//  * gemv1 (1 row, the decode step): workgroup = W waves on one tile of 16
+//    output rows, the waves split K (reduced through LDS, deterministic; no
+//    cross-workgroup traffic).  A wave requests all weight words, scales and
+//    zero points of a batch of groups before it waits, stages the batch's
+//    activation limbs in its own LDS slot and runs the MFMAs.
+//  * gemv (2..32 rows): workgroup = 4 waves x R tiles of 16 rows on one slice
+//    of K; the slice's activation limbs are staged once per workgroup in
+//    LDS and shared by all 4R tiles.  Slices are split across workgroups
+//    when the matrix is too short to fill the GPU; the last workgroup of a
+//    row block adds the slice partials in slice order (deterministic) and
+//    resets its counter, so no clearing is needed between launches.
+#include <cstdlib>
+
 #include "iq_internal.h"
 
 namespace iq {
 
 namespace {
 
-constexpr int kWaves = 4;  // waves per workgroup
-constexpr int kXinvStride = kMaxRowsGemv;
+typedef int int4v_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMeta = kMaxRowsGemv;   // meta records per group (one per row slot)
+constexpr int kLimbRec = 3 * kGroup;  // bytes of limbs per (row, group)
+
+__device__ __forceinline__ int4v_t mfma_i8(int4v_t a, int4v_t b, int4v_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int4v_t u4_to_i4v(uint4 v) {
+    return int4v_t{int(v.x), int(v.y), int(v.z), int(v.w)};
+}
+
+// Position of natural column c (0..127) inside a group's limb record.
+//   int8 weights: natural order.
+//   int4 weights: the lane owning bytes [16j, 16j+16) of a row's 64-byte
+//   group splits them into even columns (low nibbles) and odd columns (high
+//   nibbles); record = [even columns of j = 0..3 | odd columns of j = 0..3].
+__host__ __device__ constexpr int limb_pos(int c, bool perm) {
+    return perm ? (c & 1) * 64 + (c >> 5) * 16 + ((c & 31) >> 1) : c;
+}
 
 // ------------------------------------------------------------------ xprep
+// One wave per (row, 4 groups); 16 lanes per group, 8 columns per lane.
 template <bool PERM, bool VECX>
 __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int M, int64_t K,
-                                                    int64_t G, int64_t Kp, int64_t quads,
-                                                    _Float16* __restrict__ xh,
-                                                    _Float16* __restrict__ xl,
-                                                    float* __restrict__ xinv) {
+                                                    int64_t G, int64_t quads,
+                                                    int8_t* __restrict__ xq, int4* __restrict__ meta) {
     const int lane = threadIdx.x & 63;
     const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (wave >= int64_t(M) * quads) return;
     const int m = int(wave / quads);
     const int64_t g = (wave % quads) * 4 + (lane >> 4);
     const bool gvalid = g < G;
-    const int64_t c0 = g * kGroup + (lane & 15) * 8;
+    const int j = lane & 15;
+    const int64_t c0 = g * kGroup + j * 8;
     const float* xr = x + int64_t(m) * K;
     float v[8];
     if (VECX && gvalid && c0 + 8 <= K) {
@@ -67,50 +95,95 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = (gvalid && c0 + i < K) ? xr[c0 + i] : 0.0f;
     }
+    // absmax; NaN must not be lost (fmaxf drops it), so track finiteness apart.
     float amax = 0.0f;
+    int fin = 1;
 #pragma unroll
-    for (int i = 0; i < 8; i++) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+    for (int i = 0; i < 8; i++) {
+        const float a = __builtin_fabsf(v[i]);
+        fin &= int(a <= 3.402823466e38f);
+        amax = fmaxf(amax, a);
+    }
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
-    // 2^k with amax * 2^k in [2^14, 2^15): |hi| stays below fp16's 65504.
+    for (int off = 8; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+        fin &= __shfl_xor(fin, off, 16);
+    }
     int k = 0;
-    if (amax > 0.0f && amax <= 3.0e38f) {
+    if (fin && amax > 0.0f) {
         int E;
         (void)frexpf(amax, &E);  // amax = f * 2^E, f in [0.5, 1)
-        k = 15 - E;
-        k = k < -126 ? -126 : (k > 127 ? 127 : k);
+        k = 22 - E;              // amax * 2^k in [2^21, 2^22)
     }
-    const float sc = ldexpf(1.0f, k);
-    if (!gvalid) return;
-    uint32_t hb[4], lb[4];
+    int X[8];
 #pragma unroll
-    for (int o = 0; o < 8; o += 2) {
-        const int i0 = PERM ? perm8(o) : o, i1 = PERM ? perm8(o + 1) : o + 1;
-        const float a0 = v[i0] * sc, a1 = v[i1] * sc;
-        const _Float16 h0 = _Float16(a0), h1 = _Float16(a1);
-        const _Float16 l0 = _Float16(a0 - float(h0)), l1 = _Float16(a1 - float(h1));
-        hb[o / 2] = uint32_t(__builtin_bit_cast(uint16_t, h0)) | (uint32_t(__builtin_bit_cast(uint16_t, h1)) << 16);
-        lb[o / 2] = uint32_t(__builtin_bit_cast(uint16_t, l0)) | (uint32_t(__builtin_bit_cast(uint16_t, l1)) << 16);
+    for (int i = 0; i < 8; i++) X[i] = fin ? int(__builtin_rintf(ldexpf(v[i], k))) : 0;
+    // balanced byte limbs: X = 2^16 x0 + 2^8 x1 + x2, each in [-128, 127]
+    int l0[8], l1[8], l2[8];
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int a2 = int(int8_t(X[i] & 0xFF));
+        const int r1 = (X[i] - a2) >> 8;
+        const int a1 = int(int8_t(r1 & 0xFF));
+        const int a0 = (r1 - a1) >> 8;
+        l0[i] = a0; l1[i] = a1; l2[i] = a2;
+        s0 += a0; s1 += a1; s2 += a2;
     }
-    *reinterpret_cast<uint4*>(xh + int64_t(m) * Kp + c0) = make_uint4(hb[0], hb[1], hb[2], hb[3]);
-    *reinterpret_cast<uint4*>(xl + int64_t(m) * Kp + c0) = make_uint4(lb[0], lb[1], lb[2], lb[3]);
-    if ((lane & 15) == 0) xinv[g * kXinvStride + m] = ldexpf(1.0f, -k);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+        s0 += __shfl_xor(s0, off, 16);
+        s1 += __shfl_xor(s1, off, 16);
+        s2 += __shfl_xor(s2, off, 16);
+    }
+    if (!gvalid) return;
+    int8_t* rec = xq + (int64_t(m) * G + g) * kLimbRec;
+    const int* L[3] = {l0, l1, l2};
+    if (PERM) {
+        // columns 8j..8j+7: evens -> 4 contiguous bytes, odds -> 4 contiguous bytes
+        const int pe = limb_pos(j * 8, true), po = limb_pos(j * 8 + 1, true);
+#pragma unroll
+        for (int li = 0; li < 3; li++) {
+            uint32_t ev = 0, od = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                ev |= uint32_t(uint8_t(L[li][2 * e])) << (8 * e);
+                od |= uint32_t(uint8_t(L[li][2 * e + 1])) << (8 * e);
+            }
+            *reinterpret_cast<uint32_t*>(rec + li * kGroup + pe) = ev;
+            *reinterpret_cast<uint32_t*>(rec + li * kGroup + po) = od;
+        }
+    } else {
+#pragma unroll
+        for (int li = 0; li < 3; li++) {
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                lo |= uint32_t(uint8_t(L[li][e])) << (8 * e);
+                hi |= uint32_t(uint8_t(L[li][e + 4])) << (8 * e);
+            }
+            *reinterpret_cast<uint2*>(rec + li * kGroup + j * 8) = make_uint2(lo, hi);
+        }
+    }
+    // 2^-k (NaN when the group holds a non-finite value, so it propagates);
+    // a group of values below ~2^-149 * 2^22 contributes 0.
+    const float fx = fin ? ldexpf(1.0f, -k) : __builtin_nanf("");
+    if (j == 0) meta[g * kMeta + m] = make_int4(__float_as_int(fx), s0, s1, s2);
 }
 
-// ------------------------------------------------------------------ gemv
+// ------------------------------------------------------------------ shared pieces
 struct GemvParams {
     const uint8_t* q;
     const uint16_t* scales;
     const uint8_t* zeros;
-    int64_t N, K, G, Kp;
-    const _Float16* xh;
-    const _Float16* xl;
-    const float* xinv;
+    int64_t N, K, G;
+    const int8_t* xq;
+    const int4* meta;
     const uint16_t* bias;
     float* y;
     float* part;
     int* cnt;
-    int M, S, gs, nrb, nrb_pad;
+    int M, S, gs, nrb;
 };
 
 // 16 bytes of a row at byte offset `off`, zero past `row_bytes` (unaligned
@@ -123,38 +196,259 @@ __device__ __forceinline__ uint4 load16_slow(const uint8_t* row, int64_t off, in
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-template <int KIND, int MT, int R, bool FAST>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
-    const int lane = threadIdx.x & 63, ln = lane & 15, kg = lane >> 4;
-    const int wid = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    const int ks = wid / p.nrb_pad, rb = wid % p.nrb_pad;
-    if (rb >= p.nrb) return;
-    const int64_t row0 = int64_t(rb) * 16 * R;
-    const int64_t row_bytes = KIND == 1 ? p.K / 2 : p.K;
+// The two B operands (k-steps of 64 columns) of one lane for one group.
+//   int8: the two 16-byte loads as they are.
+//   int4: the one 16-byte load split into low nibbles (even columns) and
+//   high nibbles (odd columns), one byte per code.
+template <int KIND>
+__device__ __forceinline__ void weight_operands(const uint4* w, int4v_t& b0, int4v_t& b1) {
+    if (KIND == 1) {
+        const uint4 v = w[0];
+        b0 = int4v_t{int(v.x & 0x0F0F0F0Fu), int(v.y & 0x0F0F0F0Fu), int(v.z & 0x0F0F0F0Fu), int(v.w & 0x0F0F0F0Fu)};
+        b1 = int4v_t{int((v.x >> 4) & 0x0F0F0F0Fu), int((v.y >> 4) & 0x0F0F0F0Fu),
+                     int((v.z >> 4) & 0x0F0F0F0Fu), int((v.w >> 4) & 0x0F0F0F0Fu)};
+    } else {
+        b0 = u4_to_i4v(w[0]);
+        b1 = u4_to_i4v(w[1]);
+    }
+}
 
-    const uint8_t* qrow[R];
-    const uint16_t* srow[R];
-    const uint8_t* zrow[R];
+// fp32 value of one group's exact integer limb sums (t_L = S_L - z * sum X_L,
+// computed with 24-bit multiplies: |z| <= 15, |sum X_L| < 2^15), times the
+// weight scale and the activation factor 2^-k, added to acc.
+__device__ __forceinline__ float combine(float acc, int d0, int d1, int d2, int z, int4 md, float s) {
+    const int t0 = d0 - __mul24(z, md.y), t1 = d1 - __mul24(z, md.z), t2 = d2 - __mul24(z, md.w);
+    const float v = __builtin_fmaf(float(t0), 65536.0f, __builtin_fmaf(float(t1), 256.0f, float(t2)));
+    return __builtin_fmaf(v, s * __int_as_float(md.x), acc);
+}
+
+// ------------------------------------------------------------------ 1 row
+// Weight words + scales + zero points of one batch of GB groups of a lane.
+template <int KIND, int GB>
+struct WBatch {
+    static constexpr int WPG = KIND == 1 ? 1 : 2;
+    uint4 w[GB][WPG];
+    uint2 s[GB / 4];     // 4 bf16 scales per entry
+    uint32_t z[GB / 4];  // 4 zero points per entry (int4)
+};
+
+// Loads batch [g0, g0 + GB) of one lane (columns of the lane's quarter of
+// each group); groups at or past `gend` re-load group gend-1 (the compute
+// skips them), so every load is unconditional and stays in bounds.
+template <int KIND, int GB, bool VEC>
+__device__ __forceinline__ void load_batch(WBatch<KIND, GB>& b, const uint8_t* qrow, const uint16_t* srow,
+                                           const uint8_t* zrow, int g0, int gend, int kg,
+                                           int row_bytes) {
+    constexpr int WPG = WBatch<KIND, GB>::WPG;
+#pragma unroll
+    for (int gl = 0; gl < GB; gl++) {
+        const int g = g0 + gl < gend ? g0 + gl : gend - 1;
+#pragma unroll
+        for (int h = 0; h < WPG; h++) {
+            const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
+            b.w[gl][h] = VEC ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes);
+        }
+    }
+#pragma unroll
+    for (int q4 = 0; q4 < GB / 4; q4++) {
+        if (VEC) {
+            // gend is a multiple of 4 here (G % 4 == 0 and gs % 4 == 0)
+            const int g = g0 + 4 * q4 < gend ? g0 + 4 * q4 : gend - 4;
+            b.s[q4] = *reinterpret_cast<const uint2*>(srow + g);
+            b.z[q4] = KIND == 1 ? *reinterpret_cast<const uint32_t*>(zrow + g) : 0u;
+        } else {
+            uint32_t s4[4], z4 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int g = g0 + 4 * q4 + e < gend ? g0 + 4 * q4 + e : gend - 1;
+                s4[e] = srow[g];
+                if (KIND == 1) z4 |= uint32_t(zrow[g]) << (8 * e);
+            }
+            b.s[q4] = make_uint2(s4[0] | (s4[1] << 16), s4[2] | (s4[3] << 16));
+            b.z[q4] = z4;
+        }
+    }
+}
+
+// One activation row (the decode step).  Workgroup = TW x KS waves: TW tiles
+// of 16 output rows, each tile's K split into KS slices (wave = one tile,
+// one slice of gs <= NB*GB groups).  Every weight word, scale and zero point
+// of a wave's slice is requested at kernel start (NB batches of GB groups,
+// all loads unconditional - clamped into the slice - so nothing waits before
+// the last one is issued).  The activation row (limbs + meta records) is
+// staged in LDS once per workgroup, shared by the TW tiles; its loads are
+// issued before the weight loads, so waiting for them leaves the weights in
+// flight while the MFMAs start on the first groups.  With KS > 1 the slice partials of a tile are added through LDS in
+// slice order (deterministic): no cross-workgroup traffic, no device-scope
+// fence.  The A operand carries the activation's three byte limbs as rows
+// 0..2 of the 16-row MFMA tile (lanes l%16 = 0, 1, 2; the other lanes read a
+// zero block, no branches), so two MFMAs per 128 columns yield all three
+// exact limb sums, in D rows 0..2 of lanes 0..15.  VEC: K % 128 == 0, G % 4 == 0
+// and gs % 4 == 0 -> 16-byte weight loads and one load per 4 groups for
+// scales (8 B) and zero points (4 B).
+template <int KIND, int TW, int KS, int GB, int NB, bool VEC>
+__global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p) {
+    constexpr int W = TW * KS;
+    extern __shared__ __attribute__((aligned(16))) int8_t xs1[];  // limbs [G][384] (padded), meta [G]
+    __shared__ __attribute__((aligned(16))) int8_t xzero[16];
+    __shared__ float red[W][16];
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
+    const int tw = wave / KS, ksl = wave % KS;
+    const int G = int(p.G);
+    const int64_t tile = int64_t(blockIdx.x) * TW + tw;
+    const int64_t row = tile * 16 + ln;
+    const int64_t rc = row < p.N ? row : p.N - 1;
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const uint8_t* qrow = p.q + rc * row_bytes;
+    const uint16_t* srow = p.scales + rc * G;
+    const uint8_t* zrow = KIND == 1 ? p.zeros + rc * G : nullptr;
+    const int gbeg = ksl * p.gs < G ? ksl * p.gs : G;
+    const int gend = gbeg + p.gs < G ? gbeg + p.gs : G;
+    const bool active = gend > gbeg;
+    // Clamp bound for idle waves (their loads re-read groups 0..3, in bounds;
+    // the 4-group scale loads need a bound of at least 4).
+    const int g0c = active ? gbeg : 0;
+    const int gcl = active ? gend : (VEC ? 4 : 1);
+    const int nch = G * (kLimbRec / 16);      // 16-byte limb chunks of the row
+    int4* ms1 = reinterpret_cast<int4*>(xs1 + nch * 16);
+
+    // 1. Activation limbs and meta records: loads issued first (so that a
+    //    wait for them leaves the weight words in flight), at most 8 chunks
+    //    per thread (host guarantees nch <= 8 * 64 * W); indices past the end
+    //    re-read / re-write the last chunk (identical bytes, no branches).
+    uint4 xc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int c = tid + i * 64 * W;
+        xc[i] = reinterpret_cast<const uint4*>(p.xq)[c < nch ? c : nch - 1];
+    }
+    const int4 mreg = p.meta[(tid < G ? tid : G - 1) * kMeta];  // G <= 64*W (host)
+    const int mslot = tid < G ? tid : G;                            // slot G: scratch
+    if (tid < 4) reinterpret_cast<uint32_t*>(xzero)[tid] = 0u;
+
+    // 2. All weight batches of the slice.
+    WBatch<KIND, GB> wb[NB];
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++) load_batch<KIND, GB, VEC>(wb[bi], qrow, srow, zrow, g0c + bi * GB, gcl, kg, row_bytes);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int c = tid + i * 64 * W;
+        reinterpret_cast<uint4*>(xs1)[c < nch ? c : nch - 1] = xc[i];
+    }
+    ms1[mslot] = mreg;
+    __syncthreads();
+
+    // 3. Per batch: all activation operands, then all MFMAs, then the fp32
+    //    combination (independent chains, so LDS / MFMA latencies overlap).
+    float acc = 0.0f;
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++) {
+        // A operand rows 0, 1, 2 = the activation's three limbs (lanes with
+        // l%16 = L), rows 3..15 zero: one MFMA per 64 columns gives all three
+        // exact limb sums, in D rows 0..2 of lanes 0..15.
+        int4v_t a[GB][2];
+#pragma unroll
+        for (int gl = 0; gl < GB; gl++) {
+            const int g = gbeg + bi * GB + gl < gend ? gbeg + bi * GB + gl : gbeg;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const int8_t* pa = ln < 3 ? xs1 + g * kLimbRec + ln * kGroup + st * 64 + kg * 16 : xzero;
+                a[gl][st] = *reinterpret_cast<const int4v_t*>(pa);
+            }
+        }
+        int4v_t D[GB];
+#pragma unroll
+        for (int gl = 0; gl < GB; gl++) {
+            int4v_t b0, b1;
+            weight_operands<KIND>(wb[bi].w[gl], b0, b1);
+            D[gl] = mfma_i8(a[gl][0], b0, int4v_t{0, 0, 0, 0});
+            D[gl] = mfma_i8(a[gl][1], b1, D[gl]);
+        }
+#pragma unroll
+        for (int gl = 0; gl < GB; gl++) {
+            const int g = gbeg + bi * GB + gl;
+            if (g >= gend) break;
+            const uint32_t sw = (gl & 2) ? wb[bi].s[gl / 4].y : wb[bi].s[gl / 4].x;
+            const float s = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+            const int z = KIND == 1 ? int((wb[bi].z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
+            acc = combine(acc, D[gl][0], D[gl][1], D[gl][2], z, ms1[g], s);
+        }
+    }
+    if (KS == 1) {
+        if (lane < 16 && row < p.N) p.y[row] = acc + (p.bias ? bf16_to_f32(p.bias[row]) : 0.0f);
+        return;
+    }
+    if (lane < 16) red[wave][lane] = acc;
+    __syncthreads();
+    if (tid < 16 * TW) {
+        const int t = tid / 16, r = tid % 16;
+        const int64_t n = (int64_t(blockIdx.x) * TW + t) * 16 + r;
+        if (n < p.N) {
+            float sum = red[t * KS][r];
+#pragma unroll
+            for (int k = 1; k < KS; k++) sum += red[t * KS + k][r];
+            p.y[n] = sum + (p.bias ? bf16_to_f32(p.bias[n]) : 0.0f);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ 2..32 rows
+constexpr int kLdsBudget = 72 * 1024;  // activation slice per workgroup
+
+// Workgroup = 4 waves; wave w owns R tiles of 16 output rows
+// (rows (rb*4 + w)*16R ...); the workgroup owns the K slice of groups
+// [ks*gs, ks*gs + gs), gs <= GMAX.  Every weight word of the slice is
+// requested before anything waits, the activation limbs of the slice are
+// staged once per workgroup in LDS, then the MFMAs run group by group.
+template <int KIND, int MT, int R, int GMAX, bool FAST>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
+    extern __shared__ __attribute__((aligned(16))) int8_t xsb[];
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
+    const int ks = blockIdx.x / p.nrb, rb = blockIdx.x % p.nrb;
+    const int64_t g0 = int64_t(ks) * p.gs;
+    const int ng = int(p.G - g0 < p.gs ? p.G - g0 : p.gs);
+    const int64_t row0 = (int64_t(rb) * 4 + wave) * 16 * R;
+    const int64_t row_bytes = KIND == 1 ? p.K / 2 : p.K;
+    constexpr int WPG = KIND == 1 ? 1 : 2;
+
+    // 1. Weight words, scales and zero points of the whole slice, all in flight.
+    uint4 wv[GMAX][R][WPG];
+    float sc[GMAX][R];
+    int zz[GMAX][R];
     bool rv[R];
 #pragma unroll
     for (int t = 0; t < R; t++) {
         const int64_t r = row0 + 16 * t + ln;
         rv[t] = r < p.N;
         const int64_t rc = rv[t] ? r : p.N - 1;
-        qrow[t] = p.q + rc * row_bytes;
-        srow[t] = p.scales + rc * p.G;
-        zrow[t] = KIND == 1 ? p.zeros + rc * p.G : nullptr;
-    }
-    bool mv[MT];
-    const _Float16* xhr[MT];
-    const _Float16* xlr[MT];
+        const uint8_t* qrow = p.q + rc * row_bytes;
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int m = mt * 16 + ln;
-        mv[mt] = m < p.M;
-        xhr[mt] = p.xh + int64_t(mv[mt] ? m : 0) * p.Kp;
-        xlr[mt] = p.xl + int64_t(mv[mt] ? m : 0) * p.Kp;
+        for (int gl = 0; gl < GMAX; gl++) {
+            const int64_t g = g0 + (gl < ng ? gl : ng - 1);  // unconditional, clamped
+#pragma unroll
+            for (int h = 0; h < WPG; h++) {
+                const int64_t off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
+                wv[gl][t][h] = FAST ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes);
+            }
+            sc[gl][t] = bf16_to_f32(p.scales[rc * p.G + g]);
+            zz[gl][t] = KIND == 1 ? int(p.zeros[rc * p.G + g]) : 0;
+        }
     }
+
+    // 2. Activation limbs of the slice -> LDS as records [gl][m][3*128],
+    //    then the meta records [gl][32].
+    int4* msb = reinterpret_cast<int4*>(xsb + ng * p.M * kLimbRec);
+    {
+        const int nchunks = ng * p.M * (kLimbRec / 16);
+        for (int c = tid; c < nchunks; c += 256) {
+            const int rec = c / (kLimbRec / 16), piece = c % (kLimbRec / 16);
+            const int gl = rec / p.M, m = rec % p.M;
+            const int8_t* src = p.xq + (int64_t(m) * p.G + g0 + gl) * kLimbRec + piece * 16;
+            *reinterpret_cast<uint4*>(xsb + rec * kLimbRec + piece * 16) = *reinterpret_cast<const uint4*>(src);
+        }
+        for (int c = tid; c < ng * kMeta; c += 256) msb[c] = p.meta[(g0 + c / kMeta) * kMeta + c % kMeta];
+    }
+    __syncthreads();
 
     float4_t acc[R][MT];
 #pragma unroll
@@ -162,75 +456,48 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[t][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t g0 = int64_t(ks) * p.gs;
-    const int64_t g1 = g0 + p.gs < p.G ? g0 + p.gs : p.G;
-    for (int64_t g = g0; g < g1; g++) {
-        // Activation fragments: 4 chunks of 8 columns per lane for this group.
-        half8_t xa[MT][4], xb[MT][4];
+#pragma unroll
+    for (int gl = 0; gl < GMAX; gl++) {
+        if (gl >= ng) break;
+        int4v_t a[MT][3][2];
+        int4 md[MT][4];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
+            const int m = mt * 16 + ln;
+            const int mr = m < p.M ? m : 0;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int64_t off = g * kGroup + (KIND == 1 ? kg * 32 + 8 * c : (c >> 1) * 64 + kg * 16 + 8 * (c & 1));
-                if (mv[mt]) {
-                    xa[mt][c] = *reinterpret_cast<const half8_t*>(xhr[mt] + off);
-                    xb[mt][c] = *reinterpret_cast<const half8_t*>(xlr[mt] + off);
-                } else {
-                    xa[mt][c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-                    xb[mt][c] = xa[mt][c];
+            for (int L = 0; L < 3; L++)
+#pragma unroll
+                for (int st = 0; st < 2; st++) {
+                    const int4v_t v = *reinterpret_cast<const int4v_t*>(xsb + (gl * p.M + mr) * kLimbRec + L * kGroup + st * 64 + kg * 16);
+                    a[mt][L][st] = m < p.M ? v : int4v_t{0, 0, 0, 0};
                 }
-            }
-        }
-        float4_t inv[MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-            inv[mt] = *reinterpret_cast<const float4_t*>(p.xinv + g * kXinvStride + mt * 16 + 4 * kg);
-
+            for (int r = 0; r < 4; r++) md[mt][r] = msb[gl * kMeta + mt * 16 + 4 * kg + r];
+        }
 #pragma unroll
         for (int t = 0; t < R; t++) {
-            const float s = bf16_to_f32(srow[t][g]);
-            half8_t wf[4];
-            if (KIND == 1) {
-                const uint4 wv = FAST ? *reinterpret_cast<const uint4*>(qrow[t] + g * 64 + kg * 16)
-                                      : load16_slow(qrow[t], g * 64 + kg * 16, row_bytes);
-                const uint32_t z = zrow[t][g];
-                const uint32_t zb = zpair_1024(z), zc = zpair_64(z);
-                const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    uint32_t o0, o1, o2, o3;
-                    dq_int4_x8(d[c], zb, zc, o0, o1, o2, o3);
-                    wf[c] = pack_h8(o0, o1, o2, o3);
-                }
-            } else {
-                const uint4 wa = FAST ? *reinterpret_cast<const uint4*>(qrow[t] + g * 128 + kg * 16)
-                                      : load16_slow(qrow[t], g * 128 + kg * 16, row_bytes);
-                const uint4 wb = FAST ? *reinterpret_cast<const uint4*>(qrow[t] + g * 128 + 64 + kg * 16)
-                                      : load16_slow(qrow[t], g * 128 + 64 + kg * 16, row_bytes);
-                const uint32_t d[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    uint32_t o0, o1, o2, o3;
-                    dq_int8_x4(d[2 * c], o0, o1);
-                    dq_int8_x4(d[2 * c + 1], o2, o3);
-                    wf[c] = pack_h8(o0, o1, o2, o3);
-                }
-            }
+            int4v_t b0, b1;
+            weight_operands<KIND>(wv[gl][t], b0, b1);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                float4_t D = {0.f, 0.f, 0.f, 0.f};
+                int4v_t D[3];
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    D = mfma16(xa[mt][c], wf[c], D);
-                    D = mfma16(xb[mt][c], wf[c], D);
+                for (int L = 0; L < 3; L++) {
+                    D[L] = mfma_i8(a[mt][L][0], b0, int4v_t{0, 0, 0, 0});
+                    D[L] = mfma_i8(a[mt][L][1], b1, D[L]);
                 }
+                const int z = zz[gl][t];
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[t][mt][r] = __builtin_fmaf(s * inv[mt][r], D[r], acc[t][mt][r]);
+                for (int r = 0; r < 4; r++) {
+                    const int m = mt * 16 + 4 * kg + r;
+                    if (m < p.M) acc[t][mt][r] = combine(acc[t][mt][r], D[0][r], D[1][r], D[2][r], z, md[mt][r], sc[gl][t]);
+                }
             }
         }
     }
 
-    // Epilogue.  Lane holds D rows m = mt*16 + 4*kg + r for output n = row0+16t+ln.
+    // 3. Epilogue.  Lane holds rows m = mt*16 + 4*kg + r of output n = row0 + 16t + ln.
     if (p.S == 1) {
 #pragma unroll
         for (int t = 0; t < R; t++) {
@@ -247,6 +514,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
         }
         return;
     }
+    // Split K: publish this slice's partial sums; the last of the S slices to
+    // arrive for this wave's rows adds them in slice order (deterministic).
 #pragma unroll
     for (int t = 0; t < R; t++) {
         if (!rv[t]) continue;
@@ -260,8 +529,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
             }
     }
     __threadfence();
+    const int ci = rb * 4 + wave;
     int prev = 0;
-    if (lane == 0) prev = atomicAdd(p.cnt + rb, 1);
+    if (lane == 0) prev = atomicAdd(p.cnt + ci, 1);
     prev = __shfl(prev, 0);
     if (prev != p.S - 1) return;
     __threadfence();
@@ -281,29 +551,62 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                 p.y[int64_t(m) * p.N + n] = sum + b;
             }
     }
-    if (lane == 0) p.cnt[rb] = 0;
+    if (lane == 0) p.cnt[ci] = 0;
 }
 
-template <int KIND, int MT, int R>
-void launch_gemv_t(const GemvParams& p, bool fast, unsigned grid, hipStream_t stream) {
-    if (fast) gemv_kernel<KIND, MT, R, true><<<grid, 256, 0, stream>>>(p);
-    else gemv_kernel<KIND, MT, R, false><<<grid, 256, 0, stream>>>(p);
+template <int KIND, int TW, int KS, int GB>
+void launch_gemv1_s(const GemvParams& p, int nb, bool vec, unsigned grid, size_t lds, hipStream_t stream) {
+#define IQ_G1(NB)                                                                                  \
+    do {                                                                                           \
+        if (vec) gemv1_kernel<KIND, TW, KS, GB, NB, true><<<grid, 64 * TW * KS, lds, stream>>>(p); \
+        else gemv1_kernel<KIND, TW, KS, GB, NB, false><<<grid, 64 * TW * KS, lds, stream>>>(p);    \
+    } while (0)
+    switch (nb) {
+        case 1: IQ_G1(1); break;
+        case 2: IQ_G1(2); break;
+        case 3: IQ_G1(3); break;
+        default: IQ_G1(4); break;
+    }
+#undef IQ_G1
+}
+
+// Instantiated workgroup shapes: one tile, KS = 4, 8 or 16 slices.
+template <int KIND, int GB>
+void launch_gemv1_t(const GemvParams& p, int KS, bool vec, unsigned grid, hipStream_t stream) {
+    const size_t lds = size_t(p.G) * kLimbRec + size_t(p.G + 1) * 16;
+    const int nb = (p.gs + GB - 1) / GB;
+    if (KS == 1) launch_gemv1_s<KIND, 1, 1, GB>(p, nb, vec, grid, lds, stream);
+    else if (KS == 2) launch_gemv1_s<KIND, 1, 2, GB>(p, nb, vec, grid, lds, stream);
+    else if (KS == 4) launch_gemv1_s<KIND, 1, 4, GB>(p, nb, vec, grid, lds, stream);
+    else if (KS == 8) launch_gemv1_s<KIND, 1, 8, GB>(p, nb, vec, grid, lds, stream);
+    else launch_gemv1_s<KIND, 1, 16, GB>(p, nb, vec, grid, lds, stream);
+}
+
+template <int KIND, int MT, int R, int GMAX>
+void launch_gemv_t(const GemvParams& p, bool fast, unsigned grid, size_t lds, hipStream_t stream) {
+    if (fast) gemv_kernel<KIND, MT, R, GMAX, true><<<grid, 256, lds, stream>>>(p);
+    else gemv_kernel<KIND, MT, R, GMAX, false><<<grid, 256, lds, stream>>>(p);
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
 }
 
 }  // namespace
 
 hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
-    const int64_t G = (K + kGroup - 1) / kGroup, Kp = G * kGroup;
+    const int64_t G = (K + kGroup - 1) / kGroup;
     const int64_t quads = (G + 3) / 4;
     const int64_t waves = int64_t(M) * quads;
     const unsigned grid = unsigned((waves + 3) / 4);
     const bool vecx = (K % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
     if (kind == 1) {
-        if (vecx) xprep_kernel<true, true><<<grid, 256, 0, stream>>>(x, M, K, G, Kp, quads, ws->xh, ws->xl, ws->xinv);
-        else xprep_kernel<true, false><<<grid, 256, 0, stream>>>(x, M, K, G, Kp, quads, ws->xh, ws->xl, ws->xinv);
+        if (vecx) xprep_kernel<true, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, ws->xq, ws->xmeta);
+        else xprep_kernel<true, false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, ws->xq, ws->xmeta);
     } else {
-        if (vecx) xprep_kernel<false, true><<<grid, 256, 0, stream>>>(x, M, K, G, Kp, quads, ws->xh, ws->xl, ws->xinv);
-        else xprep_kernel<false, false><<<grid, 256, 0, stream>>>(x, M, K, G, Kp, quads, ws->xh, ws->xl, ws->xinv);
+        if (vecx) xprep_kernel<false, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, ws->xq, ws->xmeta);
+        else xprep_kernel<false, false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, ws->xq, ws->xmeta);
     }
     ws->prep_M = M;
     ws->prep_K = K;
@@ -313,32 +616,72 @@ hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* w
 
 hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
                                hipStream_t stream) {
-    const int64_t N = W.rows, K = W.cols, G = W.groups, Kp = G * kGroup;
-    constexpr int R = 2;
-    GemvParams p;
+    const int64_t N = W.rows, K = W.cols, G = W.groups;
+    const int kind = W.kind;
+    GemvParams p{};
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros;
-    p.N = N; p.K = K; p.G = G; p.Kp = Kp;
-    p.xh = ws->xh; p.xl = ws->xl; p.xinv = ws->xinv;
+    p.N = N; p.K = K; p.G = G;
+    p.xq = ws->xq; p.meta = ws->xmeta;
     p.bias = bias; p.y = y; p.part = ws->partials; p.cnt = ws->counters;
     p.M = M;
-    p.nrb = int((N + 16 * R - 1) / (16 * R));
-    p.nrb_pad = (p.nrb + kWaves - 1) / kWaves * kWaves;
-    const int target = device_cu_count() * 8;
-    int S = (target + p.nrb_pad - 1) / p.nrb_pad;
-    if (S > G) S = int(G);
-    if (S < 1) S = 1;
-    while (S > 1 && (int64_t(S) * M * N > kPartialFloats || p.nrb > kMaxCounters)) S--;
-    p.gs = int((G + S - 1) / S);
-    p.S = int((G + p.gs - 1) / p.gs);
-    const unsigned grid = unsigned(int64_t(p.S) * p.nrb_pad / kWaves);
-    const bool fast = (K % kGroup == 0);
-    if (W.kind == 1) {
-        if (M <= 16) launch_gemv_t<1, 1, R>(p, fast, grid, stream);
-        else launch_gemv_t<1, 2, R>(p, fast, grid, stream);
-    } else {
-        if (M <= 16) launch_gemv_t<0, 1, R>(p, fast, grid, stream);
-        else launch_gemv_t<0, 2, R>(p, fast, grid, stream);
+    const int gb1 = kind == 1 ? 8 : 4;  // groups per batch of the 1-row kernel (8 KB per wave)
+    if (M == 1 && G * (kLimbRec + 16) <= 96 * 1024) {
+        // Workgroup = one 16-row tile x KS K-slices.  KS: the smallest of
+        // 4, 8, 16 whose slices fit 4 batches and whose threads can stage the
+        // activation row (8 chunks of 16 B each).  Measured on MI355X: 4
+        // slices beat more, smaller workgroups whenever they fit.
+        const int64_t tiles = (N + 15) / 16;
+        static const int forced = env_int("IQ_GEMV1_KS", 0);
+        int KS = 0;
+        for (int ks : {4, 8, 16}) {  // 1 and 2 are instantiated for experiments
+            int gs = int((G + ks - 1) / ks);
+            if (K % kGroup == 0 && G % 4 == 0) gs = (gs + 3) / 4 * 4;
+            if (gs <= 4 * gb1 && G * 24 <= 8 * 64 * ks && G <= 64 * ks) { KS = ks; break; }
+        }
+        if (forced && KS) KS = forced;
+        if (KS) {
+            p.gs = int((G + KS - 1) / KS);
+            const bool vec = (K % kGroup == 0) && (G % 4 == 0);
+            if (vec) p.gs = (p.gs + 3) / 4 * 4;  // 4-group aligned slices: vector scale loads
+            p.S = 1;
+            const unsigned grid = unsigned(tiles);
+            if (kind == 1) launch_gemv1_t<1, 8>(p, KS, vec, grid, stream);
+            else launch_gemv1_t<0, 4>(p, KS, vec, grid, stream);
+            return hipGetLastError();
+        }
     }
+    const int MT = M <= 16 ? 1 : 2;
+    const int R = 2;
+    const int gmax = kind == 1 ? 8 : 4;
+    static const int target = env_int("IQ_GEMV_TARGET", 8);
+    p.nrb = int((N + 64 * R - 1) / (64 * R));
+    // Slice size: at most gmax groups, within the LDS budget, and enough
+    // slices to put ~target waves per CU on the device.
+    const size_t per_group = size_t(M) * kLimbRec + size_t(kMeta) * 16;
+    int gs = gmax;
+    while (gs > 1 && size_t(gs) * per_group > size_t(kLdsBudget)) gs--;
+    const int64_t waves_per_slice = int64_t(p.nrb) * 4;
+    const int64_t want_waves = int64_t(device_cu_count()) * target;
+    const int64_t want_s = (want_waves + waves_per_slice - 1) / waves_per_slice;
+    int64_t gs_t = (G + want_s - 1) / want_s;
+    if (gs_t < 1) gs_t = 1;
+    if (gs_t < gs) gs = int(gs_t);
+    int S = int((G + gs - 1) / gs);
+    // Split-K scratch limits: partial sums and one counter per wave.
+    if (S > 1 && (int64_t(S) * M * N > kPartialFloats || int64_t(p.nrb) * 4 > kMaxCounters)) return hipErrorInvalidValue;
+    p.gs = gs;
+    p.S = S;
+    const unsigned grid = unsigned(int64_t(S) * p.nrb);
+    const size_t lds = size_t(gs) * per_group;
+    const bool fast = (K % kGroup == 0);
+#define IQ_GEMV_DISPATCH(KIND, GM)                                                         \
+    do {                                                                                   \
+        if (MT == 1) launch_gemv_t<KIND, 1, 2, GM>(p, fast, grid, lds, stream);            \
+        else launch_gemv_t<KIND, 2, 2, GM>(p, fast, grid, lds, stream);                    \
+    } while (0)
+    if (kind == 1) IQ_GEMV_DISPATCH(1, 8);
+    else IQ_GEMV_DISPATCH(0, 4);
+#undef IQ_GEMV_DISPATCH
     return hipGetLastError();
 }
 

@@ -19,17 +19,17 @@ struct QView {
     const uint8_t* zeros;
 };
 
-// Per-device scratch used by the GEMV: fp16 hi/lo activations, per-row
-// power-of-two prescale, split-K partial sums and split-K arrival counters.
+// Per-device scratch used by the GEMV: the activations as byte limbs with
+// their per-(group, row) exponent and limb sums, split-K partial sums and
+// split-K arrival counters.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
     int* counters = nullptr;   // kMaxCounters ints, zero between launches
-    float* xinv = nullptr;     // kMaxRowsGemv floats
-    _Float16* xh = nullptr;    // kMaxRowsGemv * kMaxKp
-    _Float16* xl = nullptr;
+    int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs
+    int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {k, sum X0, sum X1, sum X2}
     float* partials = nullptr; // kPartialFloats
-    // Shape of the activations last prepared into xh/xl/xinv (host-side record).
+    // Shape of the activations last prepared into xq/xmeta (host-side record).
     int prep_M = 0;
     int64_t prep_K = 0;
     int prep_kind = -1;
