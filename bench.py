@@ -104,23 +104,27 @@ class Step:
         self.y = {name: torch.empty(M, out, device="cuda") for name, out, _, _ in model.shapes}
         if model.head is not None:
             self.y["head"] = torch.empty(M, model.head.rows, device="cuda")
-        # op list: ("prep", slot, kind) | ("gemv", W, yname)
+        # op list: ("prep", slot, kind) | ("gemv", [W...], [yname...]); matrices
+        # that share an activation (q|k|v, gate|up) go in one call.
         self.ops_list = []
         for L in model.layers:
             last = None
             for name, out, inn, slot in model.shapes:
                 if slot != last:
                     self.ops_list.append(("prep", slot, model.kind))
+                    self.ops_list.append(("gemv", [], []))
                     last = slot
-                self.ops_list.append(("gemv", L[name], name))
+                self.ops_list[-1][1].append(L[name])
+                self.ops_list[-1][2].append(name)
         if model.head is not None:
             self.ops_list.append(("prep", "head", model.head.kind))
-            self.ops_list.append(("gemv", model.head, "head"))
+            self.ops_list.append(("gemv", [model.head], ["head"]))
         self.bytes = 0
         for op in self.ops_list:
             if op[0] == "gemv":
-                W = op[1]
-                self.bytes += W.nbytes() + 4 * M * W.cols + 4 * M * W.rows
+                for W in op[1]:
+                    self.bytes += W.nbytes() + 4 * M * W.rows
+                self.bytes += 4 * M * op[1][0].cols
 
     def run(self, timing=None):
         ops, M = self.ops, self.M
@@ -130,12 +134,15 @@ class Step:
                 x = self.x[op[1]]
                 ops.gemv_prep(x, M, x.shape[1], op[2])
             else:
-                W, yname = op[1], op[2]
+                Ws, ynames = op[1], op[2]
                 if timing is not None:
-                    timing.append((W, self.torch.cuda.Event(enable_timing=True),
+                    timing.append((Ws, self.torch.cuda.Event(enable_timing=True),
                                    self.torch.cuda.Event(enable_timing=True)))
                     timing[-1][1].record()
-                ops.gemv_prepped(W, None, M, W.cols, W.rows, self.y[yname])
+                if len(Ws) == 1:
+                    ops.gemv_prepped(Ws[0], None, M, Ws[0].cols, Ws[0].rows, self.y[ynames[0]])
+                else:
+                    ops.gemv_prepped_multi(Ws, None, M, Ws[0].cols, [self.y[n] for n in ynames])
                 if timing is not None:
                     timing[-1][2].record()
 
@@ -174,11 +181,11 @@ def kernel_roofline(torch, step, only_kind=None):
     step.run(timing)
     torch.cuda.synchronize()
     tot_b, tot_ms, n = 0, 0.0, 0
-    for W, a, b in timing:
-        if only_kind is not None and W.kind != only_kind:
+    for Ws, a, b in timing:
+        if only_kind is not None and Ws[0].kind != only_kind:
             continue
         ms = a.elapsed_time(b)
-        tot_b += W.nbytes() + 4 * step.M * W.cols + 4 * step.M * W.rows
+        tot_b += sum(W.nbytes() + 4 * step.M * W.rows for W in Ws) + 4 * step.M * Ws[0].cols
         tot_ms += ms
         n += 1
     return tot_b, tot_ms, n
@@ -298,7 +305,7 @@ def main():
             traffic = None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "gemv_kernel<int4, 1 row-tile, R=2> over the 196 int4 layer matrices",
+                "kernel": "gemv1_kernel (int4, 1 row): the 112 launches of the 28 layers (q|k|v, o, gate|up, down)",
                 "launches": rn, "avg_launch_us": round(rms * 1e3 / max(rn, 1), 3),
                 "algorithmic_bytes_per_launch": int(rb / max(rn, 1))}
     del g

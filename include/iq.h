@@ -80,6 +80,15 @@ int iq_gemv_prep(const float* x, int B, int64_t in, int kind, void* stream);
 int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
                     float* y, void* stream);
 
+/* iq_gemv_prepped for n <= 4 matrices of one kind and width at once
+ * (y_i = x * W_i^T + bias_i, out_i = Ws[i]->rows): q|k|v or gate|up of a
+ * layer in one launch.  The reference runs them as separate launches
+ * (kernels/batch_gpu.cu:192-194,210-211) and fuses only bf16 weights
+ * (kernels/model_gpu.cu:31-38).  biases may be NULL (no bias anywhere) or
+ * hold NULL entries. */
+int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
+                          int64_t in, float* const* ys, void* stream);
+
 /* Same contract for any T >= 1 (fp32 activations).  Replaces
  * launch_gemm_tiled_q (kernels/ops/ops.cuh:175-176, kernels/ops/quant.cu:347-351).
  * Runs the MFMA prefill GEMM with the activations split into bf16 hi + lo. */

@@ -31,19 +31,35 @@ def hipcc():
     return p
 
 
+def _run(cmd):
+    return subprocess.run(cmd, capture_output=True, text=True)
+
+
 def build(verbose=False):
+    """Compiles every source to an object (in parallel), then links libiq.so."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    cmds = [[hipcc()] + compile_flags + ["-c", src, "-o", obj] for src, obj in zip(srcs, objs)]
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 4)) as ex:
+        results = list(ex.map(_run, cmds))
+    msgs = []
+    for r in results:
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError("hipcc failed building libiq.so")
+        # hipcc's host pass warns that it does not know the packed-fp32 feature.
+        msgs += [l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l]
     tmp = LIB + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + ["-o", tmp] + srcs
-    r = subprocess.run(cmd, capture_output=True, text=True)
+    r = _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed building libiq.so")
-    if verbose:
-        # hipcc's host pass warns that it does not know the packed-fp32 feature.
-        msgs = [l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l]
-        if msgs:
-            sys.stderr.write("\n".join(msgs) + "\n")
+        raise RuntimeError("hipcc failed linking libiq.so")
+    if verbose and msgs:
+        sys.stderr.write("\n".join(msgs) + "\n")
     os.replace(tmp, LIB)
     return LIB
 

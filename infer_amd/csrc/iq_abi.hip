@@ -161,6 +161,29 @@ int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, i
     return from_hip(iq::launch_gemv_prepped(to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
 }
 
+int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
+                          int64_t in, float* const* ys, void* stream) {
+    if (!Ws || !ys || n < 1 || n > 4) return n < 1 || n > 4 ? IQ_ESHAPE : IQ_ENULL;
+    iq::QView v[4];
+    const uint16_t* b[4];
+    float* y[4];
+    for (int i = 0; i < n; i++) {
+        if (!Ws[i]) return IQ_ENULL;
+        const int rc = check_view(Ws[i], in, Ws[i]->rows);
+        if (rc) return rc;
+        if (Ws[i]->kind != Ws[0]->kind) return IQ_EKIND;
+        if (!ys[i]) return IQ_ENULL;
+        v[i] = to_qview(Ws[i]);
+        b[i] = biases ? biases[i] : nullptr;
+        y[i] = ys[i];
+    }
+    iq::Workspace* ws = nullptr;
+    hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    if (B != ws->prep_M || in != ws->prep_K || Ws[0]->kind != ws->prep_kind) return IQ_ESHAPE;
+    return from_hip(iq::launch_gemv_prepped_multi(v, b, y, n, B, ws, static_cast<hipStream_t>(stream)));
+}
+
 int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,
             int64_t out, float* y, void* stream) {
     int rc = check_view(W, in, out);

@@ -71,7 +71,36 @@ __host__ __device__ constexpr int limb_pos(int c, bool perm) {
 }
 
 // ------------------------------------------------------------------ xprep
-// One wave per (row, 4 groups); 16 lanes per group, 8 columns per lane.
+// Rotation of a value inside its 16-lane DPP row (row_ror:N).
+template <int N>
+__device__ __forceinline__ int row_ror(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x120 + N, 0xF, 0xF, false);
+}
+// All-reduce over the 16 lanes of a DPP row (4 rotations, no LDS traffic).
+__device__ __forceinline__ int row16_sum(int v) {
+    v += row_ror<8>(v);
+    v += row_ror<4>(v);
+    v += row_ror<2>(v);
+    v += row_ror<1>(v);
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(row_ror<8>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(row_ror<4>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(row_ror<2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(row_ror<1>(__float_as_int(v))));
+    return v;
+}
+__device__ __forceinline__ int row16_and(int v) {
+    v &= row_ror<8>(v);
+    v &= row_ror<4>(v);
+    v &= row_ror<2>(v);
+    v &= row_ror<1>(v);
+    return v;
+}
+
+// One wave per (row, 4 groups); 16 lanes (one DPP row) per group, 8 columns
+// per lane.
 template <bool PERM, bool VECX>
 __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int M, int64_t K,
                                                     int64_t G, int64_t quads,
@@ -104,20 +133,13 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
         fin &= int(a <= 3.402823466e38f);
         amax = fmaxf(amax, a);
     }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 16));
-        fin &= __shfl_xor(fin, off, 16);
-    }
-    int k = 0;
-    if (fin && amax > 0.0f) {
-        int E;
-        (void)frexpf(amax, &E);  // amax = f * 2^E, f in [0.5, 1)
-        k = 22 - E;              // amax * 2^k in [2^21, 2^22)
-    }
+    amax = row16_max(amax);
+    fin = row16_and(fin);
+    // amax = f * 2^E, f in [0.5, 1): k = 22 - E puts amax * 2^k in [2^21, 2^22)
+    const int k = (fin && amax > 0.0f) ? 22 - __builtin_amdgcn_frexp_expf(amax) : 0;
     int X[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) X[i] = fin ? int(__builtin_rintf(ldexpf(v[i], k))) : 0;
+    for (int i = 0; i < 8; i++) X[i] = fin ? int(__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], k))) : 0;
     // balanced byte limbs: X = 2^16 x0 + 2^8 x1 + x2, each in [-128, 127]
     int l0[8], l1[8], l2[8];
     int s0 = 0, s1 = 0, s2 = 0;
@@ -130,12 +152,9 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
         l0[i] = a0; l1[i] = a1; l2[i] = a2;
         s0 += a0; s1 += a1; s2 += a2;
     }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) {
-        s0 += __shfl_xor(s0, off, 16);
-        s1 += __shfl_xor(s1, off, 16);
-        s2 += __shfl_xor(s2, off, 16);
-    }
+    s0 = row16_sum(s0);
+    s1 = row16_sum(s1);
+    s2 = row16_sum(s2);
     if (!gvalid) return;
     int8_t* rec = xq + (int64_t(m) * G + g) * kLimbRec;
     const int* L[3] = {l0, l1, l2};
@@ -167,12 +186,28 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
     }
     // 2^-k (NaN when the group holds a non-finite value, so it propagates);
     // a group of values below ~2^-149 * 2^22 contributes 0.
-    const float fx = fin ? ldexpf(1.0f, -k) : __builtin_nanf("");
+    const float fx = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
     if (j == 0) meta[g * kMeta + m] = make_int4(__float_as_int(fx), s0, s1, s2);
 }
 
 // ------------------------------------------------------------------ shared pieces
+constexpr int kMaxMulti = 4;  // matrices sharing one activation in one 1-row launch
+
+// One matrix of a multi-matrix 1-row launch: its 16-row tiles are the
+// workgroups [tile0, tile0 + ceil(N/16)).
+struct MatRef {
+    const uint8_t* q;
+    const uint16_t* scales;
+    const uint8_t* zeros;
+    const uint16_t* bias;
+    float* y;
+    int64_t N;
+    int tile0;
+};
+
 struct GemvParams {
+    MatRef mat[kMaxMulti];
+    int nmat;
     const uint8_t* q;
     const uint16_t* scales;
     const uint8_t* zeros;
@@ -235,7 +270,10 @@ struct WBatch {
 // Loads batch [g0, g0 + GB) of one lane (columns of the lane's quarter of
 // each group); groups at or past `gend` re-load group gend-1 (the compute
 // skips them), so every load is unconditional and stays in bounds.
-template <int KIND, int GB, bool VEC>
+// MODE 0: unaligned rows (byte loads); 1: 16-byte weight loads, one scale /
+// zero load per group; 2: also one 8-byte scale and one 4-byte zero-point
+// load per 4 groups (G % 4 == 0, slices of whole 4-group blocks).
+template <int KIND, int GB, int MODE>
 __device__ __forceinline__ void load_batch(WBatch<KIND, GB>& b, const uint8_t* qrow, const uint16_t* srow,
                                            const uint8_t* zrow, int g0, int gend, int kg,
                                            int row_bytes) {
@@ -246,12 +284,12 @@ __device__ __forceinline__ void load_batch(WBatch<KIND, GB>& b, const uint8_t* q
 #pragma unroll
         for (int h = 0; h < WPG; h++) {
             const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
-            b.w[gl][h] = VEC ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes);
+            b.w[gl][h] = MODE >= 1 ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes);
         }
     }
 #pragma unroll
     for (int q4 = 0; q4 < GB / 4; q4++) {
-        if (VEC) {
+        if (MODE == 2) {
             // gend is a multiple of 4 here (G % 4 == 0 and gs % 4 == 0)
             const int g = g0 + 4 * q4 < gend ? g0 + 4 * q4 : gend - 4;
             b.s[q4] = *reinterpret_cast<const uint2*>(srow + g);
@@ -283,32 +321,35 @@ __device__ __forceinline__ void load_batch(WBatch<KIND, GB>& b, const uint8_t* q
 // fence.  The A operand carries the activation's three byte limbs as rows
 // 0..2 of the 16-row MFMA tile (lanes l%16 = 0, 1, 2; the other lanes read a
 // zero block, no branches), so two MFMAs per 128 columns yield all three
-// exact limb sums, in D rows 0..2 of lanes 0..15.  VEC: K % 128 == 0, G % 4 == 0
-// and gs % 4 == 0 -> 16-byte weight loads and one load per 4 groups for
-// scales (8 B) and zero points (4 B).
-template <int KIND, int TW, int KS, int GB, int NB, bool VEC>
+// exact limb sums, in D rows 0..2 of lanes 0..15.  MODE: see load_batch.
+template <int KIND, int TW, int KS, int GB, int NB, int MODE>
 __global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p) {
     constexpr int W = TW * KS;
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];  // limbs [G][384] (padded), meta [G]
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
     __shared__ float red[W][16];
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
-    const int tw = wave / KS, ksl = wave % KS;
+    static_assert(TW == 1, "one tile per workgroup");
+    const int ksl = wave;
     const int G = int(p.G);
-    const int64_t tile = int64_t(blockIdx.x) * TW + tw;
-    const int64_t row = tile * 16 + ln;
-    const int64_t rc = row < p.N ? row : p.N - 1;
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxMulti; i++)
+        if (i < p.nmat && int(blockIdx.x) >= p.mat[i].tile0) mi = i;
+    const MatRef& mr = p.mat[mi];
+    const int64_t row = (int64_t(blockIdx.x) - mr.tile0) * 16 + ln;
+    const int64_t rc = row < mr.N ? row : mr.N - 1;
     const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
-    const uint8_t* qrow = p.q + rc * row_bytes;
-    const uint16_t* srow = p.scales + rc * G;
-    const uint8_t* zrow = KIND == 1 ? p.zeros + rc * G : nullptr;
+    const uint8_t* qrow = mr.q + rc * row_bytes;
+    const uint16_t* srow = mr.scales + rc * G;
+    const uint8_t* zrow = KIND == 1 ? mr.zeros + rc * G : nullptr;
     const int gbeg = ksl * p.gs < G ? ksl * p.gs : G;
     const int gend = gbeg + p.gs < G ? gbeg + p.gs : G;
     const bool active = gend > gbeg;
     // Clamp bound for idle waves (their loads re-read groups 0..3, in bounds;
     // the 4-group scale loads need a bound of at least 4).
     const int g0c = active ? gbeg : 0;
-    const int gcl = active ? gend : (VEC ? 4 : 1);
+    const int gcl = active ? gend : (MODE == 2 ? 4 : 1);
     const int nch = G * (kLimbRec / 16);      // 16-byte limb chunks of the row
     int4* ms1 = reinterpret_cast<int4*>(xs1 + nch * 16);
 
@@ -329,7 +370,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p)
     // 2. All weight batches of the slice.
     WBatch<KIND, GB> wb[NB];
 #pragma unroll
-    for (int bi = 0; bi < NB; bi++) load_batch<KIND, GB, VEC>(wb[bi], qrow, srow, zrow, g0c + bi * GB, gcl, kg, row_bytes);
+    for (int bi = 0; bi < NB; bi++) load_batch<KIND, GB, MODE>(wb[bi], qrow, srow, zrow, g0c + bi * GB, gcl, kg, row_bytes);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int c = tid + i * 64 * W;
@@ -375,191 +416,213 @@ __global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p)
         }
     }
     if (KS == 1) {
-        if (lane < 16 && row < p.N) p.y[row] = acc + (p.bias ? bf16_to_f32(p.bias[row]) : 0.0f);
+        if (lane < 16 && row < mr.N) mr.y[row] = acc + (mr.bias ? bf16_to_f32(mr.bias[row]) : 0.0f);
         return;
     }
     if (lane < 16) red[wave][lane] = acc;
     __syncthreads();
-    if (tid < 16 * TW) {
-        const int t = tid / 16, r = tid % 16;
-        const int64_t n = (int64_t(blockIdx.x) * TW + t) * 16 + r;
-        if (n < p.N) {
-            float sum = red[t * KS][r];
+    if (tid < 16) {
+        const int64_t n = (int64_t(blockIdx.x) - mr.tile0) * 16 + tid;
+        if (n < mr.N) {
+            float sum = red[0][tid];
 #pragma unroll
-            for (int k = 1; k < KS; k++) sum += red[t * KS + k][r];
-            p.y[n] = sum + (p.bias ? bf16_to_f32(p.bias[n]) : 0.0f);
+            for (int k = 1; k < KS; k++) sum += red[k][tid];
+            mr.y[n] = sum + (mr.bias ? bf16_to_f32(mr.bias[n]) : 0.0f);
         }
     }
 }
 
 // ------------------------------------------------------------------ 2..32 rows
-constexpr int kLdsBudget = 72 * 1024;  // activation slice per workgroup
-
-// Workgroup = 4 waves; wave w owns R tiles of 16 output rows
-// (rows (rb*4 + w)*16R ...); the workgroup owns the K slice of groups
-// [ks*gs, ks*gs + gs), gs <= GMAX.  Every weight word of the slice is
-// requested before anything waits, the activation limbs of the slice are
-// staged once per workgroup in LDS, then the MFMAs run group by group.
-template <int KIND, int MT, int R, int GMAX, bool FAST>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
-    extern __shared__ __attribute__((aligned(16))) int8_t xsb[];
-    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
-    const int ks = blockIdx.x / p.nrb, rb = blockIdx.x % p.nrb;
-    const int64_t g0 = int64_t(ks) * p.gs;
-    const int ng = int(p.G - g0 < p.gs ? p.G - g0 : p.gs);
-    const int64_t row0 = (int64_t(rb) * 4 + wave) * 16 * R;
-    const int64_t row_bytes = KIND == 1 ? p.K / 2 : p.K;
+// Workgroup = 8 waves, wave w owns the 16-row tile (blockIdx.x % nrb) * 8 + w;
+// the workgroup walks its K slice (groups [ks*gs, ks*gs + gs)) in chunks of
+// GC groups.  Per chunk the activation limbs of all M rows are staged in LDS
+// once and shared by the 8 tiles; the weight words of the next chunk and the
+// activation limbs of the next chunk are in flight (registers) while the
+// current chunk is multiplied.
+//
+// Activation rows on the MFMA A operand (16 rows):
+//   ROWS4 (M <= 8): row 4*mm + L = limb L of activation row mt*4 + mm, so a
+//     tile of 4 activation rows needs 2 MFMAs per 128 columns, and lane
+//     (l%16 = n, l/16 = mm) ends with the 3 limb sums of one (row, n).
+//   otherwise: A row i = activation row mt*16 + i, one MFMA per limb
+//     (6 per 128 columns for 16 rows); D register r of limb L's MFMA holds
+//     (row mt*16 + 4*(l/16) + r, n = l%16).
+// With S > 1 slices (matrices too short to fill the GPU) each slice writes
+// fp32 partial sums and gemv_reduce adds them in slice order (deterministic).
+template <int KIND, bool ROWS4, int MT, int GC, bool VEC>
+__global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
+    extern __shared__ __attribute__((aligned(16))) int8_t xsb[];  // [GC][M][384] limbs, [GC][32] meta
+    __shared__ __attribute__((aligned(16))) int8_t xzero[16];
+    constexpr int NT = 512;
     constexpr int WPG = KIND == 1 ? 1 : 2;
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
+    const int G = int(p.G), M = p.M;
+    const int ks = blockIdx.x / p.nrb, rb = blockIdx.x % p.nrb;
+    const int gbeg = ks * p.gs < G ? ks * p.gs : G;
+    const int gend = gbeg + p.gs < G ? gbeg + p.gs : G;
+    const int nchunk = (gend - gbeg + GC - 1) / GC;
+    const int64_t row0 = (int64_t(rb) * 8 + wave) * 16;
+    const int64_t row = row0 + ln;
+    const int64_t rc = row < p.N ? row : p.N - 1;
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const uint8_t* qrow = p.q + rc * row_bytes;
+    const uint16_t* srow = p.scales + rc * G;
+    const uint8_t* zrow = KIND == 1 ? p.zeros + rc * G : nullptr;
+    const int xrec = M * kLimbRec;                 // bytes of limbs per group (all rows)
+    const int xch = GC * xrec / 16;                // 16-byte chunks per activation chunk
+    int4* msb = reinterpret_cast<int4*>(xsb + GC * xrec);
+    constexpr int XPT = (GC * kMaxRowsGemv * kLimbRec / 16 + NT - 1) / NT;  // max chunks per thread
+    if (tid < 4) reinterpret_cast<uint32_t*>(xzero)[tid] = 0u;
 
-    // 1. Weight words, scales and zero points of the whole slice, all in flight.
-    uint4 wv[GMAX][R][WPG];
-    float sc[GMAX][R];
-    int zz[GMAX][R];
-    bool rv[R];
-#pragma unroll
-    for (int t = 0; t < R; t++) {
-        const int64_t r = row0 + 16 * t + ln;
-        rv[t] = r < p.N;
-        const int64_t rc = rv[t] ? r : p.N - 1;
-        const uint8_t* qrow = p.q + rc * row_bytes;
-#pragma unroll
-        for (int gl = 0; gl < GMAX; gl++) {
-            const int64_t g = g0 + (gl < ng ? gl : ng - 1);  // unconditional, clamped
-#pragma unroll
-            for (int h = 0; h < WPG; h++) {
-                const int64_t off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
-                wv[gl][t][h] = FAST ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes);
-            }
-            sc[gl][t] = bf16_to_f32(p.scales[rc * p.G + g]);
-            zz[gl][t] = KIND == 1 ? int(p.zeros[rc * p.G + g]) : 0;
-        }
-    }
+    // register copies of one chunk: weights of this wave's tile, the
+    // activation limbs / meta slice of this thread
+    uint4 wcur[GC][WPG], wnxt[GC][WPG];
+    int4v_t xr[XPT];
+    int4v_t mr;
+#define IQ_LOAD_W(W_, C_)                                                                               \
+    do {                                                                                                \
+        const int g0_ = gbeg + (C_) * GC;                                                               \
+        _Pragma("unroll") for (int gl = 0; gl < GC; gl++) {                                             \
+            const int g = g0_ + gl < gend ? g0_ + gl : gend - 1;                                        \
+            _Pragma("unroll") for (int h = 0; h < WPG; h++) {                                           \
+                const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;              \
+                W_[gl][h] = VEC ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes); \
+            }                                                                                           \
+        }                                                                                               \
+    } while (0)
+#define IQ_LOAD_X(C_)                                                                                   \
+    do {                                                                                                \
+        const int g0_ = gbeg + (C_) * GC;                                                               \
+        const int ng_ = gend - g0_ < GC ? gend - g0_ : GC;                                              \
+        const int lim_ = ng_ * xrec / 16;                                                               \
+        _Pragma("unroll") for (int i = 0; i < XPT; i++) {                                               \
+            const int t = tid + i * NT < lim_ ? tid + i * NT : lim_ - 1;                                \
+            const int gl = t / (xrec / 16), rem = t % (xrec / 16);                                      \
+            xr[i] = *reinterpret_cast<const int4v_t*>(p.xq + (int64_t(rem / 24) * G + g0_ + gl) * kLimbRec + (rem % 24) * 16); \
+        }                                                                                               \
+        mr = reinterpret_cast<const int4v_t*>(p.meta)[(g0_ + (tid / kMeta < ng_ ? tid / kMeta : ng_ - 1)) * kMeta + tid % kMeta]; \
+    } while (0)
+#define IQ_STORE_X(C_)                                                                                  \
+    do {                                                                                                \
+        const int g0_ = gbeg + (C_) * GC;                                                               \
+        const int ng_ = gend - g0_ < GC ? gend - g0_ : GC;                                              \
+        const int lim_ = ng_ * xrec / 16;                                                               \
+        _Pragma("unroll") for (int i = 0; i < XPT; i++) {                                               \
+            const int t = tid + i * NT < lim_ ? tid + i * NT : lim_ - 1; /* clamped: identical bytes */ \
+            reinterpret_cast<int4v_t*>(xsb)[t] = xr[i];                                                 \
+        }                                                                                               \
+        const int gl_ = tid / kMeta < ng_ ? tid / kMeta : ng_ - 1;                                      \
+        if (tid < GC * kMeta) reinterpret_cast<int4v_t*>(msb)[gl_ * kMeta + tid % kMeta] = mr;         \
+    } while (0)
 
-    // 2. Activation limbs of the slice -> LDS as records [gl][m][3*128],
-    //    then the meta records [gl][32].
-    int4* msb = reinterpret_cast<int4*>(xsb + ng * p.M * kLimbRec);
-    {
-        const int nchunks = ng * p.M * (kLimbRec / 16);
-        for (int c = tid; c < nchunks; c += 256) {
-            const int rec = c / (kLimbRec / 16), piece = c % (kLimbRec / 16);
-            const int gl = rec / p.M, m = rec % p.M;
-            const int8_t* src = p.xq + (int64_t(m) * p.G + g0 + gl) * kLimbRec + piece * 16;
-            *reinterpret_cast<uint4*>(xsb + rec * kLimbRec + piece * 16) = *reinterpret_cast<const uint4*>(src);
-        }
-        for (int c = tid; c < ng * kMeta; c += 256) msb[c] = p.meta[(g0 + c / kMeta) * kMeta + c % kMeta];
-    }
+    constexpr int NACC = ROWS4 ? 1 : 4;
+    float acc[MT][NACC];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int r = 0; r < NACC; r++) acc[mt][r] = 0.0f;
+
+    IQ_LOAD_X(0);
+    IQ_LOAD_W(wcur, 0);
+    IQ_LOAD_W(wnxt, 1 < nchunk ? 1 : 0);
+    IQ_STORE_X(0);
     __syncthreads();
-
-    float4_t acc[R][MT];
+    for (int c = 0; c < nchunk; c++) {
+        if (c + 1 < nchunk) IQ_LOAD_X(c + 1);
+        const int g0 = gbeg + c * GC;
+        const int ng = gend - g0 < GC ? gend - g0 : GC;
 #pragma unroll
-    for (int t = 0; t < R; t++)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[t][mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll
-    for (int gl = 0; gl < GMAX; gl++) {
-        if (gl >= ng) break;
-        int4v_t a[MT][3][2];
-        int4 md[MT][4];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const int m = mt * 16 + ln;
-            const int mr = m < p.M ? m : 0;
-#pragma unroll
-            for (int L = 0; L < 3; L++)
-#pragma unroll
-                for (int st = 0; st < 2; st++) {
-                    const int4v_t v = *reinterpret_cast<const int4v_t*>(xsb + (gl * p.M + mr) * kLimbRec + L * kGroup + st * 64 + kg * 16);
-                    a[mt][L][st] = m < p.M ? v : int4v_t{0, 0, 0, 0};
-                }
-#pragma unroll
-            for (int r = 0; r < 4; r++) md[mt][r] = msb[gl * kMeta + mt * 16 + 4 * kg + r];
-        }
-#pragma unroll
-        for (int t = 0; t < R; t++) {
+        for (int gl = 0; gl < GC; gl++) {
+            if (gl >= ng) break;
+            const int g = g0 + gl;
             int4v_t b0, b1;
-            weight_operands<KIND>(wv[gl][t], b0, b1);
+            weight_operands<KIND>(wcur[gl], b0, b1);
+            const uint32_t sw = srow[g];  // bf16 scale (L1/L2 hit after the first tile)
+            const float s = __uint_as_float(sw << 16);
+            const int z = KIND == 1 ? int(zrow[g]) : 0;
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                int4v_t D[3];
+                if (ROWS4) {
+                    const int mm = ln >> 2, L = ln & 3, m = mt * 4 + mm;
+                    int4v_t a[2];
 #pragma unroll
-                for (int L = 0; L < 3; L++) {
-                    D[L] = mfma_i8(a[mt][L][0], b0, int4v_t{0, 0, 0, 0});
-                    D[L] = mfma_i8(a[mt][L][1], b1, D[L]);
-                }
-                const int z = zz[gl][t];
+                    for (int st = 0; st < 2; st++) {
+                        const int8_t* pa = (L < 3 && m < M) ? xsb + (gl * M + m) * kLimbRec + L * kGroup + st * 64 + kg * 16 : xzero;
+                        a[st] = *reinterpret_cast<const int4v_t*>(pa);
+                    }
+                    int4v_t D = mfma_i8(a[0], b0, int4v_t{0, 0, 0, 0});
+                    D = mfma_i8(a[1], b1, D);
+                    const int mo = mt * 4 + kg;  // activation row of this lane's D
+                    if (mo < M) acc[mt][0] = combine(acc[mt][0], D[0], D[1], D[2], z, msb[gl * kMeta + mo], s);
+                } else {
+                    const int m = mt * 16 + ln;
+                    int4v_t D[3];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int m = mt * 16 + 4 * kg + r;
-                    if (m < p.M) acc[t][mt][r] = combine(acc[t][mt][r], D[0][r], D[1][r], D[2][r], z, md[mt][r], sc[gl][t]);
+                    for (int L = 0; L < 3; L++) {
+                        int4v_t a[2];
+#pragma unroll
+                        for (int st = 0; st < 2; st++) {
+                            const int8_t* pa = m < M ? xsb + (gl * M + m) * kLimbRec + L * kGroup + st * 64 + kg * 16 : xzero;
+                            a[st] = *reinterpret_cast<const int4v_t*>(pa);
+                        }
+                        D[L] = mfma_i8(a[0], b0, int4v_t{0, 0, 0, 0});
+                        D[L] = mfma_i8(a[1], b1, D[L]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int mo = mt * 16 + 4 * kg + r;
+                        if (mo < M) acc[mt][r] = combine(acc[mt][r], D[0][r], D[1][r], D[2][r], z, msb[gl * kMeta + mo], s);
+                    }
                 }
             }
+        }
+        if (c + 1 < nchunk) {
+#pragma unroll
+            for (int gl = 0; gl < GC; gl++)
+#pragma unroll
+                for (int h = 0; h < WPG; h++) wcur[gl][h] = wnxt[gl][h];
+            IQ_LOAD_W(wnxt, c + 2 < nchunk ? c + 2 : c + 1);
+            __syncthreads();  // every wave is done with chunk c in LDS
+            IQ_STORE_X(c + 1);
+            __syncthreads();
         }
     }
 
-    // 3. Epilogue.  Lane holds rows m = mt*16 + 4*kg + r of output n = row0 + 16t + ln.
-    if (p.S == 1) {
+#undef IQ_LOAD_W
+#undef IQ_LOAD_X
+#undef IQ_STORE_X
+    // Epilogue: this lane's outputs (row, activation row) pairs.
+    if (row >= p.N) return;
+    const float b = p.bias ? bf16_to_f32(p.bias[row]) : 0.0f;
 #pragma unroll
-        for (int t = 0; t < R; t++) {
-            if (!rv[t]) continue;
-            const int64_t n = row0 + 16 * t + ln;
-            const float b = p.bias ? bf16_to_f32(p.bias[n]) : 0.0f;
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int m = mt * 16 + 4 * kg + r;
-                    if (m < p.M) p.y[int64_t(m) * p.N + n] = acc[t][mt][r] + b;
-                }
+        for (int r = 0; r < NACC; r++) {
+            const int mo = ROWS4 ? mt * 4 + kg : mt * 16 + 4 * kg + r;
+            if (ROWS4 && ln >= 16) continue;
+            if (mo >= M) continue;
+            if (p.S == 1) p.y[int64_t(mo) * p.N + row] = acc[mt][r] + b;
+            else p.part[(int64_t(ks) * M + mo) * p.N + row] = acc[mt][r];
         }
-        return;
-    }
-    // Split K: publish this slice's partial sums; the last of the S slices to
-    // arrive for this wave's rows adds them in slice order (deterministic).
-#pragma unroll
-    for (int t = 0; t < R; t++) {
-        if (!rv[t]) continue;
-        const int64_t n = row0 + 16 * t + ln;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mt * 16 + 4 * kg + r;
-                if (m < p.M) p.part[(int64_t(ks) * p.M + m) * p.N + n] = acc[t][mt][r];
-            }
-    }
-    __threadfence();
-    const int ci = rb * 4 + wave;
-    int prev = 0;
-    if (lane == 0) prev = atomicAdd(p.cnt + ci, 1);
-    prev = __shfl(prev, 0);
-    if (prev != p.S - 1) return;
-    __threadfence();
-#pragma unroll
-    for (int t = 0; t < R; t++) {
-        if (!rv[t]) continue;
-        const int64_t n = row0 + 16 * t + ln;
-        const float b = p.bias ? bf16_to_f32(p.bias[n]) : 0.0f;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mt * 16 + 4 * kg + r;
-                if (m >= p.M) continue;
-                float sum = 0.0f;
-                for (int s = 0; s < p.S; s++) sum += __builtin_nontemporal_load(p.part + (int64_t(s) * p.M + m) * p.N + n);
-                p.y[int64_t(m) * p.N + n] = sum + b;
-            }
-    }
-    if (lane == 0) p.cnt[ci] = 0;
+}
+
+// y[m, n] = sum over slices s of part[s, m, n] (in slice order) + bias[n].
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part, int S, int M, int64_t N,
+                                                          const uint16_t* __restrict__ bias, float* __restrict__ y) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(M) * N) return;
+    float sum = 0.0f;
+    for (int s = 0; s < S; s++) sum += part[int64_t(s) * M * N + i];
+    y[i] = sum + (bias ? bf16_to_f32(bias[i % N]) : 0.0f);
 }
 
 template <int KIND, int TW, int KS, int GB>
-void launch_gemv1_s(const GemvParams& p, int nb, bool vec, unsigned grid, size_t lds, hipStream_t stream) {
+void launch_gemv1_s(const GemvParams& p, int nb, int mode, unsigned grid, size_t lds, hipStream_t stream) {
 #define IQ_G1(NB)                                                                                  \
     do {                                                                                           \
-        if (vec) gemv1_kernel<KIND, TW, KS, GB, NB, true><<<grid, 64 * TW * KS, lds, stream>>>(p); \
-        else gemv1_kernel<KIND, TW, KS, GB, NB, false><<<grid, 64 * TW * KS, lds, stream>>>(p);    \
+        if (mode == 2) gemv1_kernel<KIND, TW, KS, GB, NB, 2><<<grid, 64 * TW * KS, lds, stream>>>(p); \
+        else if (mode == 1) gemv1_kernel<KIND, TW, KS, GB, NB, 1><<<grid, 64 * TW * KS, lds, stream>>>(p); \
+        else gemv1_kernel<KIND, TW, KS, GB, NB, 0><<<grid, 64 * TW * KS, lds, stream>>>(p);        \
     } while (0)
     switch (nb) {
         case 1: IQ_G1(1); break;
@@ -572,20 +635,27 @@ void launch_gemv1_s(const GemvParams& p, int nb, bool vec, unsigned grid, size_t
 
 // Instantiated workgroup shapes: one tile, KS = 4, 8 or 16 slices.
 template <int KIND, int GB>
-void launch_gemv1_t(const GemvParams& p, int KS, bool vec, unsigned grid, hipStream_t stream) {
+void launch_gemv1_t(const GemvParams& p, int KS, int vec, unsigned grid, hipStream_t stream) {
     const size_t lds = size_t(p.G) * kLimbRec + size_t(p.G + 1) * 16;
     const int nb = (p.gs + GB - 1) / GB;
-    if (KS == 1) launch_gemv1_s<KIND, 1, 1, GB>(p, nb, vec, grid, lds, stream);
-    else if (KS == 2) launch_gemv1_s<KIND, 1, 2, GB>(p, nb, vec, grid, lds, stream);
-    else if (KS == 4) launch_gemv1_s<KIND, 1, 4, GB>(p, nb, vec, grid, lds, stream);
+    if (KS == 4) launch_gemv1_s<KIND, 1, 4, GB>(p, nb, vec, grid, lds, stream);
     else if (KS == 8) launch_gemv1_s<KIND, 1, 8, GB>(p, nb, vec, grid, lds, stream);
     else launch_gemv1_s<KIND, 1, 16, GB>(p, nb, vec, grid, lds, stream);
 }
 
-template <int KIND, int MT, int R, int GMAX>
-void launch_gemv_t(const GemvParams& p, bool fast, unsigned grid, size_t lds, hipStream_t stream) {
-    if (fast) gemv_kernel<KIND, MT, R, GMAX, true><<<grid, 256, lds, stream>>>(p);
-    else gemv_kernel<KIND, MT, R, GMAX, false><<<grid, 256, lds, stream>>>(p);
+template <int KIND, int GC>
+void launch_gemvb_t(const GemvParams& p, bool vec, unsigned grid, size_t lds, hipStream_t stream) {
+    const int M = p.M;
+#define IQ_GB(R4, MT)                                                                         \
+    do {                                                                                      \
+        if (vec) gemvb_kernel<KIND, R4, MT, GC, true><<<grid, 512, lds, stream>>>(p);         \
+        else gemvb_kernel<KIND, R4, MT, GC, false><<<grid, 512, lds, stream>>>(p);            \
+    } while (0)
+    if (M <= 4) IQ_GB(true, 1);
+    else if (M <= 8) IQ_GB(true, 2);
+    else if (M <= 16) IQ_GB(false, 1);
+    else IQ_GB(false, 2);
+#undef IQ_GB
 }
 
 int env_int(const char* name, int dflt) {
@@ -614,7 +684,10 @@ hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* w
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
+namespace {
+
+// 2..32 rows (or a 1-row case the 1-row kernel does not cover), one matrix.
+hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
                                hipStream_t stream) {
     const int64_t N = W.rows, K = W.cols, G = W.groups;
     const int kind = W.kind;
@@ -624,65 +697,83 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
     p.xq = ws->xq; p.meta = ws->xmeta;
     p.bias = bias; p.y = y; p.part = ws->partials; p.cnt = ws->counters;
     p.M = M;
+    const int gc = (kind == 1 && M <= 16) ? 8 : 4;  // groups per chunk (LDS: 2 * gc * M * 384 B max)
+    static const int target = env_int("IQ_GEMV_WAVES", 2048);
+    p.nrb = int((N + 127) / 128);
+    const int64_t want_s = (int64_t(target) * device_cu_count() / 256 + int64_t(p.nrb) * 8 - 1) / (int64_t(p.nrb) * 8);
+    int S = int(want_s < 1 ? 1 : want_s);
+    if (S > (G + 1) / 2) S = int((G + 1) / 2);      // at least 2 groups per slice
+    if (S < 1) S = 1;
+    while (S > 1 && int64_t(S) * M * N > kPartialFloats) S--;
+    p.gs = int((G + S - 1) / S);
+    S = int((G + p.gs - 1) / p.gs);
+    p.S = S;
+    const unsigned grid = unsigned(int64_t(S) * p.nrb);
+    const size_t lds = size_t(gc) * (size_t(M) * kLimbRec + kMeta * 16);
+    const bool vec = (K % kGroup == 0);
+    if (kind == 1) {
+        if (gc == 8) launch_gemvb_t<1, 8>(p, vec, grid, lds, stream);
+        else launch_gemvb_t<1, 4>(p, vec, grid, lds, stream);
+    } else {
+        launch_gemvb_t<0, 4>(p, vec, grid, lds, stream);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    const int64_t n = int64_t(M) * N;
+    gemv_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, S, M, N, bias, y);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n,
+                                     int M, Workspace* ws, hipStream_t stream) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    const int kind = W[0].kind;
     const int gb1 = kind == 1 ? 8 : 4;  // groups per batch of the 1-row kernel (8 KB per wave)
-    if (M == 1 && G * (kLimbRec + 16) <= 96 * 1024) {
+    if (M == 1 && n <= kMaxMulti && G * (kLimbRec + 16) <= 96 * 1024) {
         // Workgroup = one 16-row tile x KS K-slices.  KS: the smallest of
         // 4, 8, 16 whose slices fit 4 batches and whose threads can stage the
         // activation row (8 chunks of 16 B each).  Measured on MI355X: 4
         // slices beat more, smaller workgroups whenever they fit.
-        const int64_t tiles = (N + 15) / 16;
         static const int forced = env_int("IQ_GEMV1_KS", 0);
         int KS = 0;
-        for (int ks : {4, 8, 16}) {  // 1 and 2 are instantiated for experiments
+        const int mode = K % kGroup ? 0 : (G % 4 ? 1 : 2);
+        for (int ks : {4, 8, 16}) {
             int gs = int((G + ks - 1) / ks);
-            if (K % kGroup == 0 && G % 4 == 0) gs = (gs + 3) / 4 * 4;
+            if (mode == 2) gs = (gs + 3) / 4 * 4;
             if (gs <= 4 * gb1 && G * 24 <= 8 * 64 * ks && G <= 64 * ks) { KS = ks; break; }
         }
         if (forced && KS) KS = forced;
         if (KS) {
+            GemvParams p{};
+            int tiles = 0;
+            for (int i = 0; i < n; i++) {
+                p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i], W[i].rows, tiles};
+                tiles += int((W[i].rows + 15) / 16);
+            }
+            p.nmat = n;
+            p.K = K; p.G = G;
+            p.xq = ws->xq; p.meta = ws->xmeta;
+            p.M = 1;
             p.gs = int((G + KS - 1) / KS);
-            const bool vec = (K % kGroup == 0) && (G % 4 == 0);
-            if (vec) p.gs = (p.gs + 3) / 4 * 4;  // 4-group aligned slices: vector scale loads
+            if (mode == 2) p.gs = (p.gs + 3) / 4 * 4;  // 4-group aligned slices: vector scale loads
             p.S = 1;
-            const unsigned grid = unsigned(tiles);
-            if (kind == 1) launch_gemv1_t<1, 8>(p, KS, vec, grid, stream);
-            else launch_gemv1_t<0, 4>(p, KS, vec, grid, stream);
+            if (kind == 1) launch_gemv1_t<1, 8>(p, KS, mode, unsigned(tiles), stream);
+            else launch_gemv1_t<0, 4>(p, KS, mode, unsigned(tiles), stream);
             return hipGetLastError();
         }
     }
-    const int MT = M <= 16 ? 1 : 2;
-    const int R = 2;
-    const int gmax = kind == 1 ? 8 : 4;
-    static const int target = env_int("IQ_GEMV_TARGET", 8);
-    p.nrb = int((N + 64 * R - 1) / (64 * R));
-    // Slice size: at most gmax groups, within the LDS budget, and enough
-    // slices to put ~target waves per CU on the device.
-    const size_t per_group = size_t(M) * kLimbRec + size_t(kMeta) * 16;
-    int gs = gmax;
-    while (gs > 1 && size_t(gs) * per_group > size_t(kLdsBudget)) gs--;
-    const int64_t waves_per_slice = int64_t(p.nrb) * 4;
-    const int64_t want_waves = int64_t(device_cu_count()) * target;
-    const int64_t want_s = (want_waves + waves_per_slice - 1) / waves_per_slice;
-    int64_t gs_t = (G + want_s - 1) / want_s;
-    if (gs_t < 1) gs_t = 1;
-    if (gs_t < gs) gs = int(gs_t);
-    int S = int((G + gs - 1) / gs);
-    // Split-K scratch limits: partial sums and one counter per wave.
-    if (S > 1 && (int64_t(S) * M * N > kPartialFloats || int64_t(p.nrb) * 4 > kMaxCounters)) return hipErrorInvalidValue;
-    p.gs = gs;
-    p.S = S;
-    const unsigned grid = unsigned(int64_t(S) * p.nrb);
-    const size_t lds = size_t(gs) * per_group;
-    const bool fast = (K % kGroup == 0);
-#define IQ_GEMV_DISPATCH(KIND, GM)                                                         \
-    do {                                                                                   \
-        if (MT == 1) launch_gemv_t<KIND, 1, 2, GM>(p, fast, grid, lds, stream);            \
-        else launch_gemv_t<KIND, 2, 2, GM>(p, fast, grid, lds, stream);                    \
-    } while (0)
-    if (kind == 1) IQ_GEMV_DISPATCH(1, 8);
-    else IQ_GEMV_DISPATCH(0, 4);
-#undef IQ_GEMV_DISPATCH
-    return hipGetLastError();
+    for (int i = 0; i < n; i++) {
+        const hipError_t e = launch_gemv_batched(W[i], bias[i], M, y[i], ws, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
+                               hipStream_t stream) {
+    return launch_gemv_prepped_multi(&W, &bias, &y, 1, M, ws, stream);
 }
 
 hipError_t launch_gemv(const float* x, const QView& W, const uint16_t* bias, int M, float* y,

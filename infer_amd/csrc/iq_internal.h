@@ -52,6 +52,10 @@ hipError_t launch_gemv(const float* x, const QView& W, const uint16_t* bias, int
 hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream);
 hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
                                hipStream_t stream);
+// Several matrices of one kind and width on the same prepared activations
+// (n <= 4): one launch for 1 row, one launch per matrix otherwise.
+hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n,
+                                     int M, Workspace* ws, hipStream_t stream);
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
                        const uint16_t* bias, int64_t T, float* y, hipStream_t stream);
 

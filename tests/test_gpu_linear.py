@@ -120,3 +120,21 @@ def test_embedding_exact(kind):
     ref = O.embedding(W.q, W.s, W.z, kind, 256, ids)
     assert np.array_equal(o[: ids.size * 256].reshape(len(ids), 256), ref)
     assert np.all(o[ids.size * 256:] == CANARY)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_multi_matches_oracle(kind, M):
+    """q|k|v (and gate|up) in one call: each output equals the oracle."""
+    rng = np.random.default_rng(31 + kind + M)
+    K = 1536
+    Ws = [QFix(rng, N, K, kind, sd=0.02) for N in (1536, 256, 256)]
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    bb, bd = bias_of(rng, 256)
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("gemv multi", kind, M)
+    ops.gemv_prep(torch.from_numpy(x).cuda(), M, K, kind)
+    ops.gemv_prepped_multi([W.view for W in Ws], [None, bd, None], M, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y) in enumerate(zip(Ws, ys)):
+        check_linear(y, x, W, bb if i == 1 else None, M, f"multi[{i}] kind={kind} M={M}")
