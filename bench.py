@@ -19,8 +19,10 @@ timed region; the 7B set is ~4 GB, far beyond the 256 MB MALL, so each step
 streams the weights from HBM.
 
 Also reported (measured after the timed region, outside it):
-  roofline   the GEMV kernel alone (int4, 1 row) from HIP events around each
-             launch on its stream, bytes-weighted over the 196 layer matrices;
+  roofline   the GEMV kernel alone (int4, 1 row): its 112 launches (q|k|v,
+             o, gate|up, down of 28 layers) timed with HIP events on their
+             stream, grouped by matrix shape and run back to back; traffic
+             from profiles/gemv_int4_7b_m1_traffic.json (rocprofv3 counters);
   cpu_baseline  the reference CPU path (src/forward.cpp linear over dequant(),
              restated in oracle/iq_oracle.c) on a bounded sample, 1 thread;
   detail     int4 at 16 rows, the int8 set at 1 and 16 rows, the prefill GEMM
@@ -126,25 +128,18 @@ class Step:
                     self.bytes += W.nbytes() + 4 * M * W.rows
                 self.bytes += 4 * M * op[1][0].cols
 
-    def run(self, timing=None):
+    def run(self):
         ops, M = self.ops, self.M
-        cur = None
         for op in self.ops_list:
             if op[0] == "prep":
                 x = self.x[op[1]]
                 ops.gemv_prep(x, M, x.shape[1], op[2])
             else:
                 Ws, ynames = op[1], op[2]
-                if timing is not None:
-                    timing.append((Ws, self.torch.cuda.Event(enable_timing=True),
-                                   self.torch.cuda.Event(enable_timing=True)))
-                    timing[-1][1].record()
                 if len(Ws) == 1:
                     ops.gemv_prepped(Ws[0], None, M, Ws[0].cols, Ws[0].rows, self.y[ynames[0]])
                 else:
                     ops.gemv_prepped_multi(Ws, None, M, Ws[0].cols, [self.y[n] for n in ynames])
-                if timing is not None:
-                    timing[-1][2].record()
 
     def capture(self):
         torch = self.torch
@@ -173,21 +168,47 @@ def time_graph(torch, g, steps, warmup):
 
 
 def kernel_roofline(torch, step, only_kind=None):
-    """Per-launch GEMV kernel durations from HIP events on the launch stream.
-    The queue is backed up with a device-side sleep first so that the events
-    bracket kernels that run back to back."""
+    """Average GEMV launch duration from HIP events on the launch stream
+    (torch's current stream, which the ctypes calls pass down).  The step's
+    GEMV launches are grouped by their place in a layer (q|k|v, o, gate|up,
+    down); for each group the activation block is prepared once, then the
+    group's launches (one per layer, each on its own weights) run back to back
+    between two events.  A device-side sleep queued first lets the host
+    enqueue everything before the GPU reaches it, so the events bracket
+    kernels and not host launch latency."""
+    groups = {}
+    prep = None
+    for op in step.ops_list:
+        if op[0] == "prep":
+            prep = op
+        else:
+            key = tuple(W.rows for W in op[1]) + (op[1][0].cols, op[1][0].kind)
+            groups.setdefault(key, (prep, []))[1].append(op)
+    M, ops = step.M, step.ops
     timing = []
     torch.cuda._sleep(int(2.4e9 * 0.05))
-    step.run(timing)
+    for key, (prep, gops) in groups.items():
+        if only_kind is not None and key[-1] != only_kind:
+            continue
+        x = step.x[prep[1]]
+        ops.gemv_prep(x, M, x.shape[1], prep[2])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _, Ws, ynames in gops:
+            if len(Ws) == 1:
+                ops.gemv_prepped(Ws[0], None, M, Ws[0].cols, Ws[0].rows, step.y[ynames[0]])
+            else:
+                ops.gemv_prepped_multi(Ws, None, M, Ws[0].cols, [step.y[n] for n in ynames])
+        e1.record()
+        nb = sum(sum(W.nbytes() + 4 * M * W.rows for W in Ws) + 4 * M * Ws[0].cols
+                 for _, Ws, _ in gops)
+        timing.append((nb, len(gops), e0, e1))
     torch.cuda.synchronize()
     tot_b, tot_ms, n = 0, 0.0, 0
-    for Ws, a, b in timing:
-        if only_kind is not None and Ws[0].kind != only_kind:
-            continue
-        ms = a.elapsed_time(b)
-        tot_b += sum(W.nbytes() + 4 * step.M * W.rows for W in Ws) + 4 * step.M * Ws[0].cols
-        tot_ms += ms
-        n += 1
+    for nb, cnt, e0, e1 in timing:
+        tot_b += nb
+        tot_ms += e0.elapsed_time(e1)
+        n += cnt
     return tot_b, tot_ms, n
 
 
@@ -263,6 +284,24 @@ def bench_gemv_single(torch, ops, kind, N, K, M, copies, reps=200, seed=11):
     return per_ms * 1e3, nb / (per_ms * 1e-3) / 1e9
 
 
+def profile_workload(torch, ops):
+    """Fixed short workload for `rocprofv3 --pmc` runs: 4 layers of the 7B
+    int4 set at 1 row (q|k|v, o, gate|up, down launches as in the step), then
+    a plain 256 MiB device copy (3 times) whose FETCH_SIZE / WRITE_SIZE per
+    dispatch calibrate the counters (known bytes read and written)."""
+    m4 = Model(torch, ops, 1, H7, I7, NH7 * 128, KV7 * 128, 4, head=None, seed=7)
+    st = Step(torch, ops, m4, 1)
+    for _ in range(3):
+        st.run()
+    torch.cuda.synchronize()
+    a = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -270,6 +309,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no detail / CPU baseline)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", action="store_true",
+                    help="short fixed workload for rocprofv3 counter runs (prints nothing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -280,6 +321,9 @@ def main():
     import torch
     from infer_amd import ops
     ops.init(0)
+    if args.profile:
+        profile_workload(torch, ops)
+        return
     t_setup = time.perf_counter()
 
     # ---- headline: 7B int4 set + int8 lm_head, 1 row
@@ -403,7 +447,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "int8",
         "data": "synthetic",
         "config": {
             "workload": "Qwen2.5-7B decode linear set, int4 group-128 (bf16 scale, u8 zero) x 28 layers "
