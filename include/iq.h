@@ -69,8 +69,9 @@ int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64
 /* The two halves of iq_gemv, for callers that multiply one activation
  * block by several matrices (q/k/v, gate/up share their input):
  * iq_gemv_prep converts x [B][in] (fp32) once into the device workspace
- * (fp16 hi/lo pairs with a power-of-two scale per row and 128-column group,
- * in the column order that `kind`'s dequantisation produces);
+ * (per row and 128-column group: a power-of-two scale 2^-k and the integer
+ * rint(x * 2^k) as three signed byte limbs, in the column order that
+ * `kind`'s weight unpacking produces);
  * iq_gemv_prepped then runs the GEMV of any matrix of that kind and width on
  * the prepared block.  A prepared block stays valid until the next
  * iq_gemv / iq_gemv_prep on the device (stream order).  iq_gemv_prepped
