@@ -8,10 +8,10 @@ k/v 512x3584, o 3584x3584, gate/up 18944x3584, down 3584x18944) in int4
 (group 128, bf16 scale, u8 zero point) plus the int8 lm_head 152064x3584,
 weights seeded ~N(0, 0.02) -> bf16 -> quantised on the device (bit-exact to
 src/quant.cpp), activations fp32 ~N(0, 1).  The step is issued the way a
-decode engine issues it -- activations prepared once per distinct input
-(attention input, attention context, MLP input, MLP hidden, final norm),
-then one GEMV per matrix -- and captured in one HIP graph, as the
-reference's engine captures its step (kernels/batch_gpu.cu:255-269).
+decode engine issues it -- one call per distinct input (attention input:
+q|k|v in one call; attention context: o; MLP input: gate|up in one call;
+MLP hidden: down; final norm: lm_head) -- and captured in one HIP graph, as
+the reference's engine captures its step (kernels/batch_gpu.cu:255-269).
 
 value = packed weight bytes + activation bytes read + output bytes written,
 per step, / time per step (GB/s).  All inputs are resident in HBM before the
@@ -106,40 +106,33 @@ class Step:
         self.y = {name: torch.empty(M, out, device="cuda") for name, out, _, _ in model.shapes}
         if model.head is not None:
             self.y["head"] = torch.empty(M, model.head.rows, device="cuda")
-        # op list: ("prep", slot, kind) | ("gemv", [W...], [yname...]); matrices
-        # that share an activation (q|k|v, gate|up) go in one call.
+        # op list: (activation slot, [W...], [yname...]); matrices that share
+        # an activation (q|k|v, gate|up) go in one call.
         self.ops_list = []
         for L in model.layers:
             last = None
             for name, out, inn, slot in model.shapes:
                 if slot != last:
-                    self.ops_list.append(("prep", slot, model.kind))
-                    self.ops_list.append(("gemv", [], []))
+                    self.ops_list.append((slot, [], []))
                     last = slot
                 self.ops_list[-1][1].append(L[name])
                 self.ops_list[-1][2].append(name)
         if model.head is not None:
-            self.ops_list.append(("prep", "head", model.head.kind))
-            self.ops_list.append(("gemv", [model.head], ["head"]))
+            self.ops_list.append(("head", [model.head], ["head"]))
         self.bytes = 0
-        for op in self.ops_list:
-            if op[0] == "gemv":
-                for W in op[1]:
-                    self.bytes += W.nbytes() + 4 * M * W.rows
-                self.bytes += 4 * M * op[1][0].cols
+        for _, Ws, _ in self.ops_list:
+            for W in Ws:
+                self.bytes += W.nbytes() + 4 * M * W.rows
+            self.bytes += 4 * M * Ws[0].cols
 
     def run(self):
         ops, M = self.ops, self.M
-        for op in self.ops_list:
-            if op[0] == "prep":
-                x = self.x[op[1]]
-                ops.gemv_prep(x, M, x.shape[1], op[2])
-            else:
-                Ws, ynames = op[1], op[2]
-                if len(Ws) == 1:
-                    ops.gemv_prepped(Ws[0], None, M, Ws[0].cols, Ws[0].rows, self.y[ynames[0]])
-                else:
-                    ops.gemv_prepped_multi(Ws, None, M, Ws[0].cols, [self.y[n] for n in ynames])
+        for slot, Ws, ynames in self.ops_list:
+            self.launch(slot, Ws, ynames)
+
+    def launch(self, slot, Ws, ynames):
+        x = self.x[slot]
+        self.ops.gemv_multi(x, Ws, None, self.M, x.shape[1], [self.y[n] for n in ynames])
 
     def capture(self):
         torch = self.torch
@@ -171,34 +164,25 @@ def kernel_roofline(torch, step, only_kind=None):
     """Average GEMV launch duration from HIP events on the launch stream
     (torch's current stream, which the ctypes calls pass down).  The step's
     GEMV launches are grouped by their place in a layer (q|k|v, o, gate|up,
-    down); for each group the activation block is prepared once, then the
-    group's launches (one per layer, each on its own weights) run back to back
-    between two events.  A device-side sleep queued first lets the host
-    enqueue everything before the GPU reaches it, so the events bracket
-    kernels and not host launch latency."""
+    down); each group's launches (one per layer, each on its own weights) run
+    back to back between two events.  A device-side sleep queued first lets
+    the host enqueue everything before the GPU reaches it, so the events
+    bracket kernels and not host launch latency."""
     groups = {}
-    prep = None
     for op in step.ops_list:
-        if op[0] == "prep":
-            prep = op
-        else:
-            key = tuple(W.rows for W in op[1]) + (op[1][0].cols, op[1][0].kind)
-            groups.setdefault(key, (prep, []))[1].append(op)
-    M, ops = step.M, step.ops
+        Ws = op[1]
+        key = tuple(W.rows for W in Ws) + (Ws[0].cols, Ws[0].kind)
+        groups.setdefault(key, []).append(op)
+    M = step.M
     timing = []
     torch.cuda._sleep(int(2.4e9 * 0.05))
-    for key, (prep, gops) in groups.items():
+    for key, gops in groups.items():
         if only_kind is not None and key[-1] != only_kind:
             continue
-        x = step.x[prep[1]]
-        ops.gemv_prep(x, M, x.shape[1], prep[2])
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _, Ws, ynames in gops:
-            if len(Ws) == 1:
-                ops.gemv_prepped(Ws[0], None, M, Ws[0].cols, Ws[0].rows, step.y[ynames[0]])
-            else:
-                ops.gemv_prepped_multi(Ws, None, M, Ws[0].cols, [step.y[n] for n in ynames])
+        for op in gops:
+            step.launch(*op)
         e1.record()
         nb = sum(sum(W.nbytes() + 4 * M * W.rows for W in Ws) + 4 * M * Ws[0].cols
                  for _, Ws, _ in gops)

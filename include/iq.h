@@ -90,6 +90,15 @@ int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, i
 int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
                           int64_t in, float* const* ys, void* stream);
 
+/* iq_gemv for n <= 4 matrices of one kind and width sharing the activations
+ * x [B][in]: at B = 1 one launch reads x and all n matrices (the activation
+ * conversion happens inside the GEMV kernel); at other B, x is converted once
+ * and each matrix runs its own launch.  Same matrix/bias conventions as
+ * iq_gemv_prepped_multi; the prepared block of the workspace is overwritten
+ * when B > 1.  No reference counterpart (see iq_gemv_prepped_multi). */
+int iq_gemv_multi(const float* x, const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
+                  int64_t in, float* const* ys, void* stream);
+
 /* Same contract for any T >= 1 (fp32 activations).  Replaces
  * launch_gemm_tiled_q (kernels/ops/ops.cuh:175-176, kernels/ops/quant.cu:347-351).
  * Runs the MFMA prefill GEMM with the activations split into bf16 hi + lo. */

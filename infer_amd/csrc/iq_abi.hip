@@ -23,26 +23,21 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 hipError_t create_workspace(int dev, Workspace* ws) {
     const int64_t gmax = kMaxKp / kGroup;
-    const size_t cnt = align256(sizeof(int) * kMaxCounters);
+    const size_t xf = align256(sizeof(float) * kMaxKp);
     const size_t xq = align256(size_t(kMaxRowsGemv) * gmax * 3 * kGroup);
     const size_t meta = align256(sizeof(int4) * gmax * kMaxRowsGemv);
     const size_t part = align256(sizeof(float) * kPartialFloats);
-    const size_t total = cnt + xq + meta + part;
+    const size_t total = xf + xq + meta + part;
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, total);
     if (e != hipSuccess) return e;
-    // Counters start at zero; each split-K launch leaves them at zero.
-    e = hipMemset(base, 0, cnt);
-    if (e != hipSuccess) { (void)hipFree(base); return e; }
-    e = hipDeviceSynchronize();
-    if (e != hipSuccess) { (void)hipFree(base); return e; }
     char* p = static_cast<char*>(base);
     ws->base = base;
     ws->bytes = total;
-    ws->counters = reinterpret_cast<int*>(p);
-    ws->xq = reinterpret_cast<int8_t*>(p + cnt);
-    ws->xmeta = reinterpret_cast<int4*>(p + cnt + xq);
-    ws->partials = reinterpret_cast<float*>(p + cnt + xq + meta);
+    ws->xf = reinterpret_cast<float*>(p);
+    ws->xq = reinterpret_cast<int8_t*>(p + xf);
+    ws->xmeta = reinterpret_cast<int4*>(p + xf + xq);
+    ws->partials = reinterpret_cast<float*>(p + xf + xq + meta);
     (void)dev;
     return hipSuccess;
 }
@@ -161,12 +156,13 @@ int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, i
     return from_hip(iq::launch_gemv_prepped(to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
 }
 
-int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
-                          int64_t in, float* const* ys, void* stream) {
-    if (!Ws || !ys || n < 1 || n > 4) return n < 1 || n > 4 ? IQ_ESHAPE : IQ_ENULL;
-    iq::QView v[4];
-    const uint16_t* b[4];
-    float* y[4];
+namespace {
+
+// Validates n <= 4 matrices of one kind and width `in` and unpacks them.
+int gather_views(const iq_view* const* Ws, int n, const uint16_t* const* biases, int64_t in,
+                 float* const* ys, iq::QView* v, const uint16_t** b, float** y) {
+    if (n < 1 || n > 4) return IQ_ESHAPE;
+    if (!Ws || !ys) return IQ_ENULL;
     for (int i = 0; i < n; i++) {
         if (!Ws[i]) return IQ_ENULL;
         const int rc = check_view(Ws[i], in, Ws[i]->rows);
@@ -177,11 +173,39 @@ int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const
         b[i] = biases ? biases[i] : nullptr;
         y[i] = ys[i];
     }
+    return IQ_OK;
+}
+
+}  // namespace
+
+int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
+                          int64_t in, float* const* ys, void* stream) {
+    iq::QView v[4];
+    const uint16_t* b[4];
+    float* y[4];
+    const int rc = gather_views(Ws, n, biases, in, ys, v, b, y);
+    if (rc) return rc;
     iq::Workspace* ws = nullptr;
     hipError_t e = iq::get_workspace(&ws);
     if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
     if (B != ws->prep_M || in != ws->prep_K || Ws[0]->kind != ws->prep_kind) return IQ_ESHAPE;
     return from_hip(iq::launch_gemv_prepped_multi(v, b, y, n, B, ws, static_cast<hipStream_t>(stream)));
+}
+
+int iq_gemv_multi(const float* x, const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
+                  int64_t in, float* const* ys, void* stream) {
+    iq::QView v[4];
+    const uint16_t* b[4];
+    float* y[4];
+    const int rc = gather_views(Ws, n, biases, in, ys, v, b, y);
+    if (rc) return rc;
+    if (!x) return IQ_ENULL;
+    if (B < 1 || B > iq::kMaxRowsGemv) return IQ_ESHAPE;
+    if (Ws[0]->groups * IQ_GROUP > iq::kMaxKp) return IQ_ETOOLARGE;
+    iq::Workspace* ws = nullptr;
+    hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    return from_hip(iq::launch_gemv_multi(x, v, b, y, n, B, ws, static_cast<hipStream_t>(stream)));
 }
 
 int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,

@@ -99,31 +99,13 @@ __device__ __forceinline__ int row16_and(int v) {
     return v;
 }
 
-// One wave per (row, 4 groups); 16 lanes (one DPP row) per group, 8 columns
-// per lane.
-template <bool PERM, bool VECX>
-__global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int M, int64_t K,
-                                                    int64_t G, int64_t quads,
-                                                    int8_t* __restrict__ xq, int4* __restrict__ meta) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (wave >= int64_t(M) * quads) return;
-    const int m = int(wave / quads);
-    const int64_t g = (wave % quads) * 4 + (lane >> 4);
-    const bool gvalid = g < G;
-    const int j = lane & 15;
-    const int64_t c0 = g * kGroup + j * 8;
-    const float* xr = x + int64_t(m) * K;
-    float v[8];
-    if (VECX && gvalid && c0 + 8 <= K) {
-        const float4 a = *reinterpret_cast<const float4*>(xr + c0);
-        const float4 b = *reinterpret_cast<const float4*>(xr + c0 + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = (gvalid && c0 + i < K) ? xr[c0 + i] : 0.0f;
-    }
+// Converts one (activation row, 128-column group) whose columns 8j..8j+7
+// are v[] of the lane with j = lane % 16 (the 16 lanes of a DPP row hold the
+// whole group; all 16 must call this together).  Writes this lane's limb
+// bytes into the group's record `rec` (when `store`) and returns the group's
+// meta record {2^-k as fp32 bits, sum X0, sum X1, sum X2} (every lane).
+template <bool PERM>
+__device__ __forceinline__ int4 convert_group(const float (&v)[8], int j, bool store, int8_t* rec) {
     // absmax; NaN must not be lost (fmaxf drops it), so track finiteness apart.
     float amax = 0.0f;
     int fin = 1;
@@ -155,39 +137,72 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
     s0 = row16_sum(s0);
     s1 = row16_sum(s1);
     s2 = row16_sum(s2);
-    if (!gvalid) return;
-    int8_t* rec = xq + (int64_t(m) * G + g) * kLimbRec;
-    const int* L[3] = {l0, l1, l2};
-    if (PERM) {
-        // columns 8j..8j+7: evens -> 4 contiguous bytes, odds -> 4 contiguous bytes
-        const int pe = limb_pos(j * 8, true), po = limb_pos(j * 8 + 1, true);
+    if (store) {
+        const int* L[3] = {l0, l1, l2};
+        if (PERM) {
+            // columns 8j..8j+7: evens -> 4 contiguous bytes, odds -> 4 contiguous bytes
+            const int pe = limb_pos(j * 8, true), po = limb_pos(j * 8 + 1, true);
 #pragma unroll
-        for (int li = 0; li < 3; li++) {
-            uint32_t ev = 0, od = 0;
+            for (int li = 0; li < 3; li++) {
+                uint32_t ev = 0, od = 0;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                ev |= uint32_t(uint8_t(L[li][2 * e])) << (8 * e);
-                od |= uint32_t(uint8_t(L[li][2 * e + 1])) << (8 * e);
+                for (int e = 0; e < 4; e++) {
+                    ev |= uint32_t(uint8_t(L[li][2 * e])) << (8 * e);
+                    od |= uint32_t(uint8_t(L[li][2 * e + 1])) << (8 * e);
+                }
+                *reinterpret_cast<uint32_t*>(rec + li * kGroup + pe) = ev;
+                *reinterpret_cast<uint32_t*>(rec + li * kGroup + po) = od;
             }
-            *reinterpret_cast<uint32_t*>(rec + li * kGroup + pe) = ev;
-            *reinterpret_cast<uint32_t*>(rec + li * kGroup + po) = od;
-        }
-    } else {
+        } else {
 #pragma unroll
-        for (int li = 0; li < 3; li++) {
-            uint32_t lo = 0, hi = 0;
+            for (int li = 0; li < 3; li++) {
+                uint32_t lo = 0, hi = 0;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                lo |= uint32_t(uint8_t(L[li][e])) << (8 * e);
-                hi |= uint32_t(uint8_t(L[li][e + 4])) << (8 * e);
+                for (int e = 0; e < 4; e++) {
+                    lo |= uint32_t(uint8_t(L[li][e])) << (8 * e);
+                    hi |= uint32_t(uint8_t(L[li][e + 4])) << (8 * e);
+                }
+                *reinterpret_cast<uint2*>(rec + li * kGroup + j * 8) = make_uint2(lo, hi);
             }
-            *reinterpret_cast<uint2*>(rec + li * kGroup + j * 8) = make_uint2(lo, hi);
         }
     }
     // 2^-k (NaN when the group holds a non-finite value, so it propagates);
     // a group of values below ~2^-149 * 2^22 contributes 0.
     const float fx = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
-    if (j == 0) meta[g * kMeta + m] = make_int4(__float_as_int(fx), s0, s1, s2);
+    return make_int4(__float_as_int(fx), s0, s1, s2);
+}
+
+// Columns [c0, c0 + 8) of an activation row, zero past K.
+template <bool VECX>
+__device__ __forceinline__ void load_x8(const float* xr, int64_t c0, int64_t K, float (&v)[8]) {
+    if (VECX && c0 + 8 <= K) {
+        const float4 a = *reinterpret_cast<const float4*>(xr + c0);
+        const float4 b = *reinterpret_cast<const float4*>(xr + c0 + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = c0 + i < K ? xr[c0 + i] : 0.0f;
+    }
+}
+
+// One wave per (row, 4 groups); 16 lanes (one DPP row) per group, 8 columns
+// per lane.
+template <bool PERM, bool VECX>
+__global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int M, int64_t K,
+                                                    int64_t G, int64_t quads,
+                                                    int8_t* __restrict__ xq, int4* __restrict__ meta) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wave >= int64_t(M) * quads) return;
+    const int m = int(wave / quads);
+    const int64_t g = (wave % quads) * 4 + (lane >> 4);
+    const bool gvalid = g < G;
+    const int j = lane & 15;
+    float v[8];
+    load_x8<VECX>(x + int64_t(m) * K, (gvalid ? g : 0) * kGroup + j * 8, gvalid ? K : 0, v);
+    const int4 md = convert_group<PERM>(v, j, gvalid, xq + (int64_t(m) * G + (gvalid ? g : 0)) * kLimbRec);
+    if (gvalid && j == 0) meta[g * kMeta + m] = md;
 }
 
 // ------------------------------------------------------------------ shared pieces
@@ -212,12 +227,12 @@ struct GemvParams {
     const uint16_t* scales;
     const uint8_t* zeros;
     int64_t N, K, G;
+    const float* x;  // fp32 activation row (1-row kernel)
     const int8_t* xq;
     const int4* meta;
     const uint16_t* bias;
     float* y;
     float* part;
-    int* cnt;
     int M, S, gs, nrb;
 };
 
@@ -313,19 +328,22 @@ __device__ __forceinline__ void load_batch(WBatch<KIND, GB>& b, const uint8_t* q
 // one slice of gs <= NB*GB groups).  Every weight word, scale and zero point
 // of a wave's slice is requested at kernel start (NB batches of GB groups,
 // all loads unconditional - clamped into the slice - so nothing waits before
-// the last one is issued).  The activation row (limbs + meta records) is
-// staged in LDS once per workgroup, shared by the TW tiles; its loads are
-// issued before the weight loads, so waiting for them leaves the weights in
-// flight while the MFMAs start on the first groups.  With KS > 1 the slice partials of a tile are added through LDS in
-// slice order (deterministic): no cross-workgroup traffic, no device-scope
-// fence.  The A operand carries the activation's three byte limbs as rows
-// 0..2 of the 16-row MFMA tile (lanes l%16 = 0, 1, 2; the other lanes read a
-// zero block, no branches), so two MFMAs per 128 columns yield all three
-// exact limb sums, in D rows 0..2 of lanes 0..15.  MODE: see load_batch.
+// the last one is issued).  The fp32 activations of the wave's slice are
+// requested before the weights, and converted to byte limbs (as xprep does)
+// into the workgroup's LDS copy of the row while the weight words are in
+// flight: no separate conversion launch.  With KS > 1 the slice partials of
+// a tile are added through LDS in slice order (deterministic): no
+// cross-workgroup traffic, no device-scope fence.  The A operand carries the
+// activation's three byte limbs as rows 0..2 of the 16-row MFMA tile (lanes
+// l%16 = 0, 1, 2; the other lanes read a zero block, no branches), so two
+// MFMAs per 128 columns yield all three exact limb sums, in D rows 0..2 of
+// lanes 0..15.  MODE: see load_batch (MODE >= 1 also means K % 128 == 0 and
+// a 16-byte aligned activation row).
 template <int KIND, int TW, int KS, int GB, int NB, int MODE>
 __global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p) {
     constexpr int W = TW * KS;
-    extern __shared__ __attribute__((aligned(16))) int8_t xs1[];  // limbs [G][384] (padded), meta [G]
+    constexpr int XP = NB * GB / 4;  // conversion passes of 4 groups per wave
+    extern __shared__ __attribute__((aligned(16))) int8_t xs1[];  // limbs [G][384], meta [G]
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
     __shared__ float red[W][16];
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
@@ -350,33 +368,33 @@ __global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p)
     // the 4-group scale loads need a bound of at least 4).
     const int g0c = active ? gbeg : 0;
     const int gcl = active ? gend : (MODE == 2 ? 4 : 1);
-    const int nch = G * (kLimbRec / 16);      // 16-byte limb chunks of the row
-    int4* ms1 = reinterpret_cast<int4*>(xs1 + nch * 16);
+    int4* ms1 = reinterpret_cast<int4*>(xs1 + G * kLimbRec);
 
-    // 1. Activation limbs and meta records: loads issued first (so that a
-    //    wait for them leaves the weight words in flight), at most 8 chunks
-    //    per thread (host guarantees nch <= 8 * 64 * W); indices past the end
-    //    re-read / re-write the last chunk (identical bytes, no branches).
-    uint4 xc[8];
+    // 1. The slice's activations: pass t converts groups gbeg + 4t + kg,
+    //    16 lanes (one DPP row) per group, 8 columns per lane.  Loads are
+    //    clamped to the slice (idle waves: group 0), stores are masked.
+    float xv[XP][8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int c = tid + i * 64 * W;
-        xc[i] = reinterpret_cast<const uint4*>(p.xq)[c < nch ? c : nch - 1];
+    for (int t = 0; t < XP; t++) {
+        const int g = g0c + 4 * t + kg < gcl ? g0c + 4 * t + kg : gcl - 1;
+        load_x8<MODE >= 1>(p.x, int64_t(g) * kGroup + ln * 8, p.K, xv[t]);
     }
-    const int4 mreg = p.meta[(tid < G ? tid : G - 1) * kMeta];  // G <= 64*W (host)
-    const int mslot = tid < G ? tid : G;                            // slot G: scratch
     if (tid < 4) reinterpret_cast<uint32_t*>(xzero)[tid] = 0u;
 
     // 2. All weight batches of the slice.
     WBatch<KIND, GB> wb[NB];
 #pragma unroll
     for (int bi = 0; bi < NB; bi++) load_batch<KIND, GB, MODE>(wb[bi], qrow, srow, zrow, g0c + bi * GB, gcl, kg, row_bytes);
+
+    // 3. Convert (the weights stay in flight).
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int c = tid + i * 64 * W;
-        reinterpret_cast<uint4*>(xs1)[c < nch ? c : nch - 1] = xc[i];
+    for (int t = 0; t < XP; t++) {
+        const int g = gbeg + 4 * t + kg;
+        if (gbeg + 4 * t >= gend) break;  // wave-uniform
+        const bool st = g < gend;
+        const int4 md = convert_group<KIND == 1>(xv[t], ln, st, xs1 + (st ? g : gbeg) * kLimbRec);
+        if (st && ln == 0) ms1[g] = md;
     }
-    ms1[mslot] = mreg;
     __syncthreads();
 
     // 3. Per batch: all activation operands, then all MFMAs, then the fp32
@@ -663,9 +681,53 @@ int env_int(const char* name, int dflt) {
     return v ? atoi(v) : dflt;
 }
 
-}  // namespace
+// MODE of the 1-row kernel (see load_batch): 16-byte paths need K % 128 == 0
+// and a 16-byte aligned activation row.
+int gemv1_mode(int64_t K, int64_t G, const float* x) {
+    if (K % kGroup || reinterpret_cast<uintptr_t>(x) % 16) return 0;
+    return G % 4 ? 1 : 2;
+}
 
-hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
+// Workgroup K-slices of the 1-row kernel: the smallest of 4, 8, 16 whose
+// slices fit 4 weight batches (measured on MI355X: 4 slices beat more,
+// smaller workgroups whenever they fit); 0 when the kernel does not apply
+// (the LDS copy of the converted row would exceed 96 KiB).
+int gemv1_slices(int64_t G, int kind, int mode) {
+    if (G * (kLimbRec + 16) > 96 * 1024) return 0;
+    const int gb1 = kind == 1 ? 8 : 4;  // groups per batch (8 KiB of weights per wave)
+    for (int ks : {4, 8, 16}) {
+        int gs = int((G + ks - 1) / ks);
+        if (mode == 2) gs = (gs + 3) / 4 * 4;
+        if (gs <= 4 * gb1) return ks;
+    }
+    return 0;
+}
+
+// The 1-row kernel on n <= kMaxMulti matrices of one kind and width: one grid,
+// matrix i owns the workgroups [tile0_i, tile0_i + ceil(N_i / 16)).
+hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n,
+                        int KS, int mode, hipStream_t stream) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    GemvParams p{};
+    int tiles = 0;
+    for (int i = 0; i < n; i++) {
+        p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i], W[i].rows, tiles};
+        tiles += int((W[i].rows + 15) / 16);
+    }
+    p.nmat = n;
+    p.K = K; p.G = G;
+    p.x = x;
+    p.M = 1;
+    p.gs = int((G + KS - 1) / KS);
+    if (mode == 2) p.gs = (p.gs + 3) / 4 * 4;  // 4-group aligned slices: vector scale loads
+    p.S = 1;
+    if (W[0].kind == 1) launch_gemv1_t<1, 8>(p, KS, mode, unsigned(tiles), stream);
+    else launch_gemv1_t<0, 4>(p, KS, mode, unsigned(tiles), stream);
+    return hipGetLastError();
+}
+
+// Byte limbs + meta of x [M][K] into the workspace.
+hipError_t launch_xprep_limbs(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
     const int64_t G = (K + kGroup - 1) / kGroup;
     const int64_t quads = (G + 3) / 4;
     const int64_t waves = int64_t(M) * quads;
@@ -678,15 +740,11 @@ hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* w
         if (vecx) xprep_kernel<false, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, ws->xq, ws->xmeta);
         else xprep_kernel<false, false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, ws->xq, ws->xmeta);
     }
-    ws->prep_M = M;
-    ws->prep_K = K;
-    ws->prep_kind = kind;
     return hipGetLastError();
 }
 
-namespace {
-
-// 2..32 rows (or a 1-row case the 1-row kernel does not cover), one matrix.
+// 2..32 rows (or a 1-row case the 1-row kernel does not cover), one matrix,
+// on the limbs prepared in the workspace.
 hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
                                hipStream_t stream) {
     const int64_t N = W.rows, K = W.cols, G = W.groups;
@@ -695,7 +753,7 @@ hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, floa
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros;
     p.N = N; p.K = K; p.G = G;
     p.xq = ws->xq; p.meta = ws->xmeta;
-    p.bias = bias; p.y = y; p.part = ws->partials; p.cnt = ws->counters;
+    p.bias = bias; p.y = y; p.part = ws->partials;
     p.M = M;
     const int gc = (kind == 1 && M <= 16) ? 8 : 4;  // groups per chunk (LDS: 2 * gc * M * 384 B max)
     static const int target = env_int("IQ_GEMV_WAVES", 2048);
@@ -724,46 +782,8 @@ hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, floa
     return hipGetLastError();
 }
 
-}  // namespace
-
-hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n,
-                                     int M, Workspace* ws, hipStream_t stream) {
-    const int64_t K = W[0].cols, G = W[0].groups;
-    const int kind = W[0].kind;
-    const int gb1 = kind == 1 ? 8 : 4;  // groups per batch of the 1-row kernel (8 KB per wave)
-    if (M == 1 && n <= kMaxMulti && G * (kLimbRec + 16) <= 96 * 1024) {
-        // Workgroup = one 16-row tile x KS K-slices.  KS: the smallest of
-        // 4, 8, 16 whose slices fit 4 batches and whose threads can stage the
-        // activation row (8 chunks of 16 B each).  Measured on MI355X: 4
-        // slices beat more, smaller workgroups whenever they fit.
-        static const int forced = env_int("IQ_GEMV1_KS", 0);
-        int KS = 0;
-        const int mode = K % kGroup ? 0 : (G % 4 ? 1 : 2);
-        for (int ks : {4, 8, 16}) {
-            int gs = int((G + ks - 1) / ks);
-            if (mode == 2) gs = (gs + 3) / 4 * 4;
-            if (gs <= 4 * gb1 && G * 24 <= 8 * 64 * ks && G <= 64 * ks) { KS = ks; break; }
-        }
-        if (forced && KS) KS = forced;
-        if (KS) {
-            GemvParams p{};
-            int tiles = 0;
-            for (int i = 0; i < n; i++) {
-                p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i], W[i].rows, tiles};
-                tiles += int((W[i].rows + 15) / 16);
-            }
-            p.nmat = n;
-            p.K = K; p.G = G;
-            p.xq = ws->xq; p.meta = ws->xmeta;
-            p.M = 1;
-            p.gs = int((G + KS - 1) / KS);
-            if (mode == 2) p.gs = (p.gs + 3) / 4 * 4;  // 4-group aligned slices: vector scale loads
-            p.S = 1;
-            if (kind == 1) launch_gemv1_t<1, 8>(p, KS, mode, unsigned(tiles), stream);
-            else launch_gemv1_t<0, 4>(p, KS, mode, unsigned(tiles), stream);
-            return hipGetLastError();
-        }
-    }
+hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
+                                Workspace* ws, hipStream_t stream) {
     for (int i = 0; i < n; i++) {
         const hipError_t e = launch_gemv_batched(W[i], bias[i], M, y[i], ws, stream);
         if (e != hipSuccess) return e;
@@ -771,16 +791,61 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
     return hipSuccess;
 }
 
+}  // namespace
+
+// A 1-row preparation that the 1-row kernel will consume is a copy of x
+// (the kernel converts it itself); anything else is converted to limbs.
+hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
+    const int64_t G = (K + kGroup - 1) / kGroup;
+    hipError_t e;
+    if (M == 1 && gemv1_slices(G, kind, gemv1_mode(K, G, ws->xf)) > 0) {
+        e = hipMemcpyAsync(ws->xf, x, sizeof(float) * size_t(K), hipMemcpyDeviceToDevice, stream);
+        ws->prep_copy = true;
+    } else {
+        e = launch_xprep_limbs(x, M, K, kind, ws, stream);
+        ws->prep_copy = false;
+    }
+    ws->prep_M = M;
+    ws->prep_K = K;
+    ws->prep_kind = kind;
+    return e;
+}
+
+hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n,
+                                     int M, Workspace* ws, hipStream_t stream) {
+    if (ws->prep_copy) {
+        const int64_t K = W[0].cols, G = W[0].groups;
+        const int mode = gemv1_mode(K, G, ws->xf);
+        return launch_gemv1(ws->xf, W, bias, y, n, gemv1_slices(G, W[0].kind, mode), mode, stream);
+    }
+    return launch_batched_multi(W, bias, y, n, M, ws, stream);
+}
+
 hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, float* y, Workspace* ws,
                                hipStream_t stream) {
     return launch_gemv_prepped_multi(&W, &bias, &y, 1, M, ws, stream);
 }
 
+hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
+                             int n, int M, Workspace* ws, hipStream_t stream) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    if (M == 1) {
+        const int mode = gemv1_mode(K, G, x);
+        const int KS = gemv1_slices(G, W[0].kind, mode);
+        if (KS > 0) return launch_gemv1(x, W, bias, y, n, KS, mode, stream);
+    }
+    hipError_t e = launch_xprep_limbs(x, M, K, W[0].kind, ws, stream);
+    ws->prep_copy = false;
+    ws->prep_M = M;
+    ws->prep_K = K;
+    ws->prep_kind = W[0].kind;
+    if (e != hipSuccess) return e;
+    return launch_batched_multi(W, bias, y, n, M, ws, stream);
+}
+
 hipError_t launch_gemv(const float* x, const QView& W, const uint16_t* bias, int M, float* y,
                        Workspace* ws, hipStream_t stream) {
-    hipError_t e = launch_xprep(x, M, W.cols, W.kind, ws, stream);
-    if (e != hipSuccess) return e;
-    return launch_gemv_prepped(W, bias, M, y, ws, stream);
+    return launch_gemv_multi(x, &W, &bias, &y, 1, M, ws, stream);
 }
 
 }  // namespace iq

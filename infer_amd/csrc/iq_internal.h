@@ -19,13 +19,13 @@ struct QView {
     const uint8_t* zeros;
 };
 
-// Per-device scratch used by the GEMV: the activations as byte limbs with
-// their per-(group, row) exponent and limb sums, split-K partial sums and
-// split-K arrival counters.
+// Per-device scratch used by the GEMV: a copy of a prepared 1-row
+// activation, the activations as byte limbs with their per-(group, row)
+// exponent and limb sums, and split-K partial sums.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
-    int* counters = nullptr;   // kMaxCounters ints, zero between launches
+    float* xf = nullptr;       // [kMaxKp] fp32: 1-row activation copied by a prep
     int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs
     int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {k, sum X0, sum X1, sum X2}
     float* partials = nullptr; // kPartialFloats
@@ -33,11 +33,11 @@ struct Workspace {
     int prep_M = 0;
     int64_t prep_K = 0;
     int prep_kind = -1;
+    bool prep_copy = false;   // the preparation is a copy of x in xf (1 row)
 };
 
 constexpr int kMaxRowsGemv = 32;            // GpuBatch::kMaxRows (kernels/batch_gpu.h:80)
 constexpr int64_t kMaxKp = 131072;          // padded K limit of the GEMV
-constexpr int64_t kMaxCounters = 65536;
 constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K partials
 
 // Returns the workspace of the current device, allocating it on first use.
@@ -56,6 +56,11 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 // (n <= 4): one launch for 1 row, one launch per matrix otherwise.
 hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n,
                                      int M, Workspace* ws, hipStream_t stream);
+// Several matrices of one kind and width on the activations x [M][K]
+// (n <= 4): the 1-row kernel reads x itself (one launch for all n); other
+// shapes prepare x once into the workspace, then one launch per matrix.
+hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
+                             int n, int M, Workspace* ws, hipStream_t stream);
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
                        const uint16_t* bias, int64_t T, float* y, hipStream_t stream);
 

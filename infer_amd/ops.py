@@ -51,6 +51,7 @@ SIGNATURES = {
     "iq_gemv_prep": ([_P, ctypes.c_int, _I64, ctypes.c_int, _P], ctypes.c_int),
     "iq_gemv_prepped": ([_VP, _P, ctypes.c_int, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_gemv_prepped_multi": ([_P, ctypes.c_int, _P, ctypes.c_int, _I64, _P, _P], ctypes.c_int),
+    "iq_gemv_multi": ([_P, _P, ctypes.c_int, _P, ctypes.c_int, _I64, _P, _P], ctypes.c_int),
     "iq_gemm": ([_P, _VP, _P, _I64, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_gemm_bf16x": ([_P, _VP, _P, _I64, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_linear": ([_P, _VP, _P, _I64, _I64, _I64, _P, _P], ctypes.c_int),
@@ -215,6 +216,17 @@ def gemv_prepped_multi(Ws, biases, B, in_, ys, stream=None):
     yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
     rc = lib().iq_gemv_prepped_multi(views, n, bs, int(B), int(in_), yp, _stream(stream))
     _check(rc, "iq_gemv_prepped_multi")
+
+
+def gemv_multi(x, Ws, biases, B, in_, ys, stream=None):
+    """Several matrices (same kind and width) sharing the activations
+    x [B, in]: ys[i] = x @ dequant(Ws[i])^T (+ biases[i]); one launch at B = 1."""
+    n = len(Ws)
+    views = (ctypes.c_void_p * n)(*[ctypes.addressof(W._c) for W in Ws])
+    bs = (ctypes.c_void_p * n)(*[(b.data_ptr() if b is not None else None) for b in (biases or [None] * n)])
+    yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    rc = lib().iq_gemv_multi(_ptr(x), views, n, bs, int(B), int(in_), yp, _stream(stream))
+    _check(rc, "iq_gemv_multi")
 
 
 def launch_gemm_tiled_q(x, W, bias, T, in_, out, y, stream=None):

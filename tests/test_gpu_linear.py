@@ -138,3 +138,82 @@ def test_gemv_multi_matches_oracle(kind, M):
     torch.cuda.synchronize()
     for i, (W, y) in enumerate(zip(Ws, ys)):
         check_linear(y, x, W, bb if i == 1 else None, M, f"multi[{i}] kind={kind} M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_multi_direct(kind, M):
+    """iq_gemv_multi: q|k|v at 1.5B and gate|up at 7B width, one call each."""
+    rng = np.random.default_rng(131 + kind + M)
+    for K, Ns in ((1536, (1536, 256, 256)), (3584, (18944, 18944))):
+        Ws = [QFix(rng, N, K, kind, sd=0.02) for N in Ns]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        bb, bd = bias_of(rng, Ns[-1])
+        ys = [out_buffer(M, W.rows) for W in Ws]
+        say("gemv multi direct", kind, M, K, Ns)
+        biases = [None] * (len(Ws) - 1) + [bd]
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], biases, M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y) in enumerate(zip(Ws, ys)):
+            check_linear(y, x, W, bb if i == len(Ws) - 1 else None, M, f"multi direct[{i}] kind={kind} M={M} K={K}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemv_unaligned_activation_row(kind):
+    """1 row whose fp32 activations start 4 bytes past a 16-byte boundary."""
+    rng = np.random.default_rng(61 + kind)
+    N, K = 1000, 1536
+    W = QFix(rng, N, K, kind, sd=0.02)
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    buf = torch.zeros(K + 4, device="cuda")
+    buf[1:K + 1] = torch.from_numpy(x[0]).cuda()
+    xv = buf[1:K + 1]
+    assert xv.data_ptr() % 16 == 4
+    y = out_buffer(1, N)
+    say("gemv unaligned x", kind)
+    ops.launch_gemv_batched_q(xv, W.view, None, 1, K, N, y)
+    torch.cuda.synchronize()
+    check_linear(y, x, W, None, 1, f"unaligned x kind={kind}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemv_prep_keeps_its_input(kind):
+    """A 1-row preparation holds the activations of the time of the call:
+    overwriting x afterwards does not change what gemv_prepped computes."""
+    rng = np.random.default_rng(71 + kind)
+    N, K = 512, 3584
+    W = QFix(rng, N, K, kind, sd=0.02)
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    xd = torch.from_numpy(x).cuda()
+    ops.gemv_prep(xd, 1, K, kind)
+    xd.fill_(1e30)
+    y = out_buffer(1, N)
+    say("gemv prep snapshot", kind)
+    ops.gemv_prepped(W.view, None, 1, K, N, y)
+    torch.cuda.synchronize()
+    check_linear(y, x, W, None, 1, f"prep snapshot kind={kind}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_nonfinite_activation(kind, M):
+    """An inf / NaN activation makes every output of its row non-finite (as
+    the reference's fp32 sum does); the other rows stay exact."""
+    rng = np.random.default_rng(81 + kind + M)
+    N, K = 256, 1536
+    W = QFix(rng, N, K, kind, sd=0.02)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[0, 300] = np.inf
+    if M > 1:
+        x[1, 5] = np.nan
+    y = out_buffer(M, N)
+    say("gemv nonfinite", kind, M)
+    ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()[: M * N].reshape(M, N)
+    bad = 2 if M > 1 else 1
+    assert not np.any(np.isfinite(got[:bad]))
+    if M > bad:
+        ref, cond = O.linear_dq_f64(x[bad:], W.dq, None)
+        err = np.abs(got[bad:].astype(np.float64) - ref)
+        assert float((err / np.maximum(cond, 1e-30)).max()) <= 5e-6
