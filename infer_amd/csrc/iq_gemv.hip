@@ -74,7 +74,9 @@ __host__ __device__ constexpr int limb_pos(int c, bool perm) {
 // Rotation of a value inside its 16-lane DPP row (row_ror:N).
 template <int N>
 __device__ __forceinline__ int row_ror(int v) {
-    return __builtin_amdgcn_mov_dpp(v, 0x120 + N, 0xF, 0xF, false);
+    // bound_ctrl set: lets the compiler fold the move into the consumer
+    // (v_add/v_max with a DPP operand); row_ror reads only valid lanes.
+    return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xF, 0xF, true);
 }
 // All-reduce over the 16 lanes of a DPP row (4 rotations, no LDS traffic).
 __device__ __forceinline__ int row16_sum(int v) {
@@ -99,83 +101,110 @@ __device__ __forceinline__ int row16_and(int v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t row16_or(uint32_t v) {
+    v |= uint32_t(row_ror<8>(int(v)));
+    v |= uint32_t(row_ror<4>(int(v)));
+    v |= uint32_t(row_ror<2>(int(v)));
+    v |= uint32_t(row_ror<1>(int(v)));
+    return v;
+}
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    v = max(v, uint32_t(row_ror<8>(int(v))));
+    v = max(v, uint32_t(row_ror<4>(int(v))));
+    v = max(v, uint32_t(row_ror<2>(int(v))));
+    v = max(v, uint32_t(row_ror<1>(int(v))));
+    return v;
+}
+
+// Three limb words (records 0, 1, 2 = X0, X1, X2) of the four values whose
+// biased integers U = X + 0x808080 are u0..u3, in that byte order: limb L of
+// a value is byte 2-L of U minus 128, i.e. that byte with its top bit flipped.
+__device__ __forceinline__ void pack_limbs(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t u3, uint32_t (&w)[3]) {
+    const uint32_t p = __builtin_amdgcn_perm(u1, u0, 0x05010400u);   // u0.b0 u1.b0 u0.b1 u1.b1
+    const uint32_t q = __builtin_amdgcn_perm(u3, u2, 0x05010400u);   // u2.b0 u3.b0 u2.b1 u3.b1
+    const uint32_t p2 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 ..
+    const uint32_t q2 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);  // u2.b2 u3.b2 ..
+    w[0] = __builtin_amdgcn_perm(q2, p2, 0x05040100u) ^ 0x80808080u;
+    w[1] = __builtin_amdgcn_perm(q, p, 0x07060302u) ^ 0x80808080u;
+    w[2] = __builtin_amdgcn_perm(q, p, 0x05040100u) ^ 0x80808080u;
+}
+
 // Converts one (activation row, 128-column group) whose columns 8j..8j+7
 // are v[] of the lane with j = lane % 16 (the 16 lanes of a DPP row hold the
 // whole group; all 16 must call this together).  Writes this lane's limb
 // bytes into the group's record `rec` (when `store`) and returns the group's
 // meta record {2^-k as fp32 bits, sum X0, sum X1, sum X2} (every lane).
+//
+// X = rint(x * 2^k) is formed as the bits of fma(x, 2^k, 1.5 * 2^23): with
+// |x * 2^k| <= 2^22 the sum lies in [2^23, 2^24], where the float's bits
+// minus those of 1.5 * 2^23 are X, rounded to nearest even by the fma.
+// Adding 0x808080 makes each byte of the 24-bit result its limb + 128
+// (balanced limbs in [-128, 127]).
 template <bool PERM>
 __device__ __forceinline__ int4 convert_group(const float (&v)[8], int j, bool store, int8_t* rec) {
-    // absmax; NaN must not be lost (fmaxf drops it), so track finiteness apart.
-    float amax = 0.0f;
-    int fin = 1;
+    float am = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float a = __builtin_fabsf(v[i]);
-        fin &= int(a <= 3.402823466e38f);
-        amax = fmaxf(amax, a);
-    }
-    amax = row16_max(amax);
-    fin = row16_and(fin);
+    for (int i = 0; i < 8; i++) am = fmaxf(am, __builtin_fabsf(v[i]));  // NaN ignored here
+    const uint32_t mb = row16_max_u32(__float_as_uint(am));
     // amax = f * 2^E, f in [0.5, 1): k = 22 - E puts amax * 2^k in [2^21, 2^22)
-    const int k = (fin && amax > 0.0f) ? 22 - __builtin_amdgcn_frexp_expf(amax) : 0;
-    int X[8];
+    const int k0 = mb < 0x7F800000u ? 22 - __builtin_amdgcn_frexp_expf(__uint_as_float(mb)) : 0;
+    int k = k0;
+    float xv[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) X[i] = fin ? int(__builtin_rintf(__builtin_amdgcn_ldexpf(v[i], k))) : 0;
-    // balanced byte limbs: X = 2^16 x0 + 2^8 x1 + x2, each in [-128, 127]
-    int l0[8], l1[8], l2[8];
-    int s0 = 0, s1 = 0, s2 = 0;
+    for (int i = 0; i < 8; i++) xv[i] = v[i];
+    if (k > 126) {
+        // amax below 2^-104: scale up exactly first so that 2^k stays a float
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = __builtin_amdgcn_ldexpf(xv[i], k - 126);
+        k = 126;
+    }
+    const float p2k = __uint_as_float(uint32_t(k + 127) << 23);
+    uint32_t u[8], hi = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int a2 = int(int8_t(X[i] & 0xFF));
-        const int r1 = (X[i] - a2) >> 8;
-        const int a1 = int(int8_t(r1 & 0xFF));
-        const int a0 = (r1 - a1) >> 8;
-        l0[i] = a0; l1[i] = a1; l2[i] = a2;
-        s0 += a0; s1 += a1; s2 += a2;
+        u[i] = __float_as_uint(__builtin_fmaf(xv[i], p2k, 12582912.0f)) + (0x808080u - 0x4B400000u);
+        hi |= u[i];
     }
-    s0 = row16_sum(s0);
-    s1 = row16_sum(s1);
-    s2 = row16_sum(s2);
+    // A finite group leaves byte 3 of every U zero; NaN / inf (either from
+    // the input or, for a group whose amax is inf, from the scaling) do not.
+    const bool fin = row16_or(hi >> 24) == 0;
+    uint32_t a[3], b[3];
+    if (PERM) {
+        // columns 8j..8j+7: evens -> one word per limb, odds -> one word per limb
+        pack_limbs(u[0], u[2], u[4], u[6], a);
+        pack_limbs(u[1], u[3], u[5], u[7], b);
+    } else {
+        pack_limbs(u[0], u[1], u[2], u[3], a);
+        pack_limbs(u[4], u[5], u[6], u[7], b);
+    }
+    int sl[3];
+#pragma unroll
+    for (int L = 0; L < 3; L++)
+        sl[L] = row16_sum(__builtin_amdgcn_sdot4(int(a[L]), 0x01010101, __builtin_amdgcn_sdot4(int(b[L]), 0x01010101, 0, false), false));
     if (store) {
-        const int* L[3] = {l0, l1, l2};
         if (PERM) {
-            // columns 8j..8j+7: evens -> 4 contiguous bytes, odds -> 4 contiguous bytes
             const int pe = limb_pos(j * 8, true), po = limb_pos(j * 8 + 1, true);
 #pragma unroll
-            for (int li = 0; li < 3; li++) {
-                uint32_t ev = 0, od = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    ev |= uint32_t(uint8_t(L[li][2 * e])) << (8 * e);
-                    od |= uint32_t(uint8_t(L[li][2 * e + 1])) << (8 * e);
-                }
-                *reinterpret_cast<uint32_t*>(rec + li * kGroup + pe) = ev;
-                *reinterpret_cast<uint32_t*>(rec + li * kGroup + po) = od;
+            for (int L = 0; L < 3; L++) {
+                *reinterpret_cast<uint32_t*>(rec + L * kGroup + pe) = a[L];
+                *reinterpret_cast<uint32_t*>(rec + L * kGroup + po) = b[L];
             }
         } else {
 #pragma unroll
-            for (int li = 0; li < 3; li++) {
-                uint32_t lo = 0, hi = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    lo |= uint32_t(uint8_t(L[li][e])) << (8 * e);
-                    hi |= uint32_t(uint8_t(L[li][e + 4])) << (8 * e);
-                }
-                *reinterpret_cast<uint2*>(rec + li * kGroup + j * 8) = make_uint2(lo, hi);
-            }
+            for (int L = 0; L < 3; L++) *reinterpret_cast<uint2*>(rec + L * kGroup + j * 8) = make_uint2(a[L], b[L]);
         }
     }
-    // 2^-k (NaN when the group holds a non-finite value, so it propagates);
-    // a group of values below ~2^-149 * 2^22 contributes 0.
-    const float fx = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
-    return make_int4(__float_as_int(fx), s0, s1, s2);
+    // 2^-k (NaN when the group holds a non-finite value, so it propagates)
+    const float fx = fin ? __builtin_amdgcn_ldexpf(1.0f, -k0) : __builtin_nanf("");
+    return make_int4(__float_as_int(fx), sl[0], sl[1], sl[2]);
 }
 
-// Columns [c0, c0 + 8) of an activation row, zero past K.
-template <bool VECX>
+// Columns [c0, c0 + 8) of an activation row, zero past K.  VECX: 0 scalar
+// loads; 1 two 16-byte loads where the 8 columns lie inside K; 2 two 16-byte
+// loads, the caller guarantees c0 + 8 <= K.
+template <int VECX>
 __device__ __forceinline__ void load_x8(const float* xr, int64_t c0, int64_t K, float (&v)[8]) {
-    if (VECX && c0 + 8 <= K) {
+    if (VECX == 2 || (VECX == 1 && c0 + 8 <= K)) {
         const float4 a = *reinterpret_cast<const float4*>(xr + c0);
         const float4 b = *reinterpret_cast<const float4*>(xr + c0 + 4);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
@@ -200,7 +229,7 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
     const bool gvalid = g < G;
     const int j = lane & 15;
     float v[8];
-    load_x8<VECX>(x + int64_t(m) * K, (gvalid ? g : 0) * kGroup + j * 8, gvalid ? K : 0, v);
+    load_x8<VECX ? 1 : 0>(x + int64_t(m) * K, (gvalid ? g : 0) * kGroup + j * 8, gvalid ? K : 0, v);
     const int4 md = convert_group<PERM>(v, j, gvalid, xq + (int64_t(m) * G + (gvalid ? g : 0)) * kLimbRec);
     if (gvalid && j == 0) meta[g * kMeta + m] = md;
 }
@@ -234,6 +263,7 @@ struct GemvParams {
     float* y;
     float* part;
     int M, S, gs, nrb;
+    int ntiles;  // 1-row kernel: 16-row tiles over all matrices
 };
 
 // 16 bytes of a row at byte offset `off`, zero past `row_bytes` (unaligned
@@ -273,179 +303,245 @@ __device__ __forceinline__ float combine(float acc, int d0, int d1, int d2, int 
 }
 
 // ------------------------------------------------------------------ 1 row
-// Weight words + scales + zero points of one batch of GB groups of a lane.
-template <int KIND, int GB>
-struct WBatch {
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOob = 0x80000000u;  // added to a buffer offset: reads zero, no memory access
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+
+// Weight words, scales and zero points of one wave's K slice of one tile.
+template <int KIND, int NG>
+struct Slice {
     static constexpr int WPG = KIND == 1 ? 1 : 2;
-    uint4 w[GB][WPG];
-    uint2 s[GB / 4];     // 4 bf16 scales per entry
-    uint32_t z[GB / 4];  // 4 zero points per entry (int4)
+    int4v_t w[NG][WPG];
+    uint32_t s[NG / 2];  // bf16 scales, two per word (group 2i in the low half)
+    uint32_t z[NG / 4];  // int4 zero points, four per word (group 4i in the low byte)
 };
 
-// Loads batch [g0, g0 + GB) of one lane (columns of the lane's quarter of
-// each group); groups at or past `gend` re-load group gend-1 (the compute
-// skips them), so every load is unconditional and stays in bounds.
-// MODE 0: unaligned rows (byte loads); 1: 16-byte weight loads, one scale /
-// zero load per group; 2: also one 8-byte scale and one 4-byte zero-point
+// One tile's matrix, resolved from the tile index (wave-uniform).
+struct TileSel {
+    MatRef m;
+    int64_t row0;
+};
+
+__device__ __forceinline__ TileSel select_tile(const GemvParams& p, int tile) {
+    MatRef m = p.mat[0];
+#pragma unroll
+    for (int i = 1; i < kMaxMulti; i++)
+        if (i < p.nmat && tile >= p.mat[i].tile0) m = p.mat[i];
+    return TileSel{m, int64_t(tile - m.tile0) * 16};
+}
+
+// Issues the loads of one wave's slice [gbeg, gbeg + gs) of tile `tile`
+// (lane: row row0 + ln, 16-byte column block kg of each 64-byte half group).
+// Past the last tile, past N or past the slice the loads read zero without
+// touching memory (buffer range check), so every load is unconditional.
+// MODE 0: rows not 16-byte aligned (byte loads, clamped); 1: one scale /
+// zero-point load per group; 2: one 8-byte scale and one 4-byte zero-point
 // load per 4 groups (G % 4 == 0, slices of whole 4-group blocks).
-template <int KIND, int GB, int MODE>
-__device__ __forceinline__ void load_batch(WBatch<KIND, GB>& b, const uint8_t* qrow, const uint16_t* srow,
-                                           const uint8_t* zrow, int g0, int gend, int kg,
-                                           int row_bytes) {
-    constexpr int WPG = WBatch<KIND, GB>::WPG;
+template <int KIND, int NG, int MODE>
+__device__ __forceinline__ void load_slice(Slice<KIND, NG>& b, const GemvParams& p, int tile, int gbeg, int gs,
+                                           int ln, int kg) {
+    constexpr int WPG = Slice<KIND, NG>::WPG;
+    const int G = int(p.G);
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const TileSel ts = select_tile(p, tile < p.ntiles ? tile : p.ntiles - 1);
+    const MatRef& mr = ts.m;
+    const int64_t row = ts.row0 + ln;
+    const uint32_t dead = tile < p.ntiles ? 0u : kOob;  // prefetch past the end
+    if (MODE == 0) {
+        const int64_t rc = row < mr.N ? row : mr.N - 1;
+        const uint8_t* qrow = mr.q + rc * row_bytes;
 #pragma unroll
-    for (int gl = 0; gl < GB; gl++) {
-        const int g = g0 + gl < gend ? g0 + gl : gend - 1;
+        for (int gl = 0; gl < NG; gl++) {
+            const int g = gbeg + (gl < gs ? gl : gs - 1);
 #pragma unroll
-        for (int h = 0; h < WPG; h++) {
-            const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
-            b.w[gl][h] = MODE >= 1 ? *reinterpret_cast<const uint4*>(qrow + off) : load16_slow(qrow, off, row_bytes);
+            for (int h = 0; h < WPG; h++) {
+                const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
+                const uint4 v = load16_slow(qrow, off, row_bytes);
+                b.w[gl][h] = int4v_t{int(v.x), int(v.y), int(v.z), int(v.w)};
+            }
+        }
+    } else {
+        const rsrc_t rq = make_rsrc(mr.q, mr.N * row_bytes);
+        const uint32_t vq = uint32_t(row * row_bytes) + uint32_t(gbeg * (KIND == 1 ? 64 : 128) + kg * 16) + dead;
+#pragma unroll
+        for (int gl = 0; gl < NG; gl++) {
+            const uint32_t vo = vq + (gl < gs ? 0u : kOob);
+#pragma unroll
+            for (int h = 0; h < WPG; h++)
+                b.w[gl][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rq, vo, KIND == 1 ? gl * 64 : gl * 128 + h * 64, 0));
         }
     }
+    const rsrc_t rs = make_rsrc(mr.scales, mr.N * G * 2);
+    const rsrc_t rz = make_rsrc(mr.zeros, KIND == 1 ? mr.N * G : 0);
+    const int64_t rcs = MODE == 0 ? (row < mr.N ? row : mr.N - 1) : row;
+    const uint32_t vs = uint32_t((rcs * G + gbeg) * 2) + dead;
+    const uint32_t vz = uint32_t(rcs * G + gbeg) + dead;
+    if (MODE == 2) {
 #pragma unroll
-    for (int q4 = 0; q4 < GB / 4; q4++) {
-        if (MODE == 2) {
-            // gend is a multiple of 4 here (G % 4 == 0 and gs % 4 == 0)
-            const int g = g0 + 4 * q4 < gend ? g0 + 4 * q4 : gend - 4;
-            b.s[q4] = *reinterpret_cast<const uint2*>(srow + g);
-            b.z[q4] = KIND == 1 ? *reinterpret_cast<const uint32_t*>(zrow + g) : 0u;
-        } else {
-            uint32_t s4[4], z4 = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int g = g0 + 4 * q4 + e < gend ? g0 + 4 * q4 + e : gend - 1;
-                s4[e] = srow[g];
-                if (KIND == 1) z4 |= uint32_t(zrow[g]) << (8 * e);
-            }
-            b.s[q4] = make_uint2(s4[0] | (s4[1] << 16), s4[2] | (s4[3] << 16));
-            b.z[q4] = z4;
+        for (int q4 = 0; q4 < NG / 4; q4++) {
+            const uint32_t ok = 4 * q4 < gs ? 0u : kOob;
+            const auto sv = __builtin_amdgcn_raw_buffer_load_b64(rs, vs + ok, q4 * 8, 0);
+            b.s[2 * q4] = sv[0];
+            b.s[2 * q4 + 1] = sv[1];
+            b.z[q4] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b32(rz, vz + ok, q4 * 4, 0) : 0u;
         }
+    } else {
+        uint32_t sh[NG], zb[NG];
+#pragma unroll
+        for (int gl = 0; gl < NG; gl++) {
+            const uint32_t ok = gl < gs ? 0u : kOob;
+            sh[gl] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + ok, gl * 2, 0);
+            zb[gl] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + ok, gl, 0) : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < NG / 2; i++) b.s[i] = sh[2 * i] | (sh[2 * i + 1] << 16);
+#pragma unroll
+        for (int i = 0; i < NG / 4; i++)
+            b.z[i] = zb[4 * i] | (zb[4 * i + 1] << 8) | (zb[4 * i + 2] << 16) | (zb[4 * i + 3] << 24);
     }
 }
 
-// One activation row (the decode step).  Workgroup = TW x KS waves: TW tiles
-// of 16 output rows, each tile's K split into KS slices (wave = one tile,
-// one slice of gs <= NB*GB groups).  Every weight word, scale and zero point
-// of a wave's slice is requested at kernel start (NB batches of GB groups,
-// all loads unconditional - clamped into the slice - so nothing waits before
-// the last one is issued).  The fp32 activations of the wave's slice are
-// requested before the weights, and converted to byte limbs (as xprep does)
-// into the workgroup's LDS copy of the row while the weight words are in
-// flight: no separate conversion launch.  With KS > 1 the slice partials of
-// a tile are added through LDS in slice order (deterministic): no
-// cross-workgroup traffic, no device-scope fence.  The A operand carries the
-// activation's three byte limbs as rows 0..2 of the 16-row MFMA tile (lanes
-// l%16 = 0, 1, 2; the other lanes read a zero block, no branches), so two
-// MFMAs per 128 columns yield all three exact limb sums, in D rows 0..2 of
-// lanes 0..15.  MODE: see load_batch (MODE >= 1 also means K % 128 == 0 and
-// a 16-byte aligned activation row).
-template <int KIND, int TW, int KS, int GB, int NB, int MODE>
-__global__ __launch_bounds__(64 * TW * KS) void gemv1_kernel(const GemvParams p) {
-    constexpr int W = TW * KS;
-    constexpr int XP = NB * GB / 4;  // conversion passes of 4 groups per wave
+// Multiplies one tile's slice by the staged activation limbs: the A operand
+// carries the three limbs as rows 0..2 of the 16-row MFMA tile (lanes
+// l%16 = 0, 1, 2; the other lanes read a zero block), so two MFMAs per 128
+// columns give all three exact limb sums, in D rows 0..2 of lanes 0..15.
+template <int KIND, int NG>
+__device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_t* xs, const int4* ms,
+                                           const int8_t* xzero, int gbeg, int gs, int ln, int kg) {
+    float acc = 0.0f;
+    // blocks of 4 groups: an early exit over at most 8 iterations still
+    // unrolls fully (so the slice stays in registers)
+#pragma unroll
+    for (int q4 = 0; q4 < NG / 4; q4++) {
+        if (4 * q4 >= gs) break;  // wave-uniform
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int gl = 4 * q4 + e;
+            const bool ok = gl < gs;
+            const int g = gbeg + (ok ? gl : 0);
+            int4v_t a0, a1, b0, b1;
+            {
+                const int8_t* pa = ln < 3 ? xs + g * kLimbRec + ln * kGroup + kg * 16 : xzero;
+                a0 = *reinterpret_cast<const int4v_t*>(pa);
+                a1 = *reinterpret_cast<const int4v_t*>(pa + (ln < 3 ? 64 : 0));
+            }
+            if (KIND == 1) {
+                const int4v_t v = b.w[gl][0];
+                b0 = v & 0x0F0F0F0F;
+                b1 = (v >> 4) & 0x0F0F0F0F;
+            } else {
+                b0 = b.w[gl][0];
+                b1 = b.w[gl][1];
+            }
+            int4v_t D = mfma_i8(a0, b0, int4v_t{0, 0, 0, 0});
+            D = mfma_i8(a1, b1, D);
+            const uint32_t sw = b.s[gl / 2];
+            const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+            const int z = KIND == 1 ? int((b.z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
+            const float nacc = combine(acc, D[0], D[1], D[2], z, ms[g], sc);
+            acc = ok ? nacc : acc;
+        }
+    }
+    return acc;
+}
+
+// One activation row (the decode step).  Workgroup = KS waves (runtime,
+// blockDim.x / 64) on one 16-row tile at a time, wave w owning the K slice
+// [w*gs, w*gs + gs) of every tile; the workgroups walk the tiles of all
+// matrices of the launch in strides of gridDim.x (persistent).  At start each
+// wave converts its slice of the fp32 activations into byte limbs in LDS
+// (once per workgroup, while the first tile's weights are in flight).  Per
+// tile the next tile's slice is requested before the current one is
+// multiplied (two register buffers), and the KS slice partials are added
+// through LDS in slice order (deterministic; no cross-workgroup traffic).
+template <int KIND, int NG, int MODE, int TPW, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];  // limbs [G][384], meta [G]
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
-    __shared__ float red[W][16];
+    __shared__ float red[TPW][MAXW][16];
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
-    static_assert(TW == 1, "one tile per workgroup");
-    const int ksl = wave;
+    const int KS = int(blockDim.x) >> 6;
     const int G = int(p.G);
-    int mi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxMulti; i++)
-        if (i < p.nmat && int(blockIdx.x) >= p.mat[i].tile0) mi = i;
-    const MatRef& mr = p.mat[mi];
-    const int64_t row = (int64_t(blockIdx.x) - mr.tile0) * 16 + ln;
-    const int64_t rc = row < mr.N ? row : mr.N - 1;
-    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
-    const uint8_t* qrow = mr.q + rc * row_bytes;
-    const uint16_t* srow = mr.scales + rc * G;
-    const uint8_t* zrow = KIND == 1 ? mr.zeros + rc * G : nullptr;
-    const int gbeg = ksl * p.gs < G ? ksl * p.gs : G;
-    const int gend = gbeg + p.gs < G ? gbeg + p.gs : G;
-    const bool active = gend > gbeg;
-    // Clamp bound for idle waves (their loads re-read groups 0..3, in bounds;
-    // the 4-group scale loads need a bound of at least 4).
-    const int g0c = active ? gbeg : 0;
-    const int gcl = active ? gend : (MODE == 2 ? 4 : 1);
+    const int gbeg = wave * p.gs < G ? wave * p.gs : G;
+    const int gs = (gbeg + p.gs < G ? gbeg + p.gs : G) - gbeg;
     int4* ms1 = reinterpret_cast<int4*>(xs1 + G * kLimbRec);
+    auto tile_of = [&](int i) { return int(blockIdx.x) + i * int(gridDim.x); };
 
-    // 1. The slice's activations: pass t converts groups gbeg + 4t + kg,
-    //    16 lanes (one DPP row) per group, 8 columns per lane.  Loads are
-    //    clamped to the slice (idle waves: group 0), stores are masked.
+    // 1. This wave's activations: pass t converts groups gbeg + 4t + kg,
+    //    16 lanes (one DPP row) per group, 8 columns per lane.  Every wave
+    //    requests them before any wave requests weights: the vector L1
+    //    returns data in request order, so activations asked for behind the
+    //    CU's weight misses would arrive only after them.
+    constexpr int XP = NG / 4;
     float xv[XP][8];
 #pragma unroll
     for (int t = 0; t < XP; t++) {
-        const int g = g0c + 4 * t + kg < gcl ? g0c + 4 * t + kg : gcl - 1;
-        load_x8<MODE >= 1>(p.x, int64_t(g) * kGroup + ln * 8, p.K, xv[t]);
+        const int g = 4 * t + kg < gs ? gbeg + 4 * t + kg : (gs > 0 ? gbeg + gs - 1 : 0);
+        load_x8<MODE >= 1 ? 2 : 0>(p.x, int64_t(g) * kGroup + ln * 8, p.K, xv[t]);
+    }
+    // The bias of the rows this lane may store (wave 0, lanes 0..15), bf16.
+    uint32_t bias[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; i++) {
+        const int t = tile_of(i);
+        const TileSel ts = select_tile(p, t < p.ntiles ? t : p.ntiles - 1);
+        const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
+        const bool mine = wave == 0 && lane < 16 && t < p.ntiles;
+        bias[i] = __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(ts.row0 + ln) * 2 : kOob, 0, 0);
     }
     if (tid < 4) reinterpret_cast<uint32_t*>(xzero)[tid] = 0u;
+    __syncthreads();
 
-    // 2. All weight batches of the slice.
-    WBatch<KIND, GB> wb[NB];
+    // 2. The first PD tiles' slices in flight (tiles past the end read zero
+    //    without touching memory), then the conversion while they stream in.
+    //    A wave stalls while the CU's memory queues are full, so it keeps
+    //    only PD tiles ahead and multiplies in between.
+    constexpr int PD = TPW < 2 ? TPW : 2;
+    Slice<KIND, NG> b[TPW];
 #pragma unroll
-    for (int bi = 0; bi < NB; bi++) load_batch<KIND, GB, MODE>(wb[bi], qrow, srow, zrow, g0c + bi * GB, gcl, kg, row_bytes);
-
-    // 3. Convert (the weights stay in flight).
+    for (int i = 0; i < PD; i++) load_slice<KIND, NG, MODE>(b[i], p, tile_of(i), gbeg, gs, ln, kg);
 #pragma unroll
     for (int t = 0; t < XP; t++) {
+        if (4 * t >= gs) break;  // wave-uniform
         const int g = gbeg + 4 * t + kg;
-        if (gbeg + 4 * t >= gend) break;  // wave-uniform
-        const bool st = g < gend;
+        const bool st = 4 * t + kg < gs;
         const int4 md = convert_group<KIND == 1>(xv[t], ln, st, xs1 + (st ? g : gbeg) * kLimbRec);
         if (st && ln == 0) ms1[g] = md;
     }
-    __syncthreads();
+    // (each wave reads only its own limb records; the zero block is shared)
 
-    // 3. Per batch: all activation operands, then all MFMAs, then the fp32
-    //    combination (independent chains, so LDS / MFMA latencies overlap).
-    float acc = 0.0f;
+    // 3. Tiles in order, each as its slice lands, then the request for the
+    //    tile PD ahead.  Slice partials are added through LDS in slice order
+    //    (rows k >= KS were never written and are discarded); all stores
+    //    come after the last load has been used.
+    float yv[TPW];
 #pragma unroll
-    for (int bi = 0; bi < NB; bi++) {
-        // A operand rows 0, 1, 2 = the activation's three limbs (lanes with
-        // l%16 = L), rows 3..15 zero: one MFMA per 64 columns gives all three
-        // exact limb sums, in D rows 0..2 of lanes 0..15.
-        int4v_t a[GB][2];
-#pragma unroll
-        for (int gl = 0; gl < GB; gl++) {
-            const int g = gbeg + bi * GB + gl < gend ? gbeg + bi * GB + gl : gbeg;
-#pragma unroll
-            for (int st = 0; st < 2; st++) {
-                const int8_t* pa = ln < 3 ? xs1 + g * kLimbRec + ln * kGroup + st * 64 + kg * 16 : xzero;
-                a[gl][st] = *reinterpret_cast<const int4v_t*>(pa);
-            }
-        }
-        int4v_t D[GB];
-#pragma unroll
-        for (int gl = 0; gl < GB; gl++) {
-            int4v_t b0, b1;
-            weight_operands<KIND>(wb[bi].w[gl], b0, b1);
-            D[gl] = mfma_i8(a[gl][0], b0, int4v_t{0, 0, 0, 0});
-            D[gl] = mfma_i8(a[gl][1], b1, D[gl]);
-        }
-#pragma unroll
-        for (int gl = 0; gl < GB; gl++) {
-            const int g = gbeg + bi * GB + gl;
-            if (g >= gend) break;
-            const uint32_t sw = (gl & 2) ? wb[bi].s[gl / 4].y : wb[bi].s[gl / 4].x;
-            const float s = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
-            const int z = KIND == 1 ? int((wb[bi].z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
-            acc = combine(acc, D[gl][0], D[gl][1], D[gl][2], z, ms1[g], s);
-        }
+    for (int i = 0; i < TPW; i++) {
+        const float acc = slice_dot<KIND, NG>(b[i], xs1, ms1, xzero, gbeg, gs, ln, kg);
+        if (lane < 16) red[i][wave][lane] = acc;
+        if (i + PD < TPW) load_slice<KIND, NG, MODE>(b[i + PD], p, tile_of(i + PD), gbeg, gs, ln, kg);
     }
-    if (KS == 1) {
-        if (lane < 16 && row < mr.N) mr.y[row] = acc + (mr.bias ? bf16_to_f32(mr.bias[row]) : 0.0f);
-        return;
-    }
-    if (lane < 16) red[wave][lane] = acc;
     __syncthreads();
-    if (tid < 16) {
-        const int64_t n = (int64_t(blockIdx.x) - mr.tile0) * 16 + tid;
-        if (n < mr.N) {
-            float sum = red[0][tid];
 #pragma unroll
-            for (int k = 1; k < KS; k++) sum += red[k][tid];
-            mr.y[n] = sum + (mr.bias ? bf16_to_f32(mr.bias[n]) : 0.0f);
+    for (int i = 0; i < TPW; i++) {
+        float sum = red[i][0][ln];
+#pragma unroll
+        for (int k = 1; k < MAXW; k++) {
+            const float v = red[i][k][ln];
+            sum += k < KS ? v : 0.0f;
+        }
+        yv[i] = sum + __uint_as_float(bias[i] << 16);
+    }
+    if (wave == 0 && lane < 16) {
+#pragma unroll
+        for (int i = 0; i < TPW; i++) {
+            if (tile_of(i) >= p.ntiles) break;
+            const TileSel ts = select_tile(p, tile_of(i));
+            if (ts.row0 + lane < ts.m.N) ts.m.y[ts.row0 + lane] = yv[i];
         }
     }
 }
@@ -634,33 +730,6 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restric
     y[i] = sum + (bias ? bf16_to_f32(bias[i % N]) : 0.0f);
 }
 
-template <int KIND, int TW, int KS, int GB>
-void launch_gemv1_s(const GemvParams& p, int nb, int mode, unsigned grid, size_t lds, hipStream_t stream) {
-#define IQ_G1(NB)                                                                                  \
-    do {                                                                                           \
-        if (mode == 2) gemv1_kernel<KIND, TW, KS, GB, NB, 2><<<grid, 64 * TW * KS, lds, stream>>>(p); \
-        else if (mode == 1) gemv1_kernel<KIND, TW, KS, GB, NB, 1><<<grid, 64 * TW * KS, lds, stream>>>(p); \
-        else gemv1_kernel<KIND, TW, KS, GB, NB, 0><<<grid, 64 * TW * KS, lds, stream>>>(p);        \
-    } while (0)
-    switch (nb) {
-        case 1: IQ_G1(1); break;
-        case 2: IQ_G1(2); break;
-        case 3: IQ_G1(3); break;
-        default: IQ_G1(4); break;
-    }
-#undef IQ_G1
-}
-
-// Instantiated workgroup shapes: one tile, KS = 4, 8 or 16 slices.
-template <int KIND, int GB>
-void launch_gemv1_t(const GemvParams& p, int KS, int vec, unsigned grid, hipStream_t stream) {
-    const size_t lds = size_t(p.G) * kLimbRec + size_t(p.G + 1) * 16;
-    const int nb = (p.gs + GB - 1) / GB;
-    if (KS == 4) launch_gemv1_s<KIND, 1, 4, GB>(p, nb, vec, grid, lds, stream);
-    else if (KS == 8) launch_gemv1_s<KIND, 1, 8, GB>(p, nb, vec, grid, lds, stream);
-    else launch_gemv1_s<KIND, 1, 16, GB>(p, nb, vec, grid, lds, stream);
-}
-
 template <int KIND, int GC>
 void launch_gemvb_t(const GemvParams& p, bool vec, unsigned grid, size_t lds, hipStream_t stream) {
     const int M = p.M;
@@ -681,32 +750,76 @@ int env_int(const char* name, int dflt) {
     return v ? atoi(v) : dflt;
 }
 
-// MODE of the 1-row kernel (see load_batch): 16-byte paths need K % 128 == 0
-// and a 16-byte aligned activation row.
+// MODE of the 1-row kernel (see load_slice); 16-byte paths also need a
+// 16-byte aligned activation row.
 int gemv1_mode(int64_t K, int64_t G, const float* x) {
     if (K % kGroup || reinterpret_cast<uintptr_t>(x) % 16) return 0;
     return G % 4 ? 1 : 2;
 }
 
-// Workgroup K-slices of the 1-row kernel: the smallest of 4, 8, 16 whose
-// slices fit 4 weight batches (measured on MI355X: 4 slices beat more,
-// smaller workgroups whenever they fit); 0 when the kernel does not apply
-// (the LDS copy of the converted row would exceed 96 KiB).
-int gemv1_slices(int64_t G, int kind, int mode) {
-    if (G * (kLimbRec + 16) > 96 * 1024) return 0;
-    const int gb1 = kind == 1 ? 8 : 4;  // groups per batch (8 KiB of weights per wave)
-    for (int ks : {4, 8, 16}) {
-        int gs = int((G + ks - 1) / ks);
-        if (mode == 2) gs = (gs + 3) / 4 * 4;
-        if (gs <= 4 * gb1) return ks;
+// Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
+// (ks), the slice capacity NG of the kernel instance and whether workgroups
+// walk several tiles with prefetch (pf).
+struct G1Plan {
+    int gs, ks, ng, grid, tpw;
+};
+
+// Kernel instances: (slice capacity NG, tiles per workgroup TPW, max waves
+// per workgroup).  All TPW slices of a wave are requested at the start, so
+// TPW * NG bounds the registers held by weights in flight:
+//   several tiles per workgroup (TPW 2..5): int4 (8, 8), int8 (4, 8) --
+//     128 B of weights per lane per tile, up to 256 VGPRs (2 waves / SIMD);
+//   one tile per workgroup: int4 (12, 16), int8 (20, 8).
+// ng = 0 when the 1-row kernel does not apply (the slices would exceed the
+// capacity, or the LDS copy of the converted row would exceed 64 KiB).
+// TPW aims at about 2 resident workgroups per CU holding every tile.
+G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
+    G1Plan pl{0, 0, 0, 0, 1};
+    if (G * (kLimbRec + 16) > 64 * 1024) return pl;
+    const int wpc = 2;
+    const int small = kind == 1 ? 8 : 4;
+    int per_wg = (ntiles + cus * wpc - 1) / (cus * wpc);  // tiles per workgroup
+    if (per_wg > 5) per_wg = 5;
+    int maxw;
+    if (per_wg > 1 && G <= int64_t(small) * 8) {
+        pl.ng = small;
+        pl.tpw = per_wg;
+        pl.gs = small;
+        maxw = 8;
+    } else {
+        pl.ng = kind == 1 ? 12 : 20;
+        pl.tpw = 1;
+        maxw = kind == 1 ? 16 : 8;
+        pl.gs = int((G + maxw - 1) / maxw);
+        if (mode == 2) pl.gs = (pl.gs + 3) / 4 * 4;
     }
-    return 0;
+    pl.grid = (ntiles + pl.tpw - 1) / pl.tpw;
+    if (pl.gs > G) pl.gs = int(G);
+    pl.ks = int((G + pl.gs - 1) / pl.gs);
+    if (pl.gs > pl.ng || pl.ks > maxw) pl.ng = 0;
+    return pl;
 }
 
-// The 1-row kernel on n <= kMaxMulti matrices of one kind and width: one grid,
-// matrix i owns the workgroups [tile0_i, tile0_i + ceil(N_i / 16)).
+template <int KIND, int NG, int TPW, int MAXW>
+void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
+    if (mode == 2) gemv1_kernel<KIND, NG, 2, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+    else if (mode == 1) gemv1_kernel<KIND, NG, 1, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+    else gemv1_kernel<KIND, NG, 0, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+}
+
+template <int KIND, int NG>
+void launch_gemv1_tpw(const GemvParams& p, int mode, int ks, int tpw, unsigned grid, size_t lds, hipStream_t stream) {
+    switch (tpw) {
+        case 2: launch_gemv1_m<KIND, NG, 2, 8>(p, mode, ks, grid, lds, stream); break;
+        case 3: launch_gemv1_m<KIND, NG, 3, 8>(p, mode, ks, grid, lds, stream); break;
+        case 4: launch_gemv1_m<KIND, NG, 4, 8>(p, mode, ks, grid, lds, stream); break;
+        default: launch_gemv1_m<KIND, NG, 5, 8>(p, mode, ks, grid, lds, stream); break;
+    }
+}
+
+// The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
 hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n,
-                        int KS, int mode, hipStream_t stream) {
+                        const G1Plan& pl, int mode, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
     GemvParams p{};
     int tiles = 0;
@@ -718,12 +831,25 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     p.K = K; p.G = G;
     p.x = x;
     p.M = 1;
-    p.gs = int((G + KS - 1) / KS);
-    if (mode == 2) p.gs = (p.gs + 3) / 4 * 4;  // 4-group aligned slices: vector scale loads
+    p.gs = pl.gs;
     p.S = 1;
-    if (W[0].kind == 1) launch_gemv1_t<1, 8>(p, KS, mode, unsigned(tiles), stream);
-    else launch_gemv1_t<0, 4>(p, KS, mode, unsigned(tiles), stream);
+    p.ntiles = tiles;
+    const size_t lds = size_t(G) * (kLimbRec + 16);
+    const unsigned grid = unsigned(pl.grid);
+    if (W[0].kind == 1) {
+        if (pl.tpw > 1) launch_gemv1_tpw<1, 8>(p, mode, pl.ks, pl.tpw, grid, lds, stream);
+        else launch_gemv1_m<1, 12, 1, 16>(p, mode, pl.ks, grid, lds, stream);
+    } else {
+        if (pl.tpw > 1) launch_gemv1_tpw<0, 4>(p, mode, pl.ks, pl.tpw, grid, lds, stream);
+        else launch_gemv1_m<0, 20, 1, 8>(p, mode, pl.ks, grid, lds, stream);
+    }
     return hipGetLastError();
+}
+
+int total_tiles(const QView* W, int n) {
+    int t = 0;
+    for (int i = 0; i < n; i++) t += int((W[i].rows + 15) / 16);
+    return t;
 }
 
 // Byte limbs + meta of x [M][K] into the workspace.
@@ -798,7 +924,7 @@ hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, flo
 hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
     const int64_t G = (K + kGroup - 1) / kGroup;
     hipError_t e;
-    if (M == 1 && gemv1_slices(G, kind, gemv1_mode(K, G, ws->xf)) > 0) {
+    if (M == 1 && gemv1_plan(G, kind, gemv1_mode(K, G, ws->xf), 1, device_cu_count()).ng > 0) {
         e = hipMemcpyAsync(ws->xf, x, sizeof(float) * size_t(K), hipMemcpyDeviceToDevice, stream);
         ws->prep_copy = true;
     } else {
@@ -816,7 +942,9 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
     if (ws->prep_copy) {
         const int64_t K = W[0].cols, G = W[0].groups;
         const int mode = gemv1_mode(K, G, ws->xf);
-        return launch_gemv1(ws->xf, W, bias, y, n, gemv1_slices(G, W[0].kind, mode), mode, stream);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count());
+        if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream);
+        return hipErrorInvalidValue;
     }
     return launch_batched_multi(W, bias, y, n, M, ws, stream);
 }
@@ -831,8 +959,8 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     const int64_t K = W[0].cols, G = W[0].groups;
     if (M == 1) {
         const int mode = gemv1_mode(K, G, x);
-        const int KS = gemv1_slices(G, W[0].kind, mode);
-        if (KS > 0) return launch_gemv1(x, W, bias, y, n, KS, mode, stream);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count());
+        if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream);
     }
     hipError_t e = launch_xprep_limbs(x, M, K, W[0].kind, ws, stream);
     ws->prep_copy = false;
