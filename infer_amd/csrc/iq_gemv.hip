@@ -772,11 +772,11 @@ struct G1Plan {
 //   one tile per workgroup: int4 (12, 16), int8 (20, 8).
 // ng = 0 when the 1-row kernel does not apply (the slices would exceed the
 // capacity, or the LDS copy of the converted row would exceed 64 KiB).
-// TPW aims at about 2 resident workgroups per CU holding every tile.
+// TPW aims at one workgroup per CU holding every tile (at most 5).
 G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
     G1Plan pl{0, 0, 0, 0, 1};
     if (G * (kLimbRec + 16) > 64 * 1024) return pl;
-    const int wpc = 2;
+    const int wpc = 1;
     const int small = kind == 1 ? 8 : 4;
     int per_wg = (ntiles + cus * wpc - 1) / (cus * wpc);  // tiles per workgroup
     if (per_wg > 5) per_wg = 5;
