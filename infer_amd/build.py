@@ -1,8 +1,11 @@
-"""Builds libiq.so (the gfx950 HIP kernels + C ABI) in-tree with hipcc.
+"""Builds, in-tree:
+  libiq.so       the gfx950 HIP kernels + C ABI (include/iq.h), with hipcc;
+  libiq_host.so  the C++ host layer (host/iq_host.h: .llmq container,
+                 QuantModel, QuantView launchers), over libiq.so.
 
     python -m infer_amd.build          # or infer_amd.build.build()
 
-The library is compiled for gfx950 only, without fast-math and with
+The kernels are compiled for gfx950 only, without fast-math and with
 -ffp-contract=off (the quantiser must round exactly like src/quant.cpp), and
 with packed fp32 ops disabled.
 """
@@ -14,6 +17,12 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libiq.so")
+HOST_LIB = os.path.join(HERE, "libiq_host.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+# flags for host-only C++ that uses the HIP runtime API and include/iq.h
+HOST_CXX_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+                  "-I" + os.path.join(os.path.dirname(HERE), "include"), "-I" + os.path.join(HERE, "host"),
+                  "-I" + os.path.join(ROCM, "include")]
 SOURCES = ["iq_abi.hip", "iq_quant.hip", "iq_gemv.hip", "iq_gemm.hip"]
 
 HIPCC_FLAGS = [
@@ -61,7 +70,23 @@ def build(verbose=False):
     if verbose and msgs:
         sys.stderr.write("\n".join(msgs) + "\n")
     os.replace(tmp, LIB)
+    build_host()
     return LIB
+
+
+def build_host():
+    """libiq_host.so: host/iq_host.cpp with g++, linked against libiq.so and
+    the HIP runtime (found next to it / in ROCm at run time)."""
+    tmp = HOST_LIB + ".tmp"
+    cmd = (["g++"] + HOST_CXX_FLAGS + ["-shared", "-o", tmp, os.path.join(HERE, "host", "iq_host.cpp"),
+           "-L" + HERE, "-liq", "-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+    r = _run(cmd)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("g++ failed building libiq_host.so")
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
 
 
 if __name__ == "__main__":

@@ -1,0 +1,655 @@
+// iq_host.cpp -- the C++ host layer of iq_host.h: .llmq container,
+// config.json, model loading and upload, and the QuantView launchers over the
+// C ABI of include/iq.h.
+#include "iq_host.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <stdexcept>
+
+namespace llm {
+
+namespace {
+
+// ------------------------------------------------------------------ JSON
+// The subset .llmq headers and config.json use: objects, arrays, strings,
+// numbers, true / false / null.
+struct JVal {
+    enum Type { kNull, kBool, kNum, kStr, kArr, kObj } type = kNull;
+    bool b = false;
+    double num = 0;
+    bool is_int = false;
+    int64_t inum = 0;
+    std::string str;
+    std::vector<JVal> arr;
+    std::vector<std::pair<std::string, JVal>> obj;
+
+    const JVal* find(const std::string& k) const {
+        for (const auto& kv : obj)
+            if (kv.first == k) return &kv.second;
+        return nullptr;
+    }
+    const JVal& at(const std::string& k) const {
+        const JVal* v = find(k);
+        if (!v) throw std::runtime_error("missing key \"" + k + "\"");
+        return *v;
+    }
+    int64_t as_int() const {
+        if (type != kNum) throw std::runtime_error("expected a number");
+        return is_int ? inum : int64_t(num);
+    }
+    double as_double() const {
+        if (type != kNum) throw std::runtime_error("expected a number");
+        return is_int ? double(inum) : num;
+    }
+    bool as_bool() const {
+        if (type != kBool) throw std::runtime_error("expected true or false");
+        return b;
+    }
+    const std::string& as_str() const {
+        if (type != kStr) throw std::runtime_error("expected a string");
+        return str;
+    }
+};
+
+class JParser {
+public:
+    JParser(const char* b, const char* e) : p_(b), e_(e) {}
+    JVal parse() {
+        JVal v = value();
+        ws();
+        if (p_ != e_) fail("trailing characters");
+        return v;
+    }
+
+private:
+    const char* p_;
+    const char* e_;
+
+    [[noreturn]] void fail(const char* what) { throw std::runtime_error(std::string("JSON: ") + what); }
+    void ws() {
+        while (p_ < e_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) p_++;
+    }
+    bool lit(const char* s) {
+        const size_t n = std::strlen(s);
+        if (size_t(e_ - p_) >= n && std::memcmp(p_, s, n) == 0) {
+            p_ += n;
+            return true;
+        }
+        return false;
+    }
+    JVal value() {
+        ws();
+        if (p_ >= e_) fail("unexpected end");
+        JVal v;
+        if (*p_ == '{') {
+            v.type = JVal::kObj;
+            p_++;
+            ws();
+            if (p_ < e_ && *p_ == '}') { p_++; return v; }
+            for (;;) {
+                ws();
+                std::string k = string();
+                ws();
+                if (p_ >= e_ || *p_ != ':') fail("expected ':'");
+                p_++;
+                v.obj.emplace_back(std::move(k), value());
+                ws();
+                if (p_ < e_ && *p_ == ',') { p_++; continue; }
+                if (p_ < e_ && *p_ == '}') { p_++; return v; }
+                fail("expected ',' or '}'");
+            }
+        }
+        if (*p_ == '[') {
+            v.type = JVal::kArr;
+            p_++;
+            ws();
+            if (p_ < e_ && *p_ == ']') { p_++; return v; }
+            for (;;) {
+                v.arr.push_back(value());
+                ws();
+                if (p_ < e_ && *p_ == ',') { p_++; continue; }
+                if (p_ < e_ && *p_ == ']') { p_++; return v; }
+                fail("expected ',' or ']'");
+            }
+        }
+        if (*p_ == '"') {
+            v.type = JVal::kStr;
+            v.str = string();
+            return v;
+        }
+        if (lit("true")) { v.type = JVal::kBool; v.b = true; return v; }
+        if (lit("false")) { v.type = JVal::kBool; v.b = false; return v; }
+        if (lit("null")) return v;
+        return number();
+    }
+    std::string string() {
+        if (p_ >= e_ || *p_ != '"') fail("expected a string");
+        p_++;
+        std::string s;
+        while (p_ < e_ && *p_ != '"') {
+            char c = *p_++;
+            if (c != '\\') { s += c; continue; }
+            if (p_ >= e_) fail("bad escape");
+            c = *p_++;
+            switch (c) {
+                case '"': s += '"'; break;
+                case '\\': s += '\\'; break;
+                case '/': s += '/'; break;
+                case 'b': s += '\b'; break;
+                case 'f': s += '\f'; break;
+                case 'n': s += '\n'; break;
+                case 'r': s += '\r'; break;
+                case 't': s += '\t'; break;
+                case 'u': {
+                    if (e_ - p_ < 4) fail("bad \\u escape");
+                    unsigned cp = 0;
+                    for (int i = 0; i < 4; i++) {
+                        const char h = *p_++;
+                        cp = cp * 16 + unsigned(h >= 'a' ? h - 'a' + 10 : h >= 'A' ? h - 'A' + 10 : h - '0');
+                    }
+                    // UTF-8 of a BMP code point (names here are ASCII)
+                    if (cp < 0x80) s += char(cp);
+                    else if (cp < 0x800) { s += char(0xC0 | (cp >> 6)); s += char(0x80 | (cp & 0x3F)); }
+                    else {
+                        s += char(0xE0 | (cp >> 12));
+                        s += char(0x80 | ((cp >> 6) & 0x3F));
+                        s += char(0x80 | (cp & 0x3F));
+                    }
+                    break;
+                }
+                default: fail("bad escape");
+            }
+        }
+        if (p_ >= e_) fail("unterminated string");
+        p_++;
+        return s;
+    }
+    JVal number() {
+        const char* b = p_;
+        bool frac = false;
+        if (p_ < e_ && (*p_ == '-' || *p_ == '+')) p_++;
+        while (p_ < e_ && ((*p_ >= '0' && *p_ <= '9') || *p_ == '.' || *p_ == 'e' || *p_ == 'E' ||
+                           *p_ == '-' || *p_ == '+')) {
+            if (*p_ == '.' || *p_ == 'e' || *p_ == 'E') frac = true;
+            p_++;
+        }
+        if (p_ == b) fail("unexpected character");
+        const std::string t(b, p_);
+        JVal v;
+        v.type = JVal::kNum;
+        v.num = std::strtod(t.c_str(), nullptr);
+        if (!frac) {
+            v.is_int = true;
+            v.inum = std::strtoll(t.c_str(), nullptr, 10);
+        }
+        return v;
+    }
+};
+
+JVal parse_json(const char* b, const char* e) { return JParser(b, e).parse(); }
+
+std::string read_file(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + path);
+    return std::string(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+}
+
+float bf16_bits_to_f32(uint16_t h) {
+    const uint32_t u = uint32_t(h) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void iq_check(int rc, const char* what) {
+    if (rc != IQ_OK) throw std::runtime_error(std::string(what) + ": " + iq_error_string(rc));
+}
+
+}  // namespace
+
+const char* qkind_name(QKind k) {
+    return k == QKind::kInt8 ? "int8" : k == QKind::kInt4 ? "int4" : "bf16";
+}
+
+QTensor QMatrix::view() const {
+    QTensor t;
+    t.kind = kind;
+    t.rows = rows;
+    t.cols = cols;
+    t.q = q.data();
+    t.scales = scales.data();
+    t.zeros = zeros.empty() ? nullptr : zeros.data();
+    return t;
+}
+
+float dequant(const QTensor& t, int64_t r, int64_t c) {
+    const int64_t G = t.groups(), g = c / kGroup;
+    const float s = bf16_bits_to_f32(t.scales[r * G + g]);
+    if (t.kind == QKind::kInt8) return s * float(int8_t(t.q[r * t.cols + c]));
+    const uint8_t byte = t.q[(r * t.cols + c) / 2];
+    const int v = (c & 1) ? (byte >> 4) : (byte & 0x0F);
+    return s * float(v - int(t.zeros[r * G + g]));
+}
+
+QMatrix quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, QKind kind) {
+    if (kind != QKind::kInt8 && kind != QKind::kInt4) throw std::runtime_error("quantize: kind must be int8 or int4");
+    if (kind == QKind::kInt4 && cols % 2) throw std::runtime_error("int4 quantisation needs an even column count");
+    QMatrix m;
+    m.kind = kind;
+    m.rows = rows;
+    m.cols = cols;
+    const int64_t G = (cols + kGroup - 1) / kGroup;
+    m.q.resize(kind == QKind::kInt4 ? size_t(rows) * cols / 2 : size_t(rows) * cols);
+    m.scales.resize(size_t(rows) * G);
+    if (kind == QKind::kInt4) m.zeros.resize(size_t(rows) * G);
+    const size_t nw = size_t(rows) * cols * 2, nq = m.q.size(), ns = m.scales.size() * 2, nz = m.zeros.size();
+    char* d = nullptr;
+    hip_check(hipMalloc(&d, nw + nq + ns + nz + 64), "quantize: hipMalloc");
+    auto cleanup = [&]() { (void)hipFree(d); };
+    try {
+        uint16_t* dw = reinterpret_cast<uint16_t*>(d);
+        uint8_t* dq = reinterpret_cast<uint8_t*>(d + nw);
+        uint16_t* ds = reinterpret_cast<uint16_t*>(d + ((nw + nq + 1) & ~size_t(1)));
+        uint8_t* dz = reinterpret_cast<uint8_t*>(reinterpret_cast<char*>(ds) + ns);
+        hip_check(hipMemcpy(dw, w_bf16, nw, hipMemcpyHostToDevice), "quantize: upload");
+        iq_check(iq_quantize(dw, rows, cols, kind == QKind::kInt4 ? IQ_INT4 : IQ_INT8, dq, ds,
+                             kind == QKind::kInt4 ? dz : nullptr, nullptr),
+                 "quantize");
+        hip_check(hipMemcpy(m.q.data(), dq, nq, hipMemcpyDeviceToHost), "quantize: download");
+        hip_check(hipMemcpy(m.scales.data(), ds, ns, hipMemcpyDeviceToHost), "quantize: download");
+        if (nz) hip_check(hipMemcpy(m.zeros.data(), dz, nz, hipMemcpyDeviceToHost), "quantize: download");
+    } catch (...) {
+        cleanup();
+        throw;
+    }
+    cleanup();
+    return m;
+}
+
+// ------------------------------------------------------------------ writer
+void QuantWriter::add(const std::string& name, const QMatrix& m) {
+    if (m.kind == QKind::kBf16) throw std::runtime_error("QuantWriter::add: " + name + " is not quantised");
+    entries_.push_back({name, m.kind, {m.rows, m.cols}, m.q, m.zeros, m.scales});
+}
+
+void QuantWriter::add_bf16(const std::string& name, const uint16_t* data, std::vector<int64_t> shape) {
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    Entry e{name, QKind::kBf16, std::move(shape), {}, {}, {}};
+    e.scales.assign(data, data + n);  // the bf16 payload rides in `scales`
+    entries_.push_back(std::move(e));
+}
+
+std::vector<uint8_t> QuantWriter::serialize() const {
+    // Header: names in sorted order (a JSON object with sorted keys, compact),
+    // byte ranges in insertion order; the same bytes the reference's writer
+    // produces for the same entries.
+    struct Ranges {
+        const Entry* e;
+        size_t data[2], scales[2], zeros[2];
+    };
+    std::map<std::string, Ranges> hdr;
+    size_t off = 0;
+    for (const Entry& e : entries_) {
+        Ranges r{&e, {0, 0}, {0, 0}, {0, 0}};
+        auto span = [&](size_t (&rg)[2], size_t n) { rg[0] = off; rg[1] = off + n; off += n; };
+        if (e.kind == QKind::kBf16) {
+            span(r.data, e.scales.size() * 2);
+        } else {
+            span(r.data, e.q.size());
+            span(r.scales, e.scales.size() * 2);
+            if (!e.zeros.empty()) span(r.zeros, e.zeros.size());
+        }
+        if (!hdr.emplace(e.name, r).second) throw std::runtime_error("QuantWriter: duplicate tensor " + e.name);
+    }
+    std::string h = "{";
+    bool first = true;
+    for (const auto& kv : hdr) {
+        const Ranges& r = kv.second;
+        const Entry& e = *r.e;
+        auto range = [](const size_t (&rg)[2]) { return "[" + std::to_string(rg[0]) + "," + std::to_string(rg[1]) + "]"; };
+        std::string shape = "[";
+        for (size_t i = 0; i < e.shape.size(); i++) shape += (i ? "," : "") + std::to_string(e.shape[i]);
+        shape += "]";
+        std::string esc;
+        for (char c : kv.first) {
+            if (c == '"' || c == '\\') esc += '\\';
+            esc += c;
+        }
+        h += (first ? "\"" : ",\"") + esc + "\":{\"data\":" + range(r.data) + ",\"dtype\":\"" + qkind_name(e.kind) +
+             "\",\"group\":" + std::to_string(kGroup);
+        if (e.kind != QKind::kBf16) h += ",\"scales\":" + range(r.scales);
+        h += ",\"shape\":" + shape;
+        if (e.kind != QKind::kBf16 && !e.zeros.empty()) h += ",\"zeros\":" + range(r.zeros);
+        h += "}";
+        first = false;
+    }
+    h += "}";
+    std::vector<uint8_t> out;
+    out.reserve(16 + h.size() + off);
+    const char magic[8] = {'L', 'L', 'M', 'Q', '0', '0', '0', '1'};
+    out.insert(out.end(), magic, magic + 8);
+    const uint64_t hl = h.size();
+    for (int i = 0; i < 8; i++) out.push_back(uint8_t(hl >> (8 * i)));
+    out.insert(out.end(), h.begin(), h.end());
+    auto put = [&](const void* p, size_t n) {
+        const uint8_t* b = static_cast<const uint8_t*>(p);
+        out.insert(out.end(), b, b + n);
+    };
+    for (const Entry& e : entries_) {
+        if (e.kind == QKind::kBf16) {
+            put(e.scales.data(), e.scales.size() * 2);
+            continue;
+        }
+        put(e.q.data(), e.q.size());
+        put(e.scales.data(), e.scales.size() * 2);
+        if (!e.zeros.empty()) put(e.zeros.data(), e.zeros.size());
+    }
+    return out;
+}
+
+void QuantWriter::write(const std::string& path) const {
+    const std::vector<uint8_t> b = serialize();
+    std::ofstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot write " + path);
+    f.write(reinterpret_cast<const char*>(b.data()), std::streamsize(b.size()));
+    if (!f) throw std::runtime_error("write failed: " + path);
+}
+
+// ------------------------------------------------------------------ reader
+QuantFile::~QuantFile() {
+    if (map_) munmap(map_, map_size_);
+}
+
+void QuantFile::open(const std::string& path) {
+    if (map_) {
+        munmap(map_, map_size_);
+        map_ = nullptr;
+        tensors_.clear();
+        offset_.clear();
+        kind_ = QKind::kBf16;
+    }
+    const int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) throw std::runtime_error("cannot open " + path);
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+        ::close(fd);
+        throw std::runtime_error("fstat " + path);
+    }
+    map_size_ = size_t(st.st_size);
+    map_ = map_size_ ? mmap(nullptr, map_size_, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
+    ::close(fd);
+    if (map_ == MAP_FAILED) {
+        map_ = nullptr;
+        throw std::runtime_error("mmap " + path);
+    }
+    const auto* base = static_cast<const uint8_t*>(map_);
+    if (map_size_ < 16 || std::memcmp(base, "LLMQ0001", 8) != 0) throw std::runtime_error("not an .llmq file: " + path);
+    uint64_t hl = 0;
+    for (int i = 0; i < 8; i++) hl |= uint64_t(base[8 + i]) << (8 * i);
+    if (hl > map_size_ - 16) throw std::runtime_error("truncated header: " + path);
+    const JVal h = parse_json(reinterpret_cast<const char*>(base + 16), reinterpret_cast<const char*>(base + 16 + hl));
+    if (h.type != JVal::kObj) throw std::runtime_error("bad header in " + path);
+    const uint8_t* blob = base + 16 + hl;
+    const size_t blob_size = map_size_ - 16 - hl;
+    auto range = [&](const JVal& r, size_t need, size_t* begin) {
+        if (r.type != JVal::kArr || r.arr.size() != 2) throw std::runtime_error("bad range in " + path);
+        const int64_t b = r.arr[0].as_int(), e = r.arr[1].as_int();
+        if (b < 0 || e < b || size_t(e) > blob_size) throw std::runtime_error("bad range in " + path);
+        if (size_t(e - b) != need) throw std::runtime_error("range size mismatch in " + path);
+        if (begin) *begin = size_t(b);
+        return blob + b;
+    };
+    for (const auto& kv : h.obj) {
+        const JVal& j = kv.second;
+        QTensor t;
+        const std::string& d = j.at("dtype").as_str();
+        t.kind = d == "int8" ? QKind::kInt8 : d == "int4" ? QKind::kInt4 : QKind::kBf16;
+        if (t.kind == QKind::kBf16 && d != "bf16") throw std::runtime_error("unknown dtype " + d + " in " + path);
+        const JVal& sh = j.at("shape");
+        if (sh.type != JVal::kArr) throw std::runtime_error("bad shape in " + path);
+        t.rows = sh.arr.size() >= 1 ? sh.arr[0].as_int() : 0;
+        t.cols = sh.arr.size() >= 2 ? sh.arr[1].as_int() : 1;
+        int64_t n = 1;
+        for (const JVal& x : sh.arr) n *= x.as_int();
+        size_t first = 0;
+        if (t.kind == QKind::kBf16) {
+            t.bf16 = reinterpret_cast<const uint16_t*>(range(j.at("data"), size_t(n) * 2, &first));
+        } else {
+            const JVal* g = j.find("group");
+            if (g && g->as_int() != kGroup) throw std::runtime_error("group size mismatch in " + path);
+            if (t.kind == QKind::kInt4 && t.cols % 2) throw std::runtime_error("odd int4 width in " + path);
+            t.q = range(j.at("data"), t.q_bytes(), &first);
+            t.scales = reinterpret_cast<const uint16_t*>(range(j.at("scales"), size_t(t.rows * t.groups()) * 2, nullptr));
+            if (const JVal* z = j.find("zeros")) t.zeros = range(*z, size_t(t.rows * t.groups()), nullptr);
+            if (t.kind == QKind::kInt4 && !t.zeros) throw std::runtime_error("int4 tensor without zeros in " + path);
+            kind_ = t.kind;
+        }
+        tensors_[kv.first] = t;
+        offset_[kv.first] = first;
+    }
+}
+
+const QTensor& QuantFile::get(const std::string& name) const {
+    auto it = tensors_.find(name);
+    if (it == tensors_.end()) throw std::runtime_error("tensor not in .llmq: " + name);
+    return it->second;
+}
+
+std::vector<std::string> QuantFile::names() const {
+    std::vector<std::string> v;
+    for (const auto& kv : tensors_) v.push_back(kv.first);
+    return v;
+}
+
+std::vector<std::string> QuantFile::names_in_file() const {
+    std::vector<std::pair<size_t, std::string>> v;
+    for (const auto& kv : offset_) v.emplace_back(kv.second, kv.first);
+    std::sort(v.begin(), v.end());
+    std::vector<std::string> out;
+    for (auto& p : v) out.push_back(p.second);
+    return out;
+}
+
+// ------------------------------------------------------------------ config
+ModelConfig ModelConfig::from_file(const std::string& path) {
+    const std::string text = read_file(path);
+    const JVal j = parse_json(text.data(), text.data() + text.size());
+    ModelConfig c;
+    const JVal& archs = j.at("architectures");
+    if (archs.type != JVal::kArr || archs.arr.empty()) throw std::runtime_error("empty architectures in " + path);
+    c.architecture = archs.arr[0].as_str();
+    c.hidden_size = j.at("hidden_size").as_int();
+    c.num_hidden_layers = j.at("num_hidden_layers").as_int();
+    c.num_attention_heads = j.at("num_attention_heads").as_int();
+    c.num_key_value_heads = j.at("num_key_value_heads").as_int();
+    c.intermediate_size = j.at("intermediate_size").as_int();
+    c.vocab_size = j.at("vocab_size").as_int();
+    c.rope_theta = j.at("rope_theta").as_double();
+    c.rms_norm_eps = j.at("rms_norm_eps").as_double();
+    const JVal* tie = j.find("tie_word_embeddings");
+    c.tie_word_embeddings = tie && tie->type == JVal::kBool && tie->b;
+    if (c.num_attention_heads <= 0 || c.num_key_value_heads <= 0) throw std::runtime_error("bad head counts in " + path);
+    const int64_t derived = c.hidden_size / c.num_attention_heads;
+    const JVal* hd = j.find("head_dim");
+    c.head_dim = hd && hd->type == JVal::kNum ? hd->as_int() : derived;
+    if (c.head_dim != derived) throw std::runtime_error("head_dim inconsistent with hidden_size/num_heads");
+    const JVal* ab = j.find("attention_bias");
+    if (ab && ab->type == JVal::kBool) c.attention_bias = ab->b;
+    else c.attention_bias = c.architecture == "Qwen2ForCausalLM";  // Qwen2 always has QKV bias
+    if (c.num_attention_heads % c.num_key_value_heads != 0)
+        throw std::runtime_error("num_heads not divisible by num_kv_heads (GQA requires it)");
+    return c;
+}
+
+// ------------------------------------------------------------------ model
+std::string QuantModel::file_for(const std::string& dir, QKind kind) {
+    return dir + (kind == QKind::kInt4 ? "/model.q4.llmq" : "/model.q8.llmq");
+}
+
+void QuantModel::load(const std::string& dir, QKind k) {
+    cfg = ModelConfig::from_file(dir + "/config.json");
+    kind = k;
+    file_.open(file_for(dir, k));
+    auto mat = [&](const std::string& n, int64_t rows, int64_t cols) {
+        const QTensor& t = file_.get(n);
+        if (t.rows != rows || t.cols != cols || t.kind != k) throw std::runtime_error("shape/kind mismatch for " + n);
+        return t;
+    };
+    auto vec = [&](const std::string& n, int64_t len) {
+        const QTensor& t = file_.get(n);
+        if (t.kind != QKind::kBf16 || t.rows != len) throw std::runtime_error("bad bf16 tensor " + n);
+        return t;
+    };
+    const int64_t H = cfg.hidden_size, q_out = cfg.num_attention_heads * cfg.head_dim,
+                  kv_out = cfg.num_key_value_heads * cfg.head_dim, I = cfg.intermediate_size;
+    embed_tokens = mat("model.embed_tokens.weight", cfg.vocab_size, H);
+    lm_head = QTensor{};
+    if (!cfg.tie_word_embeddings) lm_head = mat("lm_head.weight", cfg.vocab_size, H);
+    final_norm = vec("model.norm.weight", H);
+    layers.assign(size_t(cfg.num_hidden_layers), QLayer{});
+    for (int64_t i = 0; i < cfg.num_hidden_layers; i++) {
+        const std::string p = "model.layers." + std::to_string(i) + ".";
+        QLayer& L = layers[size_t(i)];
+        L.q_w = mat(p + "self_attn.q_proj.weight", q_out, H);
+        L.k_w = mat(p + "self_attn.k_proj.weight", kv_out, H);
+        L.v_w = mat(p + "self_attn.v_proj.weight", kv_out, H);
+        L.o_w = mat(p + "self_attn.o_proj.weight", H, q_out);
+        L.gate_w = mat(p + "mlp.gate_proj.weight", I, H);
+        L.up_w = mat(p + "mlp.up_proj.weight", I, H);
+        L.down_w = mat(p + "mlp.down_proj.weight", H, I);
+        L.input_ln = vec(p + "input_layernorm.weight", H);
+        L.post_attn_ln = vec(p + "post_attention_layernorm.weight", H);
+        L.has_bias = cfg.attention_bias;
+        if (L.has_bias) {
+            L.q_b = vec(p + "self_attn.q_proj.bias", q_out);
+            L.k_b = vec(p + "self_attn.k_proj.bias", kv_out);
+            L.v_b = vec(p + "self_attn.v_proj.bias", kv_out);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ device
+namespace gpu {
+
+static_assert(sizeof(QuantView) == sizeof(iq_view), "QuantView must match iq_view");
+static_assert(offsetof(QuantView, q) == offsetof(iq_view, q), "QuantView must match iq_view");
+static_assert(offsetof(QuantView, zeros) == offsetof(iq_view, zeros), "QuantView must match iq_view");
+
+namespace {
+const iq_view* as_iq(const QuantView& W) { return reinterpret_cast<const iq_view*>(&W); }
+}  // namespace
+
+void launch_gemv_batched_q(const float* x, const QuantView& W, const uint16_t* bias, int B, int64_t in, int64_t out,
+                           float* y, hipStream_t stream) {
+    iq_check(iq_gemv(x, as_iq(W), bias, B, in, out, y, stream), "launch_gemv_batched_q");
+}
+
+void launch_gemm_tiled_q(const float* x, const QuantView& W, const uint16_t* bias, int64_t T, int64_t in,
+                         int64_t out, float* y, hipStream_t stream) {
+    iq_check(iq_gemm(x, as_iq(W), bias, T, in, out, y, stream), "launch_gemm_tiled_q");
+}
+
+void launch_embedding_q(const QuantView& table, const int64_t* ids, int64_t T, int64_t H, float* out,
+                        hipStream_t stream) {
+    iq_check(iq_embedding(as_iq(table), ids, T, H, out, stream), "launch_embedding_q");
+}
+
+void linear_q(const float* x, const QuantView& W, const uint16_t* bias, int64_t T, int64_t in, int64_t out,
+              float* y, hipStream_t stream) {
+    iq_check(iq_linear(x, as_iq(W), bias, T, in, out, y, stream), "linear_q");
+}
+
+DevQuant::DevQuant(const QTensor& t) {
+    if (t.kind == QKind::kBf16) {
+        const size_t n = size_t(t.rows) * size_t(t.cols) * 2;
+        if (!n) return;
+        hip_check(hipMalloc(&data_, n), "DevQuant: hipMalloc");
+        hip_check(hipMemcpy(data_, t.bf16, n, hipMemcpyHostToDevice), "DevQuant: upload");
+        view_ = QuantView{QuantKind::kInt8, t.rows, t.cols, 0, nullptr, nullptr, nullptr};
+        return;
+    }
+    const size_t nq = t.q_bytes(), ns = size_t(t.rows * t.groups()) * 2, nz = t.zeros ? size_t(t.rows * t.groups()) : 0;
+    // q | scales | zeros in one allocation; the scales start 256-byte aligned
+    const size_t so = (nq + 255) & ~size_t(255), zo = so + ns;
+    hip_check(hipMalloc(&data_, zo + nz), "DevQuant: hipMalloc");
+    char* d = static_cast<char*>(data_);
+    try {
+        hip_check(hipMemcpy(d, t.q, nq, hipMemcpyHostToDevice), "DevQuant: upload");
+        hip_check(hipMemcpy(d + so, t.scales, ns, hipMemcpyHostToDevice), "DevQuant: upload");
+        if (nz) hip_check(hipMemcpy(d + zo, t.zeros, nz, hipMemcpyHostToDevice), "DevQuant: upload");
+    } catch (...) {
+        release();
+        throw;
+    }
+    view_ = QuantView{t.kind == QKind::kInt4 ? QuantKind::kInt4 : QuantKind::kInt8,
+                      t.rows,
+                      t.cols,
+                      t.groups(),
+                      reinterpret_cast<const uint8_t*>(d),
+                      reinterpret_cast<const uint16_t*>(d + so),
+                      nz ? reinterpret_cast<const uint8_t*>(d + zo) : nullptr};
+}
+
+void DevQuant::release() {
+    if (data_) (void)hipFree(data_);
+    data_ = nullptr;
+    view_ = QuantView{};
+}
+
+DevQuant::~DevQuant() { release(); }
+
+DevQuant::DevQuant(DevQuant&& o) noexcept : data_(o.data_), view_(o.view_) {
+    o.data_ = nullptr;
+    o.view_ = QuantView{};
+}
+
+DevQuant& DevQuant::operator=(DevQuant&& o) noexcept {
+    if (this != &o) {
+        release();
+        data_ = o.data_;
+        view_ = o.view_;
+        o.data_ = nullptr;
+        o.view_ = QuantView{};
+    }
+    return *this;
+}
+
+DevQuantModel::DevQuantModel(const QuantModel& m)
+    : embed_tokens(m.embed_tokens), lm_head(m.lm_head.rows ? DevQuant(m.lm_head) : DevQuant()),
+      final_norm(m.final_norm) {
+    layers.reserve(m.layers.size());
+    for (const QLayer& L : m.layers) {
+        DevLayer d;
+        d.q_w = DevQuant(L.q_w);
+        d.k_w = DevQuant(L.k_w);
+        d.v_w = DevQuant(L.v_w);
+        d.o_w = DevQuant(L.o_w);
+        d.gate_w = DevQuant(L.gate_w);
+        d.up_w = DevQuant(L.up_w);
+        d.down_w = DevQuant(L.down_w);
+        d.input_ln = DevQuant(L.input_ln);
+        d.post_attn_ln = DevQuant(L.post_attn_ln);
+        if (L.has_bias) {
+            d.q_b = DevQuant(L.q_b);
+            d.k_b = DevQuant(L.k_b);
+            d.v_b = DevQuant(L.v_b);
+        }
+        layers.push_back(std::move(d));
+    }
+}
+
+}  // namespace gpu
+}  // namespace llm

@@ -61,4 +61,55 @@ int ref_llmq_write(const char* path, const char* name, const uint8_t* q, const u
         return -1;
     }
 }
+
+// A QuantWriter (src/quant.h:68-77) behind a handle, for multi-tensor files.
+void* ref_writer_new() { return new llm::QuantWriter(); }
+void ref_writer_free(void* h) { delete static_cast<llm::QuantWriter*>(h); }
+
+int ref_writer_add(void* h, const char* name, const uint8_t* q, const uint16_t* scales,
+                   const uint8_t* zeros, int kind, int64_t rows, int64_t cols) {
+    try {
+        llm::QMatrix m;
+        m.kind = kind == 0 ? llm::QKind::kInt8 : llm::QKind::kInt4;
+        m.rows = rows; m.cols = cols;
+        const int64_t G = (cols + llm::kGroup - 1) / llm::kGroup;
+        m.q.assign(q, q + (kind == 1 ? rows * cols / 2 : rows * cols));
+        m.scales.assign(scales, scales + rows * G);
+        if (kind == 1) m.zeros.assign(zeros, zeros + rows * G);
+        static_cast<llm::QuantWriter*>(h)->add(name, m);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_writer_add_bf16(void* h, const char* name, const uint16_t* data, int64_t n) {
+    try {
+        static_cast<llm::QuantWriter*>(h)->add_bf16(name, data, {n});
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_writer_write(void* h, const char* path) {
+    try {
+        static_cast<llm::QuantWriter*>(h)->write(path);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// llm::QuantModel::load (src/quant.cpp:198-238): returns the number of layers
+// loaded, or -1 when the reference rejected the directory.
+int ref_quantmodel_layers(const char* dir, int kind) {
+    try {
+        llm::QuantModel m;
+        m.load(dir, kind == 0 ? llm::QKind::kInt8 : llm::QKind::kInt4);
+        return int(m.layers.size());
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
 }
