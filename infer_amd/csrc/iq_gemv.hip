@@ -133,7 +133,7 @@ __device__ __forceinline__ void pack_limbs(uint32_t u0, uint32_t u1, uint32_t u2
 // are v[] of the lane with j = lane % 16 (the 16 lanes of a DPP row hold the
 // whole group; all 16 must call this together).  Writes this lane's limb
 // bytes into the group's record `rec` (when `store`) and returns the group's
-// meta record {2^-k as fp32 bits, sum X0, sum X1, sum X2} (every lane).
+// meta record {2^-k as fp32 bits, sum X0, 256 sum X1 + sum X2, 0} (every lane).
 //
 // X = rint(x * 2^k) is formed as the bits of fma(x, 2^k, 1.5 * 2^23): with
 // |x * 2^k| <= 2^22 the sum lies in [2^23, 2^24], where the float's bits
@@ -196,7 +196,7 @@ __device__ __forceinline__ int4 convert_group(const float (&v)[8], int j, bool s
     }
     // 2^-k (NaN when the group holds a non-finite value, so it propagates)
     const float fx = fin ? __builtin_amdgcn_ldexpf(1.0f, -k0) : __builtin_nanf("");
-    return make_int4(__float_as_int(fx), sl[0], sl[1], sl[2]);
+    return make_int4(__float_as_int(fx), sl[0], (sl[1] << 8) + sl[2], 0);
 }
 
 // Columns [c0, c0 + 8) of an activation row, zero past K.  VECX: 0 scalar
@@ -293,12 +293,16 @@ __device__ __forceinline__ void weight_operands(const uint4* w, int4v_t& b0, int
     }
 }
 
-// fp32 value of one group's exact integer limb sums (t_L = S_L - z * sum X_L,
-// computed with 24-bit multiplies: |z| <= 15, |sum X_L| < 2^15), times the
-// weight scale and the activation factor 2^-k, added to acc.
+// fp32 value of one group's exact integer limb sums (t_L = S_L - z * sum X_L;
+// md = {2^-k, sum X0, 256 sum X1 + sum X2}, 24-bit multiplies: |z| <= 15,
+// |256 sum X1 + sum X2| < 2^23), times the weight scale and the activation
+// factor 2^-k, added to acc.
 __device__ __forceinline__ float combine(float acc, int d0, int d1, int d2, int z, int4 md, float s) {
-    const int t0 = d0 - __mul24(z, md.y), t1 = d1 - __mul24(z, md.z), t2 = d2 - __mul24(z, md.w);
-    const float v = __builtin_fmaf(float(t0), 65536.0f, __builtin_fmaf(float(t1), 256.0f, float(t2)));
+    // hi = t0, lo = 256 t1 + t2 exactly in int32 (|lo| < 2^30); float(lo)
+    // rounds once, as fma(t1, 256, t2) would
+    const int hi = d0 - __mul24(z, md.y);
+    const int lo = (d1 << 8) + d2 - __mul24(z, md.z);
+    const float v = __builtin_fmaf(float(hi), 65536.0f, float(lo));
     return __builtin_fmaf(v, s * __int_as_float(md.x), acc);
 }
 
@@ -720,6 +724,226 @@ __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
         }
 }
 
+// ------------------------------------------------------------------ 2..16 rows
+// Several activation rows (M <= 16 per launch; more rows run in blocks of
+// 16), K a multiple of 128.  Tile per wave: a workgroup copies the prepared
+// activations (byte limbs, xprep) of one K range once into LDS, in MFMA
+// operand order, then each wave runs over whole 16-row tiles on its own (no
+// cross-wave reduction), tile after tile and group after group, two halves
+// of D/2 groups of weights in flight (a half is multiplied while the other
+// half's loads are outstanding).  Every weight byte is read once per
+// launch.  The tile results go through LDS and are stored after the last
+// tile (a store between prefetches would make the later waits count it).
+// When the activations of all of K do not fit in LDS, K is split into S
+// ranges: workgroup (u, s) writes its range's sums to part[s][m][16*tile + n]
+// and gemvt_reduce_kernel adds the ranges.
+// A operand layouts: up to 12 rows, quad layout: A tile q row 4*mm + L =
+// limb L of activation row 4q + mm (rows 4*mm + 3 zero), two MFMAs per 128
+// columns give the three limb sums of four rows, lane (n = l%16, mm = l/16)
+// holding those of (row 4q + mm, output n).  13..16 rows, limb-major: A
+// tile L = limb L of the 16 rows (six MFMAs per group instead of eight),
+// lane (n, mm) holding rows 4*mm + i in D[i].
+constexpr int kGtTmax = 8;     // tiles per wave
+constexpr int kGtChunks = 16;  // staged 16-byte chunks per thread
+
+template <int KIND, int MQ, int D>
+__global__ __launch_bounds__(512) void gemvt_kernel(const GemvParams p) {
+    extern __shared__ __attribute__((aligned(16))) int4 gsm4[];
+    constexpr int WPG = KIND == 1 ? 1 : 2;
+    constexpr bool LM = MQ == 4;       // limb-major A
+    constexpr int NA = LM ? 3 : MQ;    // A tiles per 64 columns
+    constexpr int NACC = LM ? 4 : MQ;  // running sums per lane
+    constexpr int NM = MQ * 4;         // meta records per group
+    constexpr int CH = kGtChunks;
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KW = int(blockDim.x) >> 6;
+    const int G = int(p.G), M = p.M, S = p.S;
+    const int range = int(blockIdx.x) % S, u = int(blockIdx.x) / S;
+    const int NWu = int(gridDim.x) / S;
+    const int g0 = range * p.gs;
+    const int RG = (g0 + p.gs < G ? g0 + p.gs : G) - g0;  // groups of this range
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    int4* As = gsm4;                                      // [gs][NA][2][64]
+    int4* ms = As + p.gs * NA * 2 * 64;                   // [gs][NM]
+    float* outs = reinterpret_cast<float*>(ms + p.gs * NM);  // [KW][kGtTmax + 1][NACC][64]
+
+    // this wave's tiles: u*KW + wave + k*NWu*KW
+    const int tfirst = u * KW + wave, tstride = NWu * KW;
+    const int ntw = tfirst < p.ntiles ? (p.ntiles - 1 - tfirst) / tstride + 1 : 0;
+
+    // staging loads (A operands and meta records of the range)
+    const int total = RG * NA * 2 * 64;
+    int4 v[CH];
+    int4 mrec;
+    {
+        const rsrc_t rx = make_rsrc(p.xq, int64_t(M) * G * kLimbRec);
+        const rsrc_t rm = make_rsrc(p.meta, int64_t(G) * kMeta * 16);
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = tid + i * int(blockDim.x);
+            const int blk = c >> 6, l = c & 63;
+            const int gl = blk / (NA * 2), q = (blk >> 1) % NA, st = blk & 1;
+            const int m = LM ? (l & 15) : 4 * q + ((l & 15) >> 2), L = LM ? q : l & 3, kgl = l >> 4;
+            const bool ok = c < total && L < 3 && m < M;
+            const uint32_t off = uint32_t(m * G + g0 + gl) * kLimbRec + uint32_t(L * kGroup + st * 64 + kgl * 16);
+            v[i] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? off : kOob, 0, 0));
+        }
+        const int gl = tid / NM, mm = tid % NM;
+        const bool ok = tid < RG * NM && mm < M;
+        mrec = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rm, ok ? uint32_t((g0 + gl) * kMeta + mm) * 16 : kOob, 0, 0));
+    }
+
+    // loaded values are kept as loaded until their use (any operation on
+    // them in flight would make the loop wait for every load)
+    struct Buf {
+        int4v_t w[WPG];
+        uint32_t sc, zp;  // bf16 scale bits, zero point
+    };
+    // issue position: tile ordinal ik, group ig of the range (wave-uniform);
+    // the buffers are based at the issue tile's first row (empty past the
+    // wave's tiles) and refreshed when ik advances, so that the lane
+    // offsets stay fixed and the loads straight-line
+    int ik = 0, ig = 0;
+    rsrc_t rq, rs, rz;
+    const uint32_t vq = uint32_t(ln * row_bytes + kg * 16), vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
+    auto set_tile = [&]() {
+        const bool live = ik < ntw;
+        const int tile = tfirst + (live ? ik : 0) * tstride;
+        const TileSel ts = select_tile(p, tile < p.ntiles ? tile : p.ntiles - 1);
+        const int64_t rows = live ? ts.m.N - ts.row0 : 0;
+        rq = make_rsrc(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
+        rs = make_rsrc(ts.m.scales + ts.row0 * G, rows * G * 2);
+        rz = make_rsrc(ts.m.zeros ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+    };
+    set_tile();
+    auto issue = [&](Buf& bf) {
+        const int g = g0 + ig;
+#pragma unroll
+        for (int h = 0; h < WPG; h++)
+            bf.w[h] = __builtin_bit_cast(
+                int4v_t, __builtin_amdgcn_raw_buffer_load_b128(rq, vq, KIND == 1 ? g * 64 : g * 128 + h * 64, 0));
+        bf.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, g * 2, 0);
+        bf.zp = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz, g, 0) : 0u;
+        if (++ig == RG) {
+            ig = 0;
+            ++ik;
+            set_tile();
+        }
+    };
+
+    // The first half of the weights is requested before the staged values
+    // are written, the second after (when the staging registers are free).
+    constexpr int H = D / 2;
+    Buf buf[2][H];
+#pragma unroll
+    for (int i = 0; i < H; i++) issue(buf[0][i]);
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + i * int(blockDim.x);
+        if (c < total) As[c] = v[i];
+    }
+    if (tid < RG * NM) ms[tid] = mrec;
+#pragma unroll
+    for (int i = 0; i < H; i++) issue(buf[1][i]);
+    __syncthreads();  // A operands and meta staged
+
+    // H steps without branches (the scheduler interleaves them).  Steps past
+    // the wave's last tile multiply zero weights and scales; every step
+    // writes the running sums to an LDS slot, the tile's slot at its last
+    // group of the range and a spare slot otherwise.
+    float acc[NACC];
+#pragma unroll
+    for (int j = 0; j < NACC; j++) acc[j] = 0.0f;
+    int ck = 0, cg = 0;
+    auto compute_half = [&](const Buf (&hb)[H]) {
+#pragma unroll
+        for (int i = 0; i < H; i++) {
+            const Buf& bf = hb[i];
+            int4v_t b0, b1;
+            if (KIND == 1) {
+                b0 = bf.w[0] & 0x0F0F0F0F;
+                b1 = (bf.w[0] >> 4) & 0x0F0F0F0F;
+            } else {
+                b0 = bf.w[0];
+                b1 = bf.w[1];
+            }
+            const float sc = __uint_as_float(bf.sc << 16);
+            const int z = int(bf.zp);
+            const int4* ag = As + cg * (NA * 2 * 64) + lane;
+            const int4* mg = ms + cg * NM;
+            if (LM) {
+                int4v_t Dv[3];
+#pragma unroll
+                for (int L = 0; L < 3; L++) {
+                    Dv[L] = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * L) * 64]), b0, int4v_t{0, 0, 0, 0});
+                    Dv[L] = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * L + 1) * 64]), b1, Dv[L]);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[j] = combine(acc[j], Dv[0][j], Dv[1][j], Dv[2][j], z, mg[4 * kg + j], sc);
+            } else {
+#pragma unroll
+                for (int q = 0; q < MQ; q++) {
+                    int4v_t Dv = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * q) * 64]), b0, int4v_t{0, 0, 0, 0});
+                    Dv = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * q + 1) * 64]), b1, Dv);
+                    acc[q] = combine(acc[q], Dv[0], Dv[1], Dv[2], z, mg[4 * q + kg], sc);
+                }
+            }
+            const bool flush = cg == RG - 1;
+            const int slot = flush && ck < kGtTmax ? ck : kGtTmax;
+#pragma unroll
+            for (int j = 0; j < NACC; j++) {
+                outs[((wave * (kGtTmax + 1) + slot) * NACC + j) * 64 + lane] = acc[j];
+                acc[j] = flush ? 0.0f : acc[j];
+            }
+            cg = flush ? 0 : cg + 1;
+            ck += flush ? 1 : 0;
+        }
+    };
+    const int nsteps = ntw * RG;
+    for (int s0 = 0; s0 < nsteps; s0 += 2 * H) {
+        compute_half(buf[0]);
+#pragma unroll
+        for (int i = 0; i < H; i++) issue(buf[0][i]);
+        compute_half(buf[1]);
+#pragma unroll
+        for (int i = 0; i < H; i++) issue(buf[1][i]);
+    }
+
+    // results of this wave's tiles (its own LDS region: no barrier needed)
+    for (int k = 0; k < ntw; k++) {
+        const int tile = tfirst + k * tstride;
+        const TileSel ts = select_tile(p, tile);
+        const int64_t row = ts.row0 + ln;
+        const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
+        const uint32_t bb =
+            __builtin_amdgcn_raw_buffer_load_b16(rb, S == 1 && row < ts.m.N ? uint32_t(row) * 2 : kOob, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NACC; j++) {
+            const int m = LM ? 4 * kg + j : 4 * j + kg;
+            const float val = outs[((wave * (kGtTmax + 1) + k) * NACC + j) * 64 + lane];
+            if (m >= M || row >= ts.m.N) continue;
+            if (S == 1) ts.m.y[int64_t(m) * ts.m.N + row] = val + __uint_as_float(bb << 16);
+            else p.part[(int64_t(range) * M + m) * (int64_t(p.ntiles) * 16) + int64_t(tile) * 16 + ln] = val;
+        }
+    }
+}
+
+// y[m, n] = sum over ranges s of part[s][m][16*tile0 + n] (in range order)
+// + bias[n], for one matrix of a gemvt launch.
+__global__ __launch_bounds__(256) void gemvt_reduce_kernel(const float* __restrict__ part, int S, int M,
+                                                           int64_t ld, int64_t N,
+                                                           const uint16_t* __restrict__ bias,
+                                                           float* __restrict__ y) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(M) * N) return;
+    const int64_t m = i / N, n = i % N;
+    float sum = 0.0f;
+    for (int s = 0; s < S; s++) sum += part[(int64_t(s) * M + m) * ld + n];
+    y[i] = sum + (bias ? bf16_to_f32(bias[n]) : 0.0f);
+}
+
 // y[m, n] = sum over slices s of part[s, m, n] (in slice order) + bias[n].
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part, int S, int M, int64_t N,
                                                           const uint16_t* __restrict__ bias, float* __restrict__ y) {
@@ -908,8 +1132,118 @@ hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, floa
     return hipGetLastError();
 }
 
+// Plan of a gemvt launch (kw = 0: not applicable): K ranges of gs groups
+// whose activations take at most 96 KiB of LDS, one workgroup per CU, the
+// waves per workgroup that give the fewest idle tile slots.
+struct GtPlan {
+    int kw = 0, ks = 0, gs = 0, mq = 0, grid = 0;
+    size_t lds = 0;
+};
+
+GtPlan gemvt_plan(int64_t G, int tiles, int M, int cus) {
+    GtPlan pl;
+    const int mq = (M + 3) / 4, na = mq == 4 ? 3 : mq, nacc = mq == 4 ? 4 : mq;
+    const int rmax = 96 * 1024 / (na * 2048);
+    const int ks = int((G + rmax - 1) / rmax);
+    const int gs = int((G + ks - 1) / ks);
+    const int nwu = cus / ks > 0 ? cus / ks : 1;
+    const size_t fixed = size_t(gs) * na * 2048 + size_t(gs) * mq * 4 * 16;
+    double best = 0;
+    for (int kw = 2; kw <= 8; kw++) {
+        const size_t lds = fixed + size_t(kw) * (kGtTmax + 1) * nacc * 256;
+        if (lds > 160 * 1024) break;
+        if (int64_t(gs) * na * 128 > int64_t(kGtChunks) * 64 * kw || gs * mq * 4 > 64 * kw) continue;
+        const int waves = nwu * kw;
+        const int rounds = (tiles + waves - 1) / waves;
+        if (rounds > kGtTmax) continue;
+        const double eff = double(tiles) / (double(waves) * rounds);
+        if (eff > best + 1e-9) {
+            best = eff;
+            pl.kw = kw;
+            pl.lds = lds;
+        }
+    }
+    if (!pl.kw) return pl;
+    pl.ks = ks;
+    pl.gs = gs;
+    pl.mq = mq;
+    pl.grid = nwu * ks;
+    return pl;
+}
+
+template <int KIND>
+void launch_gemvt_k(const GemvParams& p, const GtPlan& pl, hipStream_t stream) {
+    constexpr int D = KIND == 1 ? 16 : 10;  // ~100 VGPRs of weights in flight
+    static const bool attr = [] {
+        // up to 160 KiB of dynamic LDS
+        const void* fns[4] = {reinterpret_cast<const void*>(&gemvt_kernel<KIND, 1, D>),
+                              reinterpret_cast<const void*>(&gemvt_kernel<KIND, 2, D>),
+                              reinterpret_cast<const void*>(&gemvt_kernel<KIND, 3, D>),
+                              reinterpret_cast<const void*>(&gemvt_kernel<KIND, 4, D>)};
+        for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        return true;
+    }();
+    (void)attr;
+    switch (pl.mq) {
+        case 1: gemvt_kernel<KIND, 1, D><<<pl.grid, 64 * pl.kw, pl.lds, stream>>>(p); break;
+        case 2: gemvt_kernel<KIND, 2, D><<<pl.grid, 64 * pl.kw, pl.lds, stream>>>(p); break;
+        case 3: gemvt_kernel<KIND, 3, D><<<pl.grid, 64 * pl.kw, pl.lds, stream>>>(p); break;
+        default: gemvt_kernel<KIND, 4, D><<<pl.grid, 64 * pl.kw, pl.lds, stream>>>(p); break;
+    }
+}
+
+// Batched GEMV with gemvt on n matrices sharing K (false: shape not covered).
+bool launch_gemvt(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
+                  hipStream_t stream, hipError_t* err) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    if (K % kGroup) return false;
+    const int tiles = total_tiles(W, n);
+    const int cus = device_cu_count();
+    for (int r0 = 0; r0 < M; r0 += 16) {
+        const int mb = M - r0 < 16 ? M - r0 : 16;
+        const GtPlan pl = gemvt_plan(G, tiles, mb, cus);
+        if (!pl.kw || (pl.ks > 1 && int64_t(pl.ks) * mb * tiles * 16 > kPartialFloats)) {
+            if (r0 == 0) return false;
+            *err = hipErrorInvalidValue;  // a block after the first cannot fall back
+            return true;
+        }
+        GemvParams p{};
+        int t0 = 0;
+        for (int i = 0; i < n; i++) {
+            p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i] + int64_t(r0) * W[i].rows,
+                              W[i].rows, t0};
+            t0 += int((W[i].rows + 15) / 16);
+        }
+        p.nmat = n;
+        p.K = K;
+        p.G = G;
+        p.xq = ws->xq + int64_t(r0) * G * kLimbRec;
+        p.meta = ws->xmeta + r0;
+        p.part = ws->partials;
+        p.M = mb;
+        p.S = pl.ks;
+        p.gs = pl.gs;
+        p.ntiles = tiles;
+        if (W[0].kind == 1) launch_gemvt_k<1>(p, pl, stream);
+        else launch_gemvt_k<0>(p, pl, stream);
+        if (pl.ks > 1) {
+            for (int i = 0; i < n; i++) {
+                const int64_t cnt = int64_t(mb) * W[i].rows;
+                gemvt_reduce_kernel<<<unsigned((cnt + 255) / 256), 256, 0, stream>>>(
+                    ws->partials + int64_t(p.mat[i].tile0) * 16, pl.ks, mb, int64_t(tiles) * 16, W[i].rows,
+                    bias[i], y[i] + int64_t(r0) * W[i].rows);
+            }
+        }
+        *err = hipGetLastError();
+        if (*err != hipSuccess) return true;
+    }
+    return true;
+}
+
 hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                                 Workspace* ws, hipStream_t stream) {
+    hipError_t e = hipSuccess;
+    if (launch_gemvt(W, bias, y, n, M, ws, stream, &e)) return e;
     for (int i = 0; i < n; i++) {
         const hipError_t e = launch_gemv_batched(W[i], bias[i], M, y[i], ws, stream);
         if (e != hipSuccess) return e;

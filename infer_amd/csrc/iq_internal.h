@@ -27,7 +27,7 @@ struct Workspace {
     size_t bytes = 0;
     float* xf = nullptr;       // [kMaxKp] fp32: 1-row activation copied by a prep
     int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs
-    int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {k, sum X0, sum X1, sum X2}
+    int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, sum X0, 256 sum X1 + sum X2, 0}
     float* partials = nullptr; // kPartialFloats
     // Shape of the activations last prepared into xq/xmeta (host-side record).
     int prep_M = 0;
