@@ -1016,6 +1016,15 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
         maxw = kind == 1 ? 16 : 8;
         pl.gs = int((G + maxw - 1) / maxw);
         if (mode == 2) pl.gs = (pl.gs + 3) / 4 * 4;
+        // the smallest instance that holds the slice: every slot past the
+        // slice is an out-of-range request, and those still occupy the
+        // memory pipeline
+        const int caps[3] = {4, 8, 12};
+        for (int c : caps)
+            if (pl.gs <= c && c < pl.ng) {
+                pl.ng = c;
+                break;
+            }
     }
     pl.grid = (ntiles + pl.tpw - 1) / pl.tpw;
     if (pl.gs > G) pl.gs = int(G);
@@ -1062,9 +1071,14 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     const unsigned grid = unsigned(pl.grid);
     if (W[0].kind == 1) {
         if (pl.tpw > 1) launch_gemv1_tpw<1, 8>(p, mode, pl.ks, pl.tpw, grid, lds, stream);
+        else if (pl.ng == 4) launch_gemv1_m<1, 4, 1, 16>(p, mode, pl.ks, grid, lds, stream);
+        else if (pl.ng == 8) launch_gemv1_m<1, 8, 1, 16>(p, mode, pl.ks, grid, lds, stream);
         else launch_gemv1_m<1, 12, 1, 16>(p, mode, pl.ks, grid, lds, stream);
     } else {
         if (pl.tpw > 1) launch_gemv1_tpw<0, 4>(p, mode, pl.ks, pl.tpw, grid, lds, stream);
+        else if (pl.ng == 4) launch_gemv1_m<0, 4, 1, 8>(p, mode, pl.ks, grid, lds, stream);
+        else if (pl.ng == 8) launch_gemv1_m<0, 8, 1, 8>(p, mode, pl.ks, grid, lds, stream);
+        else if (pl.ng == 12) launch_gemv1_m<0, 12, 1, 8>(p, mode, pl.ks, grid, lds, stream);
         else launch_gemv1_m<0, 20, 1, 8>(p, mode, pl.ks, grid, lds, stream);
     }
     return hipGetLastError();
