@@ -982,51 +982,35 @@ int gemv1_mode(int64_t K, int64_t G, const float* x) {
 }
 
 // Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
-// (ks), the slice capacity NG of the kernel instance and whether workgroups
-// walk several tiles with prefetch (pf).
+// (ks), the slice capacity NG of the kernel instance, the grid and the tiles
+// per workgroup (tpw, 1 with the instances built here).
 struct G1Plan {
     int gs, ks, ng, grid, tpw;
 };
 
-// Kernel instances: (slice capacity NG, tiles per workgroup TPW, max waves
-// per workgroup).  All TPW slices of a wave are requested at the start, so
-// TPW * NG bounds the registers held by weights in flight:
-//   several tiles per workgroup (TPW 2..5): int4 (8, 8), int8 (4, 8) --
-//     128 B of weights per lane per tile, up to 256 VGPRs (2 waves / SIMD);
-//   one tile per workgroup: int4 (12, 16), int8 (20, 8).
-// ng = 0 when the 1-row kernel does not apply (the slices would exceed the
-// capacity, or the LDS copy of the converted row would exceed 64 KiB).
-// TPW aims at one workgroup per CU holding every tile (at most 5).
+// Kernel instances: one 16-row tile per workgroup (measured faster than
+// workgroups walking several tiles: the hardware dispatcher keeps every CU
+// fed, and each wave requests its whole slice at once); slice capacity NG
+// in {4, 8, 12} (int4, up to 16 waves) or {4, 8, 12, 20} (int8, up to 8
+// waves): the smallest that holds the slice, since every slot past the
+// slice would be an out-of-range request, and those still occupy the
+// memory pipeline.  ng = 0 when the 1-row kernel does not apply (the
+// slices would exceed the capacity, or the LDS copy of the converted row
+// would exceed 64 KiB).
 G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
+    (void)cus;
     G1Plan pl{0, 0, 0, 0, 1};
     if (G * (kLimbRec + 16) > 64 * 1024) return pl;
-    const int wpc = 1;
-    const int small = kind == 1 ? 8 : 4;
-    int per_wg = (ntiles + cus * wpc - 1) / (cus * wpc);  // tiles per workgroup
-    if (per_wg > 5) per_wg = 5;
-    int maxw;
-    if (per_wg > 1 && G <= int64_t(small) * 8) {
-        pl.ng = small;
-        pl.tpw = per_wg;
-        pl.gs = small;
-        maxw = 8;
-    } else {
-        pl.ng = kind == 1 ? 12 : 20;
-        pl.tpw = 1;
-        maxw = kind == 1 ? 16 : 8;
-        pl.gs = int((G + maxw - 1) / maxw);
-        if (mode == 2) pl.gs = (pl.gs + 3) / 4 * 4;
-        // the smallest instance that holds the slice: every slot past the
-        // slice is an out-of-range request, and those still occupy the
-        // memory pipeline
-        const int caps[3] = {4, 8, 12};
-        for (int c : caps)
-            if (pl.gs <= c && c < pl.ng) {
-                pl.ng = c;
-                break;
-            }
-    }
-    pl.grid = (ntiles + pl.tpw - 1) / pl.tpw;
+    const int maxw = kind == 1 ? 16 : 8;
+    pl.ng = kind == 1 ? 12 : 20;
+    pl.gs = int((G + maxw - 1) / maxw);
+    if (mode == 2) pl.gs = (pl.gs + 3) / 4 * 4;
+    for (int c : {4, 8, 12})
+        if (pl.gs <= c && c < pl.ng) {
+            pl.ng = c;
+            break;
+        }
+    pl.grid = ntiles;
     if (pl.gs > G) pl.gs = int(G);
     pl.ks = int((G + pl.gs - 1) / pl.gs);
     if (pl.gs > pl.ng || pl.ks > maxw) pl.ng = 0;
@@ -1038,16 +1022,6 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
     if (mode == 2) gemv1_kernel<KIND, NG, 2, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
     else if (mode == 1) gemv1_kernel<KIND, NG, 1, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
     else gemv1_kernel<KIND, NG, 0, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
-}
-
-template <int KIND, int NG>
-void launch_gemv1_tpw(const GemvParams& p, int mode, int ks, int tpw, unsigned grid, size_t lds, hipStream_t stream) {
-    switch (tpw) {
-        case 2: launch_gemv1_m<KIND, NG, 2, 8>(p, mode, ks, grid, lds, stream); break;
-        case 3: launch_gemv1_m<KIND, NG, 3, 8>(p, mode, ks, grid, lds, stream); break;
-        case 4: launch_gemv1_m<KIND, NG, 4, 8>(p, mode, ks, grid, lds, stream); break;
-        default: launch_gemv1_m<KIND, NG, 5, 8>(p, mode, ks, grid, lds, stream); break;
-    }
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
@@ -1070,13 +1044,11 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     const size_t lds = size_t(G) * (kLimbRec + 16);
     const unsigned grid = unsigned(pl.grid);
     if (W[0].kind == 1) {
-        if (pl.tpw > 1) launch_gemv1_tpw<1, 8>(p, mode, pl.ks, pl.tpw, grid, lds, stream);
-        else if (pl.ng == 4) launch_gemv1_m<1, 4, 1, 16>(p, mode, pl.ks, grid, lds, stream);
+        if (pl.ng == 4) launch_gemv1_m<1, 4, 1, 16>(p, mode, pl.ks, grid, lds, stream);
         else if (pl.ng == 8) launch_gemv1_m<1, 8, 1, 16>(p, mode, pl.ks, grid, lds, stream);
         else launch_gemv1_m<1, 12, 1, 16>(p, mode, pl.ks, grid, lds, stream);
     } else {
-        if (pl.tpw > 1) launch_gemv1_tpw<0, 4>(p, mode, pl.ks, pl.tpw, grid, lds, stream);
-        else if (pl.ng == 4) launch_gemv1_m<0, 4, 1, 8>(p, mode, pl.ks, grid, lds, stream);
+        if (pl.ng == 4) launch_gemv1_m<0, 4, 1, 8>(p, mode, pl.ks, grid, lds, stream);
         else if (pl.ng == 8) launch_gemv1_m<0, 8, 1, 8>(p, mode, pl.ks, grid, lds, stream);
         else if (pl.ng == 12) launch_gemv1_m<0, 12, 1, 8>(p, mode, pl.ks, grid, lds, stream);
         else launch_gemv1_m<0, 20, 1, 8>(p, mode, pl.ks, grid, lds, stream);
