@@ -736,7 +736,7 @@ __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
 // tile (a store between prefetches would make the later waits count it).
 // When the activations of all of K do not fit in LDS, K is split into S
 // ranges: workgroup (u, s) writes its range's sums to part[s][m][16*tile + n]
-// and gemvt_reduce_kernel adds the ranges.
+// and gemvt_reduce_kernel adds the ranges of every matrix in one launch.
 // A operand layouts: up to 12 rows, quad layout: A tile q row 4*mm + L =
 // limb L of activation row 4q + mm (rows 4*mm + 3 zero), two MFMAs per 128
 // columns give the three limb sums of four rows, lane (n = l%16, mm = l/16)
@@ -930,18 +930,21 @@ __global__ __launch_bounds__(512) void gemvt_kernel(const GemvParams p) {
     }
 }
 
-// y[m, n] = sum over ranges s of part[s][m][16*tile0 + n] (in range order)
-// + bias[n], for one matrix of a gemvt launch.
-__global__ __launch_bounds__(256) void gemvt_reduce_kernel(const float* __restrict__ part, int S, int M,
-                                                           int64_t ld, int64_t N,
-                                                           const uint16_t* __restrict__ bias,
-                                                           float* __restrict__ y) {
+// y_i[m, n] = sum over ranges s of part[s][m][16*tile0_i + n] (in range
+// order) + bias_i[n], for every matrix i of a gemvt launch in one grid
+// (thread i covers (m, tile row) over all matrices' tiles).
+__global__ __launch_bounds__(256) void gemvt_reduce_kernel(const GemvParams p) {
+    const int64_t ld = int64_t(p.ntiles) * 16;
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= int64_t(M) * N) return;
-    const int64_t m = i / N, n = i % N;
+    if (i >= int64_t(p.M) * ld) return;
+    const int m = int(i / ld);
+    const int64_t c = i - int64_t(m) * ld;
+    const TileSel ts = select_tile(p, int(c >> 4));
+    const int64_t row = ts.row0 + (c & 15);
+    if (row >= ts.m.N) return;
     float sum = 0.0f;
-    for (int s = 0; s < S; s++) sum += part[(int64_t(s) * M + m) * ld + n];
-    y[i] = sum + (bias ? bf16_to_f32(bias[n]) : 0.0f);
+    for (int s = 0; s < p.S; s++) sum += p.part[(int64_t(s) * p.M + m) * ld + c];
+    ts.m.y[int64_t(m) * ts.m.N + row] = sum + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
 }
 
 // y[m, n] = sum over slices s of part[s, m, n] (in slice order) + bias[n].
@@ -1213,12 +1216,8 @@ bool launch_gemvt(const QView* W, const uint16_t* const* bias, float* const* y, 
         if (W[0].kind == 1) launch_gemvt_k<1>(p, pl, stream);
         else launch_gemvt_k<0>(p, pl, stream);
         if (pl.ks > 1) {
-            for (int i = 0; i < n; i++) {
-                const int64_t cnt = int64_t(mb) * W[i].rows;
-                gemvt_reduce_kernel<<<unsigned((cnt + 255) / 256), 256, 0, stream>>>(
-                    ws->partials + int64_t(p.mat[i].tile0) * 16, pl.ks, mb, int64_t(tiles) * 16, W[i].rows,
-                    bias[i], y[i] + int64_t(r0) * W[i].rows);
-            }
+            const int64_t cnt = int64_t(mb) * tiles * 16;
+            gemvt_reduce_kernel<<<unsigned((cnt + 255) / 256), 256, 0, stream>>>(p);
         }
         *err = hipGetLastError();
         if (*err != hipSuccess) return true;
