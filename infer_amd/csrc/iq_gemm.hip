@@ -17,13 +17,15 @@
 // Block order is XCD-aware: consecutive tiles along the activation rows of
 // one weight-column block land on the same XCD, so a weight tile is fetched
 // from HBM once per XCD and re-read from that XCD's L2.
+#include <type_traits>
+
 #include "iq_internal.h"
 
 namespace iq {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, LDSW = BK + 8;  // LDS row pitch (bf16)
+constexpr int BM = 128, BK = 64, LDSW = BK + 8;  // LDS row pitch (bf16)
 constexpr int kThreads = 256;
 
 struct GemmParams {
@@ -47,8 +49,11 @@ __device__ __forceinline__ uint32_t bf16_pair_int(int a, int b) {
     return bf16_pair_from_f32(float(a), float(b));
 }
 
-template <int KIND, bool XF32, bool FASTW, bool FASTX>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
+// NJ: 32-column MFMA tiles per wave along the output features (tile width
+// BN = 64 NJ): 2 for wide matrices, 1 when 128-wide tiles would leave CUs idle.
+template <int KIND, bool XF32, bool FASTW, bool FASTX, int NJ>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
+    constexpr int BN = 64 * NJ;
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t Al[XF32 ? 2 : 1][XF32 ? BM : 1][LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][LDSW];
@@ -70,69 +75,93 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
 
     // ---- register staging of one K step
     constexpr int XCH = XF32 ? 8 : 4;           // 16-byte activation chunks per thread
-    constexpr int WCH = KIND == 1 ? 1 : 2;      // 16-byte weight chunks per thread
-    uint4 xr[XCH];
-    uint4 wr[WCH];
-    uint32_t zr = 0;
+    constexpr int WCH = KIND == 1 ? 1 : NJ;     // 16-byte weight chunks per thread
+    struct Regs {
+        uint4 xr[XCH];
+        uint4 wr[WCH];
+        uint32_t zr;
+    };
+    Regs r0, r1;
 
-    auto load_step = [&](int kt) {
+    // Per-thread source rows, fixed for the whole K loop (a step adds its
+    // column offset): the fast paths need no per-step bounds arithmetic.
+    const uint8_t* wrow[WCH];
+    const uint8_t* zrow = nullptr;
+    bool wok[WCH];
+    int wcol[WCH];
+#pragma unroll
+    for (int i = 0; i < WCH; i++) {
+        const int c = tid + kThreads * i;
+        const int row = KIND == 1 ? c >> 1 : c >> 2;
+        const int64_t n = n0 + row;
+        wok[i] = row < BN && n < p.N;
+        wrow[i] = p.q + (wok[i] ? n : 0) * row_bytes;
+        wcol[i] = KIND == 1 ? (c & 1) * 16 : (c & 3) * 16;  // byte offset inside the step
+        if (KIND == 1) zrow = p.zeros + (wok[i] ? n : 0) * p.G;
+    }
+    const void* xrow[XCH];
+    bool xok[XCH];
+    int xcol[XCH];
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+        const int c = tid + kThreads * i;
+        const int row = XF32 ? c >> 4 : c >> 3;
+        const int64_t m = m0 + row;
+        xok[i] = m < p.T;
+        xrow[i] = XF32 ? static_cast<const void*>(p.xf + (xok[i] ? m : 0) * p.K)
+                       : static_cast<const void*>(p.xb + (xok[i] ? m : 0) * p.K);
+        xcol[i] = XF32 ? (c & 15) * 4 : (c & 7) * 8;  // element offset inside the step
+    }
+
+    auto load_step = [&](Regs& rg, int kt) {
+        uint4* xr = rg.xr;
+        uint4* wr = rg.wr;
+        uint32_t& zr = rg.zr;
         const int64_t k0 = int64_t(kt) * BK;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
-            const int c = tid + kThreads * i;
-            if (XF32) {
-                const int row = c >> 4, kc = c & 15;  // 16 chunks of 4 floats per row
-                const int64_t m = m0 + row, k = k0 + kc * 4;
-                if (m < p.T && FASTX) {
-                    xr[i] = *reinterpret_cast<const uint4*>(p.xf + m * p.K + k);
-                } else {
-                    float f[4];
+            const int64_t k = k0 + xcol[i];
+            if (FASTX) {
+                xr[i] = xok[i] ? (XF32 ? *reinterpret_cast<const uint4*>(static_cast<const float*>(xrow[i]) + k)
+                                       : *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xrow[i]) + k))
+                               : make_uint4(0, 0, 0, 0);
+            } else if (XF32) {
+                const float* xp = static_cast<const float*>(xrow[i]);
+                float f[4];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) f[e] = (m < p.T && k + e < p.K) ? p.xf[m * p.K + k + e] : 0.0f;
-                    xr[i] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
-                }
+                for (int e = 0; e < 4; e++) f[e] = (xok[i] && k + e < p.K) ? xp[k + e] : 0.0f;
+                xr[i] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
             } else {
-                const int row = c >> 3, kc = c & 7;  // 8 chunks of 8 bf16 per row
-                const int64_t m = m0 + row, k = k0 + kc * 8;
-                if (m < p.T && FASTX) {
-                    xr[i] = *reinterpret_cast<const uint4*>(p.xb + m * p.K + k);
-                } else {
-                    uint32_t h[4] = {0, 0, 0, 0};
+                const uint16_t* xp = static_cast<const uint16_t*>(xrow[i]);
+                uint32_t h[4] = {0, 0, 0, 0};
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        if (m < p.T && k + e < p.K) h[e / 2] |= uint32_t(p.xb[m * p.K + k + e]) << (16 * (e & 1));
-                    xr[i] = make_uint4(h[0], h[1], h[2], h[3]);
-                }
+                for (int e = 0; e < 8; e++)
+                    if (xok[i] && k + e < p.K) h[e / 2] |= uint32_t(xp[k + e]) << (16 * (e & 1));
+                xr[i] = make_uint4(h[0], h[1], h[2], h[3]);
             }
         }
 #pragma unroll
         for (int i = 0; i < WCH; i++) {
-            const int c = tid + kThreads * i;
-            int row, kc;
-            int64_t off;
-            if (KIND == 1) { row = c >> 1; kc = c & 1; off = (k0 + kc * 32) / 2; }
-            else { row = c >> 2; kc = c & 3; off = k0 + kc * 16; }
-            const int64_t n = n0 + row;
-            if (n < p.N) {
-                const uint8_t* qr = p.q + n * row_bytes;
-                if (FASTW) {
-                    wr[i] = *reinterpret_cast<const uint4*>(qr + off);
-                } else {
-                    uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-                    for (int e = 0; e < 16; e++)
-                        if (off + e < row_bytes) w[e / 4] |= uint32_t(qr[off + e]) << (8 * (e % 4));
-                    wr[i] = make_uint4(w[0], w[1], w[2], w[3]);
-                }
-                if (KIND == 1) zr = p.zeros[n * p.G + k0 / kGroup];
-            } else {
+            const int64_t off = (KIND == 1 ? k0 / 2 : k0) + wcol[i];
+            if (!wok[i]) {
                 wr[i] = make_uint4(0, 0, 0, 0);
-                zr = 0;
+            } else if (FASTW) {
+                wr[i] = *reinterpret_cast<const uint4*>(wrow[i] + off);
+            } else {
+                uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (off + e < row_bytes) w[e / 4] |= uint32_t(wrow[i][off + e]) << (8 * (e % 4));
+                wr[i] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
+        zr = (KIND == 1 && wok[0]) ? zrow[k0 / kGroup] : 0u;
     };
 
-    auto store_step = [&](int buf) {
+    auto store_step = [&](const Regs& rg, int buf) {
+        const uint4* xr = rg.xr;
+        const uint4* wr = rg.wr;
+        const uint32_t zr = rg.zr;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const int c = tid + kThreads * i;
@@ -159,6 +188,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
         for (int i = 0; i < WCH; i++) {
             const int c = tid + kThreads * i;
             const uint32_t d[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+            if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;  // int4 at BN = 64: half the threads
             if (KIND == 1) {
                 const int row = c >> 1, kc = c & 1;
                 const int z = int(zr);
@@ -193,71 +223,94 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
         }
     };
 
-    float16_t acc[2][2], P[2][2];
+    float16_t acc[2][NJ], P[2][NJ];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) { acc[i][j][r] = 0.0f; P[i][j][r] = 0.0f; }
 
     // Scale row pointers of this lane's two output columns.
-    int64_t ncol[2];
-    bool nval[2];
+    int64_t ncol[NJ];
+    bool nval[NJ];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        ncol[j] = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < NJ; j++) {
+        ncol[j] = n0 + wn * (32 * NJ) + j * 32 + (lane & 31);
         nval[j] = ncol[j] < p.N;
     }
 
-    load_step(0);
-    store_step(0);
+    // Scales of this lane's two output columns: group g's are requested a
+    // group ahead (a load waited on at the group's close would stall every
+    // second step).
+    auto load_scales = [&](int64_t g, float (&s)[NJ]) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) s[j] = (nval[j] && g < p.G) ? bf16_to_f32(p.scales[ncol[j] * p.G + g]) : 0.0f;
+    };
+    float s_cur[NJ], s_nxt[NJ];
+    load_scales(0, s_cur);
+    load_scales(1, s_nxt);
+
+    // Pipeline: while step kt is multiplied from LDS buffer kt & 1, the
+    // registers of one set hold step kt + 1 (stored into the other buffer
+    // after the MFMAs) and those of the other set step kt + 2 (requested one
+    // step earlier), so global loads have two steps to arrive.
+    load_step(r0, 0);
+    store_step(r0, 0);
+    if (nk > 1) load_step(r1, 1);
+    if (nk > 2) load_step(r0, 2);
     __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_step(kt + 1);
+    // PAR = kt & 1, fixed at compile time (the loop below alternates).
+    auto step = [&](auto par, int kt, Regs& rnext, Regs& rlater) {
+        constexpr int PAR = decltype(par)::value;
+        const int buf = PAR;
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
             const int kof = ks * 16 + 8 * (lane >> 5);
-            bf16x8_t a[2], al[2], bw[2];
+            bf16x8_t a[2], al[2], bw[NJ];
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * 64 + i * 32 + (lane & 31)][kof]);
                 if (XF32) al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[XF32 ? buf : 0][XF32 ? wm * 64 + i * 32 + (lane & 31) : 0][kof]);
             }
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                bw[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][wn * 64 + j * 32 + (lane & 31)][kof]);
+            for (int j = 0; j < NJ; j++)
+                bw[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][wn * (32 * NJ) + j * 32 + (lane & 31)][kof]);
+            // the group's first k slice starts its partial sums from zero
+            const bool first = PAR == 0 && ks == 0;
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    P[i][j] = mfma32_bf16(a[i], bw[j], P[i][j]);
+                for (int j = 0; j < NJ; j++) {
+                    P[i][j] = mfma32_bf16(a[i], bw[j], first ? float16_t{} : P[i][j]);
                     if (XF32) P[i][j] = mfma32_bf16(al[i], bw[j], P[i][j]);
                 }
         }
         // Close the 128-column group after its second 64-column step (or at the end).
-        if ((kt & 1) || kt + 1 == nk) {
-            const int64_t g = kt / 2;
+        if (PAR == 1 || kt + 1 == nk) {
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const float s = nval[j] ? bf16_to_f32(p.scales[ncol[j] * p.G + g]) : 0.0f;
+            for (int j = 0; j < NJ; j++) {
 #pragma unroll
                 for (int i = 0; i < 2; i++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        acc[i][j][r] = __builtin_fmaf(s, P[i][j][r], acc[i][j][r]);
-                        P[i][j][r] = 0.0f;
-                    }
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = __builtin_fmaf(s_cur[j], P[i][j][r], acc[i][j][r]);
+                s_cur[j] = s_nxt[j];
             }
+            load_scales(kt / 2 + 2, s_nxt);
         }
-        if (kt + 1 < nk) store_step(buf ^ 1);
+        if (kt + 1 < nk) store_step(rnext, buf ^ 1);
+        if (kt + 3 < nk) load_step(rnext, kt + 3);
         __syncthreads();
+        (void)rlater;
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(std::integral_constant<int, 0>{}, kt, r1, r0);
+        if (kt + 1 < nk) step(std::integral_constant<int, 1>{}, kt + 1, r0, r1);
     }
 
     // Epilogue: lane holds rows m = 8*(r/4) + 4*(lane/32) + r%4 of each 32x32 tile.
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NJ; j++) {
         if (!nval[j]) continue;
         const float bv = p.bias ? bf16_to_f32(p.bias[ncol[j]]) : 0.0f;
 #pragma unroll
@@ -270,13 +323,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p) {
     }
 }
 
-template <int KIND, bool XF32>
+template <int KIND, bool XF32, int NJ>
 void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
     const unsigned grid = unsigned(p.tiles_m * p.tiles_n);
-    if (fastw && fastx) gemm_kernel<KIND, XF32, true, true><<<grid, kThreads, 0, stream>>>(p);
-    else if (fastw) gemm_kernel<KIND, XF32, true, false><<<grid, kThreads, 0, stream>>>(p);
-    else if (fastx) gemm_kernel<KIND, XF32, false, true><<<grid, kThreads, 0, stream>>>(p);
-    else gemm_kernel<KIND, XF32, false, false><<<grid, kThreads, 0, stream>>>(p);
+    if (fastw && fastx) gemm_kernel<KIND, XF32, true, true, NJ><<<grid, kThreads, 0, stream>>>(p);
+    else if (fastw) gemm_kernel<KIND, XF32, true, false, NJ><<<grid, kThreads, 0, stream>>>(p);
+    else if (fastx) gemm_kernel<KIND, XF32, false, true, NJ><<<grid, kThreads, 0, stream>>>(p);
+    else gemm_kernel<KIND, XF32, false, false, NJ><<<grid, kThreads, 0, stream>>>(p);
+}
+
+template <int KIND, bool XF32>
+void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
+    // 128-wide tiles unless they leave CUs without two workgroups to run
+    const int t128 = p.tiles_m * int((p.N + 127) / 128);
+    if (t128 >= 2 * device_cu_count()) {
+        p.tiles_n = int((p.N + 127) / 128);
+        launch_gemm_t<KIND, XF32, 2>(p, fastw, fastx, stream);
+    } else {
+        p.tiles_n = int((p.N + 63) / 64);
+        launch_gemm_t<KIND, XF32, 1>(p, fastw, fastx, stream);
+    }
 }
 
 }  // namespace
@@ -288,16 +354,15 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
     p.T = T; p.N = W.rows; p.K = W.cols; p.G = W.groups;
     p.tiles_m = int((T + BM - 1) / BM);
-    p.tiles_n = int((p.N + BN - 1) / BN);
     const bool fastw = (p.K % kGroup == 0);
     const uintptr_t xa = x_f32 ? reinterpret_cast<uintptr_t>(x_f32) : reinterpret_cast<uintptr_t>(x_bf16);
     const bool fastx = (p.K % BK == 0) && (xa % 16 == 0);
     if (x_f32) {
-        if (W.kind == 1) launch_gemm_t<1, true>(p, fastw, fastx, stream);
-        else launch_gemm_t<0, true>(p, fastw, fastx, stream);
+        if (W.kind == 1) launch_gemm_nj<1, true>(p, fastw, fastx, stream);
+        else launch_gemm_nj<0, true>(p, fastw, fastx, stream);
     } else {
-        if (W.kind == 1) launch_gemm_t<1, false>(p, fastw, fastx, stream);
-        else launch_gemm_t<0, false>(p, fastw, fastx, stream);
+        if (W.kind == 1) launch_gemm_nj<1, false>(p, fastw, fastx, stream);
+        else launch_gemm_nj<0, false>(p, fastw, fastx, stream);
     }
     return hipGetLastError();
 }
