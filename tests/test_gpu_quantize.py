@@ -73,3 +73,40 @@ def test_quantize_7b_shapes_bit_exact(kind):
         assert np.array_equal(q, rq)
         if kind == 1:
             assert np.array_equal(z, rz)
+
+
+def _tie_rows(kind):
+    """Groups built on exact half-integer quotients w / s = c + 1/2 (the
+    round-half-even cases of lrint), over scales from 2^-133 (bf16 subnormal)
+    to 2^100, plus every bf16 bit pattern (NaN, inf, subnormals) in groups."""
+    groups = []
+    for e in list(range(-140, -120)) + list(range(-80, -60, 3)) + [-20, -7, 0, 3, 50, 100]:
+        p2 = np.float32(2.0) ** np.float32(e) if e > -127 else np.float32(np.ldexp(1.0, e))
+        if kind == 0:
+            c = np.arange(-127, 1, dtype=np.float32)  # 128 values: ties c + 1/2 and the max 127
+            vals = (c + np.float32(0.5)) * p2
+            vals[0] = np.float32(127.0) * p2
+        else:
+            k = np.arange(-14, 114, dtype=np.float32)  # (k / 2) s with range 15 s, zero point ~7
+            vals = (k / np.float32(2.0) - np.float32(7.0)) * p2
+            vals[0], vals[1] = np.float32(-7.5) * p2, np.float32(7.5) * p2
+        groups.append(O.f32_to_bf16(vals.astype(np.float32)))
+    rng = np.random.default_rng(7)
+    allbits = np.arange(65536, dtype=np.uint16)
+    groups += list(allbits.reshape(-1, 128))
+    groups += list(rng.permutation(allbits).reshape(-1, 128))
+    while len(groups) % 4:
+        groups.append(np.zeros(128, np.uint16))
+    return np.stack(groups).reshape(-1, 128 * 4)  # rows of four groups
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_quantize_ties_and_extreme_scales(kind):
+    w = _tie_rows(kind)
+    say("quantize ties/extremes", kind, w.shape)
+    q, s, z = gpu_quantize(w, kind)
+    rq, rs, rz = O.quantize(w, kind)
+    assert np.array_equal(s, rs)
+    assert np.array_equal(q, rq)
+    if kind == 1:
+        assert np.array_equal(z, rz)
