@@ -1225,6 +1225,282 @@ bool launch_gemvt(const QView* W, const uint16_t* const* bias, float* const* y, 
     return true;
 }
 
+// ------------------------------------------------------------------ 2..32 rows, f16 split
+// Activations as two f16 terms, weights as exact f16 integers, on
+// v_mfma_f32_16x16x32_f16.  Per (activation row m, 128-column group g):
+// 2^k with max|x| 2^k in [2^14, 2^15), v = x 2^k (exact), hi = f16(v),
+// lo = f16(v - hi); |v - hi - lo| <= 2^-22 max|v| (hi has 11 significant
+// bits, v - hi is exact in fp32 and lo keeps 11 more), so the error per
+// value is within 2^-22 of the group maximum, as with the byte limbs.  The
+// weights enter as q (int8) or q - z (int4), integers f16 holds exactly, so
+// every product is exact and the matrix core accumulates in fp32; per group
+// the kernel adds D * (s * 2^-k) to the running sums.
+//
+// Prepared layout (xhprep): per block of 16 rows b and group g, 8 KiB =
+// [MFMA k-chunk j = 0..3][term hi, lo][lane 0..63][8 f16], lane l = (row
+// i = l % 16, q = l / 16) holding x[16 b + i][128 g + 32 q + 8 j + c(e)] for
+// its 8 slots e, c(e) = perm8(e) for int4 weights (the order in which
+// dq_int4_x8 leaves the nibbles) and e for int8; and per (b, g) the 16
+// factors 2^-k (NaN when the group holds a non-finite value, so the outputs
+// it reaches are NaN).  Every A operand is then one contiguous 1 KiB load.
+constexpr int kHGroupBytes = 4 * 2 * 64 * 16;  // prepared bytes per (block, group)
+
+template <bool PERM>
+__global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x, int M, int64_t K, int64_t G,
+                                                     int64_t quads, int nb, _Float16* __restrict__ xh,
+                                                     float* __restrict__ xfx) {
+    const int lane = threadIdx.x & 63, j16 = lane & 15;
+    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wave >= int64_t(nb) * 16 * quads) return;
+    const int m = int(wave / quads);  // 0 .. 16 nb - 1 (rows past M are written as zeros)
+    const int64_t g = (wave % quads) * 4 + (lane >> 4);
+    const bool gvalid = g < G;
+    float v[8];
+    load_x8<1>(x + int64_t(m < M ? m : 0) * K, (gvalid && m < M ? g : 0) * kGroup + j16 * 8,
+               (gvalid && m < M) ? K : 0, v);
+    uint32_t am = 0, nf = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+        nf |= a >= 0x7F800000u ? 1u : 0u;
+        am = a > am ? a : am;
+    }
+    am = row16_max_u32(nf ? 0u : am);
+    const bool fin = row16_or(nf) == 0;
+    // amax = f 2^E, f in [0.5, 1): k = 15 - E puts amax 2^k in [2^14, 2^15)
+    const int k = (am > 0 && fin) ? 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(am)) : 0;
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float s = fin ? __builtin_amdgcn_ldexpf(v[e], k) : 0.0f;
+        const _Float16 h = _Float16(s);
+        hi[e] = h;
+        lo[e] = _Float16(s - float(h));
+    }
+    if (!gvalid) return;
+    _Float16 ho[8], lo2[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int slot = PERM ? 2 * (e & 3) + (e >> 2) : e;
+        ho[slot] = hi[e];
+        lo2[slot] = lo[e];
+    }
+    const int b = m >> 4, i = m & 15, q = j16 >> 2, jj = j16 & 3;
+    _Float16* base = xh + ((int64_t(b) * G + g) * kHGroupBytes) / 2;
+    const int l = i + 16 * q;
+    *reinterpret_cast<half8_t*>(base + ((jj * 2 + 0) * 64 + l) * 8) =
+        half8_t{ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
+    *reinterpret_cast<half8_t*>(base + ((jj * 2 + 1) * 64 + l) * 8) =
+        half8_t{lo2[0], lo2[1], lo2[2], lo2[3], lo2[4], lo2[5], lo2[6], lo2[7]};
+    if (j16 == 0) xfx[(int64_t(b) * G + g) * 16 + i] = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
+}
+
+// Workgroup = T consecutive 16-row tiles (of any of the call's matrices) x
+// KS waves, wave w taking groups [w gs, w gs + gs) of every tile; per group a
+// wave loads the 8 prepared A operands once (contiguous 1 KiB each, from
+// L2) and applies them to its T tiles' weights, with the next group's loads
+// in flight.  Slice sums are added through LDS in wave order
+// (deterministic).  p.M <= 16 rows of the block; p.xq / p.meta point at the
+// block's prepared operands and factors.
+template <int KIND, int T>
+__global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvParams p) {
+    extern __shared__ float hred[];  // [T][KS][4][64]
+    constexpr int WPG = KIND == 1 ? 1 : 2;
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KS = int(blockDim.x) >> 6;
+    const int G = int(p.G);
+    const int g0 = wave * p.gs < G ? wave * p.gs : G;
+    const int g1 = g0 + p.gs < G ? g0 + p.gs : G;
+    const int tb = int(blockIdx.x) * T;
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+
+    rsrc_t rq[T], rs[T], rz[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const bool ok = tb + t < p.ntiles;
+        const TileSel ts = select_tile(p, ok ? tb + t : p.ntiles - 1);
+        const int64_t left = ts.m.N - ts.row0;
+        const int64_t rows = ok ? (left < 16 ? left : 16) : 0;
+        rq[t] = make_rsrc(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
+        rs[t] = make_rsrc(ts.m.scales + ts.row0 * G, rows * G * 2);
+        rz[t] = make_rsrc(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+    }
+    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * kHGroupBytes);
+    const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
+    const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
+    const uint32_t vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
+
+    struct GB {
+        int4v_t a[8];       // [j][term]
+        float4_t fx;        // 2^-k of activation rows 4q .. 4q + 3
+        int4v_t w[T][WPG];
+        uint32_t s[T], z[T];
+    };
+    auto load = [&](int g, GB& b) {
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            b.a[c] = __builtin_bit_cast(int4v_t,
+                                        __builtin_amdgcn_raw_buffer_load_b128(ra, uint32_t(lane * 16), g * kHGroupBytes + c * 1024, 0));
+        b.fx = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rf, uint32_t(q * 16), g * 64, 0));
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+#pragma unroll
+            for (int h = 0; h < WPG; h++)
+                b.w[t][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            rq[t], vq, g * (KIND == 1 ? 64 : 128) + h * 16, 0));
+            b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(rs[t], vs, g * 2, 0);
+            b.z[t] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz[t], vz, g, 0) : 0u;
+        }
+    };
+    float acc[T][4];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
+    auto compute = [&](const GB& b) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            half8_t B[4];
+            if (KIND == 1) {
+                const uint32_t zb = zpair_1024(b.z[t]), zc = zpair_64(b.z[t]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t o0, o1, o2, o3;
+                    dq_int4_x8(uint32_t(b.w[t][0][j]), zb, zc, o0, o1, o2, o3);
+                    B[j] = pack_h8(o0, o1, o2, o3);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t l0, h0, l1, h1;
+                    const int4v_t& wv = b.w[t][j >> 1];
+                    dq_int8_x4(uint32_t(wv[2 * (j & 1)]), l0, h0);
+                    dq_int8_x4(uint32_t(wv[2 * (j & 1) + 1]), l1, h1);
+                    B[j] = pack_h8(l0, h0, l1, h1);
+                }
+            }
+            float4_t D = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j]), B[j], D);
+                D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j + 1]), B[j], D);
+            }
+            const float s = __uint_as_float(b.s[t] << 16);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(D[r], s * b.fx[r], acc[t][r]);
+        }
+    };
+    GB b0, b1;
+    if (g0 < g1) load(g0, b0);
+    for (int g = g0; g < g1; g += 2) {
+        if (g + 1 < g1) load(g + 1, b1);
+        compute(b0);
+        if (g + 1 >= g1) break;
+        if (g + 2 < g1) load(g + 2, b0);
+        compute(b1);
+    }
+
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) hred[((t * KS + wave) * 4 + r) * 64 + lane] = acc[t][r];
+    __syncthreads();
+    for (int o = tid; o < T * 256; o += int(blockDim.x)) {
+        const int t = o >> 8, r = (o >> 6) & 3, l = o & 63;
+        const int m = 4 * (l >> 4) + r, n = l & 15;
+        if (m >= p.M || tb + t >= p.ntiles) continue;
+        float sum = 0.0f;
+        for (int w = 0; w < KS; w++) sum += hred[((t * KS + w) * 4 + r) * 64 + l];
+        const TileSel ts = select_tile(p, tb + t);
+        const int64_t row = ts.row0 + n;
+        if (row < ts.m.N)
+            ts.m.y[int64_t(m) * ts.m.N + row] = sum + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
+    }
+}
+
+// f16 split preparation of x [M][K] (M <= kMaxRowsGemv, K % 128 == 0).
+hipError_t launch_xhprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
+    const int64_t G = K / kGroup, quads = (G + 3) / 4;
+    const int nb = (M + 15) / 16;
+    const int64_t waves = int64_t(nb) * 16 * quads;
+    const unsigned grid = unsigned((waves + 3) / 4);
+    _Float16* xh = reinterpret_cast<_Float16*>(ws->xq);
+    float* xfx = reinterpret_cast<float*>(ws->xmeta);
+    if (kind == 1) xhprep_kernel<true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+    else xhprep_kernel<false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+    return hipGetLastError();
+}
+
+bool gemvh_applies(int64_t K, int M) {
+    return M >= 2 && M <= kMaxRowsGemv && K % kGroup == 0;
+}
+
+// Direct calls (x given with the matrices) pick per shape, from 7B and
+// 1.5B measurements at 2..16 rows: gemvh for narrow calls (< 512 tiles: 7B
+// q|k|v 13.7 against 16 us, o 10.8 against 16); gemvt, whose workgroups share
+// one LDS copy of the activations over many tiles and pack 4 rows x 3 limbs
+// per MFMA up to 8 rows, for wider calls up to 8 rows and for 1024..4095-tile
+// calls with short K (7B gate|up: 27..38 against 47..48 us); gemvh otherwise
+// (lm_head at 12..16 rows: 173 against 184 us).
+bool gemvh_preferred(int64_t K, int M, int tiles) {
+    if (!gemvh_applies(K, M)) return false;
+    if (tiles < 512) return true;
+    if (M <= 8) return false;
+    return !(tiles >= 1024 && tiles < 4096 && K / kGroup <= 64);
+}
+
+template <int KIND, int T>
+void launch_gemvh_t(const GemvParams& p, int ks, hipStream_t stream) {
+    const unsigned grid = unsigned((p.ntiles + T - 1) / T);
+    gemvh_kernel<KIND, T><<<grid, 64 * ks, size_t(T) * ks * 4 * 64 * 4, stream>>>(p);
+}
+
+// The n matrices (one kind and width) on the prepared f16 split activations.
+hipError_t launch_gemvh(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
+                        hipStream_t stream) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    const int tiles = total_tiles(W, n);
+    // tiles per workgroup (measured, 7B shapes at 16 rows): the prepared
+    // operands of a group are read from L2 once per workgroup and group, so
+    // wide calls share them over more tiles (lm_head: 174 us at 4 against
+    // 280 at 1); narrow ones keep enough workgroups to fill the GPU (o: 10.8
+    // us at 1 against 13.8 at 2; q|k|v: 13.8 at 2 against 16.2 at 1)
+    const int T = tiles >= 4096 ? 4 : ((tiles >= 256 && G <= 64) ? 2 : 1);
+    const int maxw = T == 1 ? 16 : 8;  // the kernel's launch bound
+    int gs = int((G + maxw - 1) / maxw);
+    const int ks = int((G + gs - 1) / gs);
+    for (int r0 = 0; r0 < M; r0 += 16) {
+        GemvParams p{};
+        int t0 = 0;
+        for (int i = 0; i < n; i++) {
+            p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i] + int64_t(r0) * W[i].rows, W[i].rows, t0};
+            t0 += int((W[i].rows + 15) / 16);
+        }
+        p.nmat = n;
+        p.K = K;
+        p.G = G;
+        p.xq = ws->xq + int64_t(r0 / 16) * G * kHGroupBytes;
+        p.meta = reinterpret_cast<const int4*>(reinterpret_cast<const float*>(ws->xmeta) + int64_t(r0 / 16) * G * 16);
+        p.M = M - r0 < 16 ? M - r0 : 16;
+        p.gs = gs;
+        p.S = 1;
+        p.ntiles = tiles;
+        if (W[0].kind == 1) {
+            if (T == 4) launch_gemvh_t<1, 4>(p, ks, stream);
+            else if (T == 2) launch_gemvh_t<1, 2>(p, ks, stream);
+            else launch_gemvh_t<1, 1>(p, ks, stream);
+        } else {
+            if (T == 4) launch_gemvh_t<0, 4>(p, ks, stream);
+            else if (T == 2) launch_gemvh_t<0, 2>(p, ks, stream);
+            else launch_gemvh_t<0, 1>(p, ks, stream);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                                 Workspace* ws, hipStream_t stream) {
     hipError_t e = hipSuccess;
@@ -1246,9 +1522,15 @@ hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* w
     if (M == 1 && gemv1_plan(G, kind, gemv1_mode(K, G, ws->xf), 1, device_cu_count()).ng > 0) {
         e = hipMemcpyAsync(ws->xf, x, sizeof(float) * size_t(K), hipMemcpyDeviceToDevice, stream);
         ws->prep_copy = true;
+        ws->prep_h = false;
+    } else if (gemvh_applies(K, M)) {
+        e = launch_xhprep(x, M, K, kind, ws, stream);
+        ws->prep_copy = false;
+        ws->prep_h = true;
     } else {
         e = launch_xprep_limbs(x, M, K, kind, ws, stream);
         ws->prep_copy = false;
+        ws->prep_h = false;
     }
     ws->prep_M = M;
     ws->prep_K = K;
@@ -1265,6 +1547,7 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
         if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream);
         return hipErrorInvalidValue;
     }
+    if (ws->prep_h) return launch_gemvh(W, bias, y, n, M, ws, stream);
     return launch_batched_multi(W, bias, y, n, M, ws, stream);
 }
 
@@ -1281,11 +1564,18 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count());
         if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream);
     }
-    hipError_t e = launch_xprep_limbs(x, M, K, W[0].kind, ws, stream);
     ws->prep_copy = false;
     ws->prep_M = M;
     ws->prep_K = K;
     ws->prep_kind = W[0].kind;
+    if (gemvh_preferred(K, M, total_tiles(W, n))) {
+        ws->prep_h = true;
+        const hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
+        if (e != hipSuccess) return e;
+        return launch_gemvh(W, bias, y, n, M, ws, stream);
+    }
+    ws->prep_h = false;
+    hipError_t e = launch_xprep_limbs(x, M, K, W[0].kind, ws, stream);
     if (e != hipSuccess) return e;
     return launch_batched_multi(W, bias, y, n, M, ws, stream);
 }

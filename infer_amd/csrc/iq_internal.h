@@ -26,7 +26,8 @@ struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
     float* xf = nullptr;       // [kMaxKp] fp32: 1-row activation copied by a prep
-    int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs
+    int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs, or the f16 hi/lo
+                               // A operands [kMaxRowsGemv/16][kMaxKp/128][8 KiB] (gemvh)
     int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, sum X0, 256 sum X1 + sum X2, 0}
     float* partials = nullptr; // kPartialFloats
     // Shape of the activations last prepared into xq/xmeta (host-side record).
@@ -34,6 +35,7 @@ struct Workspace {
     int64_t prep_K = 0;
     int prep_kind = -1;
     bool prep_copy = false;   // the preparation is a copy of x in xf (1 row)
+    bool prep_h = false;      // the preparation is the f16 hi/lo split for gemvh (xq, xmeta)
 };
 
 constexpr int kMaxRowsGemv = 32;            // GpuBatch::kMaxRows (kernels/batch_gpu.h:80)

@@ -217,3 +217,25 @@ def test_gemv_nonfinite_activation(kind, M):
         ref, cond = O.linear_dq_f64(x[bad:], W.dq, None)
         err = np.abs(got[bad:].astype(np.float64) - ref)
         assert float((err / np.maximum(cond, 1e-30)).max()) <= 5e-6
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [2, 16, 17, 32])
+def test_gemv_prepared_f16_split_tile_blocks(kind, M):
+    """The prepare-once path (iq_gemv_prep + iq_gemv_prepped_multi) at 2..32
+    rows runs the f16 hi/lo split kernel for every width: one, two and four
+    16-row tiles per workgroup (224, 288 and 4096+ tiles per call), with a
+    bias on one matrix and activations spanning several decades."""
+    rng = np.random.default_rng(700 + 10 * kind + M)
+    for K, Ns in ((3584, (3584,)), (1536, (4096, 256, 256)), (256, (65536,))):
+        Ws = [QFix(rng, N, K, kind, sd=0.02) for N in Ns]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        x *= np.float32(10.0) ** rng.integers(-3, 3, size=(M, K)).astype(np.float32)
+        bb, bd = bias_of(rng, Ns[0])
+        ys = [out_buffer(M, W.rows) for W in Ws]
+        say("gemv prepared f16 split", kind, M, K, Ns)
+        ops.gemv_prep(torch.from_numpy(x).cuda(), M, K, kind)
+        ops.gemv_prepped_multi([W.view for W in Ws], [bd] + [None] * (len(Ws) - 1), M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y) in enumerate(zip(Ws, ys)):
+            check_linear(y, x, W, bb if i == 0 else None, M, f"prepared[{i}] kind={kind} M={M} K={K}")
