@@ -1245,7 +1245,11 @@ bool launch_gemvt(const QView* W, const uint16_t* const* bias, float* const* y, 
 // it reaches are NaN).  Every A operand is then one contiguous 1 KiB load.
 constexpr int kHGroupBytes = 4 * 2 * 64 * 16;  // prepared bytes per (block, group)
 
-template <bool PERM>
+// PK (M <= 8): one A operand per k-chunk holds both terms, rows 0..7 the hi
+// and rows 8..15 the lo terms of the 8 activation rows (4 KiB per group,
+// half the operand bytes and MFMAs); the kernel adds the two halves of each
+// output at the end.
+template <bool PERM, bool PK>
 __global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x, int M, int64_t K, int64_t G,
                                                      int64_t quads, int nb, _Float16* __restrict__ xh,
                                                      float* __restrict__ xfx) {
@@ -1286,12 +1290,21 @@ __global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x
         lo2[slot] = lo[e];
     }
     const int b = m >> 4, i = m & 15, q = j16 >> 2, jj = j16 & 3;
-    _Float16* base = xh + ((int64_t(b) * G + g) * kHGroupBytes) / 2;
-    const int l = i + 16 * q;
-    *reinterpret_cast<half8_t*>(base + ((jj * 2 + 0) * 64 + l) * 8) =
-        half8_t{ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
-    *reinterpret_cast<half8_t*>(base + ((jj * 2 + 1) * 64 + l) * 8) =
-        half8_t{lo2[0], lo2[1], lo2[2], lo2[3], lo2[4], lo2[5], lo2[6], lo2[7]};
+    if (PK) {
+        if (m >= 8) return;
+        _Float16* base = xh + (g * (kHGroupBytes / 2)) / 2;
+        *reinterpret_cast<half8_t*>(base + (jj * 64 + i + 16 * q) * 8) =
+            half8_t{ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
+        *reinterpret_cast<half8_t*>(base + (jj * 64 + i + 8 + 16 * q) * 8) =
+            half8_t{lo2[0], lo2[1], lo2[2], lo2[3], lo2[4], lo2[5], lo2[6], lo2[7]};
+    } else {
+        _Float16* base = xh + ((int64_t(b) * G + g) * kHGroupBytes) / 2;
+        const int l = i + 16 * q;
+        *reinterpret_cast<half8_t*>(base + ((jj * 2 + 0) * 64 + l) * 8) =
+            half8_t{ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
+        *reinterpret_cast<half8_t*>(base + ((jj * 2 + 1) * 64 + l) * 8) =
+            half8_t{lo2[0], lo2[1], lo2[2], lo2[3], lo2[4], lo2[5], lo2[6], lo2[7]};
+    }
     if (j16 == 0) xfx[(int64_t(b) * G + g) * 16 + i] = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
 }
 
@@ -1302,7 +1315,7 @@ __global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x
 // in flight.  Slice sums are added through LDS in wave order
 // (deterministic).  p.M <= 16 rows of the block; p.xq / p.meta point at the
 // block's prepared operands and factors.
-template <int KIND, int T>
+template <int KIND, int T, bool PK>
 __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvParams p) {
     extern __shared__ float hred[];  // [T][KS][4][64]
     constexpr int WPG = KIND == 1 ? 1 : 2;
@@ -1326,23 +1339,25 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
         rs[t] = make_rsrc(ts.m.scales + ts.row0 * G, rows * G * 2);
         rz[t] = make_rsrc(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
     }
-    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * kHGroupBytes);
+    constexpr int NA = PK ? 4 : 8;  // A operands per group
+    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * NA * 1024);
     const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
     const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
     const uint32_t vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
 
     struct GB {
-        int4v_t a[8];       // [j][term]
+        int4v_t a[NA];      // [j][term], or [j] with both terms (PK)
         float4_t fx;        // 2^-k of activation rows 4q .. 4q + 3
         int4v_t w[T][WPG];
         uint32_t s[T], z[T];
     };
     auto load = [&](int g, GB& b) {
 #pragma unroll
-        for (int c = 0; c < 8; c++)
+        for (int c = 0; c < NA; c++)
             b.a[c] = __builtin_bit_cast(int4v_t,
-                                        __builtin_amdgcn_raw_buffer_load_b128(ra, uint32_t(lane * 16), g * kHGroupBytes + c * 1024, 0));
-        b.fx = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rf, uint32_t(q * 16), g * 64, 0));
+                                        __builtin_amdgcn_raw_buffer_load_b128(ra, uint32_t(lane * 16), g * NA * 1024 + c * 1024, 0));
+        // factors of this lane's activation rows (PK: rows 4q .. 4q + 3 mod 8)
+        b.fx = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rf, uint32_t((PK ? q & 1 : q) * 16), g * 64, 0));
 #pragma unroll
         for (int t = 0; t < T; t++) {
 #pragma unroll
@@ -1383,8 +1398,12 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
             float4_t D = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j]), B[j], D);
-                D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j + 1]), B[j], D);
+                if (PK) {
+                    D = mfma16(__builtin_bit_cast(half8_t, b.a[j]), B[j], D);
+                } else {
+                    D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j]), B[j], D);
+                    D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j + 1]), B[j], D);
+                }
             }
             const float s = __uint_as_float(b.s[t] << 16);
 #pragma unroll
@@ -1412,6 +1431,12 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
         if (m >= p.M || tb + t >= p.ntiles) continue;
         float sum = 0.0f;
         for (int w = 0; w < KS; w++) sum += hred[((t * KS + w) * 4 + r) * 64 + l];
+        if (PK) {
+            // rows 8..15 of the operand carried the lo terms: lane l + 32
+            float lo = 0.0f;
+            for (int w = 0; w < KS; w++) lo += hred[((t * KS + w) * 4 + r) * 64 + l + 32];
+            sum += lo;
+        }
         const TileSel ts = select_tile(p, tb + t);
         const int64_t row = ts.row0 + n;
         if (row < ts.m.N)
@@ -1427,8 +1452,13 @@ hipError_t launch_xhprep(const float* x, int M, int64_t K, int kind, Workspace* 
     const unsigned grid = unsigned((waves + 3) / 4);
     _Float16* xh = reinterpret_cast<_Float16*>(ws->xq);
     float* xfx = reinterpret_cast<float*>(ws->xmeta);
-    if (kind == 1) xhprep_kernel<true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
-    else xhprep_kernel<false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+    if (M <= 8) {
+        if (kind == 1) xhprep_kernel<true, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+        else xhprep_kernel<false, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+    } else {
+        if (kind == 1) xhprep_kernel<true, false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+        else xhprep_kernel<false, false><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
+    }
     return hipGetLastError();
 }
 
@@ -1453,7 +1483,9 @@ bool gemvh_preferred(int64_t K, int M, int tiles) {
 template <int KIND, int T>
 void launch_gemvh_t(const GemvParams& p, int ks, hipStream_t stream) {
     const unsigned grid = unsigned((p.ntiles + T - 1) / T);
-    gemvh_kernel<KIND, T><<<grid, 64 * ks, size_t(T) * ks * 4 * 64 * 4, stream>>>(p);
+    const size_t lds = size_t(T) * ks * 4 * 64 * 4;
+    if (p.M <= 8 && p.S == 0) gemvh_kernel<KIND, T, true><<<grid, 64 * ks, lds, stream>>>(p);
+    else gemvh_kernel<KIND, T, false><<<grid, 64 * ks, lds, stream>>>(p);
 }
 
 // The n matrices (one kind and width) on the prepared f16 split activations.
@@ -1484,7 +1516,7 @@ hipError_t launch_gemvh(const QView* W, const uint16_t* const* bias, float* cons
         p.meta = reinterpret_cast<const int4*>(reinterpret_cast<const float*>(ws->xmeta) + int64_t(r0 / 16) * G * 16);
         p.M = M - r0 < 16 ? M - r0 : 16;
         p.gs = gs;
-        p.S = 1;
+        p.S = M <= 8 ? 0 : 1;  // 0: the packed (M <= 8) preparation
         p.ntiles = tiles;
         if (W[0].kind == 1) {
             if (T == 4) launch_gemvh_t<1, 4>(p, ks, stream);
