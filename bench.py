@@ -225,18 +225,28 @@ def cpu_baseline(torch, model, seconds=10.0):
     return done_b / t_tot / 1e9, f"{n} matrices ({names[0]}..{names[-1]}), {done_b / 1e6:.0f} MB packed, {t_tot:.1f} s"
 
 
-def bench_gemm(torch, ops, kind, T, N, K, reps=10, seed=5):
+def bench_gemm(torch, ops, kind, T, N, K, reps=10, seed=5, fp32x=False):
+    """Prefill GEMM at config 5: bf16 activations (iq_gemm_bf16x), or fp32
+    activations through the reference-compatible launch_gemm_tiled_q
+    (split into bf16 hi + lo inside the kernel, two MFMAs per product)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     W = quantize_seeded(torch, ops, kind, N, K, g)
-    x = torch.randn(T, K, generator=g, device="cuda").to(torch.bfloat16)
+    xf = torch.randn(T, K, generator=g, device="cuda")
+    x = xf.to(torch.bfloat16)
     y = torch.empty(T, N, device="cuda")
+
+    def run():
+        if fp32x:
+            ops.launch_gemm_tiled_q(xf, W, None, T, K, N, y)
+        else:
+            ops.launch_gemm_bf16x(x.view(torch.int16), W, None, T, K, N, y)
     for _ in range(2):
-        ops.launch_gemm_bf16x(x.view(torch.int16), W, None, T, K, N, y)
+        run()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
-        ops.launch_gemm_bf16x(x.view(torch.int16), W, None, T, K, N, y)
+        run()
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
@@ -391,9 +401,13 @@ def main():
         del w
         # prefill GEMM (config 5), int8, bf16 activations, T = 1024
         for (N, K, nm) in ((I7, H7, "gate_up"), (H7, I7, "down")):
-            ms, tf = bench_gemm(torch, ops, 0, 1024, N, K)
-            detail[f"prefill_int8_{nm}_1024"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
-                                                 "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            for kind, kn in ((0, "int8"), (1, "int4")):
+                ms, tf = bench_gemm(torch, ops, kind, 1024, N, K)
+                detail[f"prefill_{kn}_{nm}_1024"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
+                                                     "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            ms, tf = bench_gemm(torch, ops, 0, 1024, N, K, fp32x=True)
+            detail[f"prefill_int8_{nm}_1024_fp32x"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
+                                                       "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
         # config 1: int8 8960x1536, 1 row, rotated over 64 copies
         us, gbs = bench_gemv_single(torch, ops, 0, I15, H15, 1, copies=64)
         detail["cfg1_int8_8960x1536_m1"] = {"us": round(us, 2), "GBps": round(gbs, 1)}

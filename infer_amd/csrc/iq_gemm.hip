@@ -27,6 +27,7 @@ namespace {
 
 constexpr int BM = 128, BK = 64, LDSW = BK + 8;  // LDS row pitch (bf16)
 constexpr int kThreads = 256;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 struct GemmParams {
     const float* xf;      // fp32 activations [T][K] or null
@@ -169,13 +170,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
                 const int row = c >> 4, kc = c & 15;
                 const float f[4] = {__uint_as_float(xr[i].x), __uint_as_float(xr[i].y),
                                     __uint_as_float(xr[i].z), __uint_as_float(xr[i].w)};
+                // hi = bf16(x), lo = bf16(x - hi), both rounded to nearest
+                // even by the packed hardware conversion (x - hi is exact)
                 uint32_t hi[2], lo[2];
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    const uint16_t h0 = f32_to_bf16(f[2 * e]), h1 = f32_to_bf16(f[2 * e + 1]);
-                    const float r0 = f[2 * e] - bf16_to_f32(h0), r1 = f[2 * e + 1] - bf16_to_f32(h1);
-                    hi[e] = uint32_t(h0) | (uint32_t(h1) << 16);
-                    lo[e] = uint32_t(f32_to_bf16(r0)) | (uint32_t(f32_to_bf16(r1)) << 16);
+                    const bf16x2_t h = {__bf16(f[2 * e]), __bf16(f[2 * e + 1])};
+                    const bf16x2_t l = {__bf16(f[2 * e] - float(h[0])), __bf16(f[2 * e + 1] - float(h[1]))};
+                    hi[e] = __builtin_bit_cast(uint32_t, h);
+                    lo[e] = __builtin_bit_cast(uint32_t, l);
                 }
                 *reinterpret_cast<uint2*>(&As[buf][row][kc * 4]) = make_uint2(hi[0], hi[1]);
                 *reinterpret_cast<uint2*>(&Al[XF32 ? buf : 0][XF32 ? row : 0][kc * 4]) = make_uint2(lo[0], lo[1]);
