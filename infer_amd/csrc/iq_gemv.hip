@@ -40,6 +40,7 @@
 //    when the matrix is too short to fill the GPU; the last workgroup of a
 //    row block adds the slice partials in slice order (deterministic) and
 //    resets its counter, so no clearing is needed between launches.
+#include <algorithm>
 #include <cstdlib>
 
 #include "iq_internal.h"
@@ -337,53 +338,27 @@ __device__ __forceinline__ TileSel select_tile(const GemvParams& p, int tile) {
     return TileSel{m, int64_t(tile - m.tile0) * 16};
 }
 
-// Issues the loads of one wave's slice [gbeg, gbeg + gs) of tile `tile`
-// (lane: row row0 + ln, 16-byte column block kg of each 64-byte half group).
-// Past the last tile, past N or past the slice the loads read zero without
-// touching memory (buffer range check), so every load is unconditional.
+// The loads of one wave's slice [gbeg, gbeg + gs) of the tile at row0
+// (lane: row row0 + ln, 16-byte column block kg of each 64-byte half group),
+// in two calls: scales and zero points first, then the weight words, so the
+// small metadata requests are not queued behind the weights.  Rows past N
+// and slots past the slice read zero without touching memory (buffer range
+// check), so every load is unconditional.
 // MODE 0: rows not 16-byte aligned (byte loads, clamped); 1: one scale /
 // zero-point load per group; 2: one 8-byte scale and one 4-byte zero-point
-// load per 4 groups (G % 4 == 0, slices of whole 4-group blocks).
+// load per 4 groups (G % 4 == 0, slices of whole 4-group blocks), unless the
+// workgroup stages the tile's scales and zero points in LDS.
 template <int KIND, int NG, int MODE>
-__device__ __forceinline__ void load_slice(Slice<KIND, NG>& b, const GemvParams& p, int tile, int gbeg, int gs,
-                                           int ln, int kg) {
-    constexpr int WPG = Slice<KIND, NG>::WPG;
+__device__ __forceinline__ void load_meta(Slice<KIND, NG>& b, const GemvParams& p, const TileSel& ts, int gbeg,
+                                          int gs, int ln) {
     const int G = int(p.G);
-    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
-    const TileSel ts = select_tile(p, tile < p.ntiles ? tile : p.ntiles - 1);
     const MatRef& mr = ts.m;
     const int64_t row = ts.row0 + ln;
-    const uint32_t dead = tile < p.ntiles ? 0u : kOob;  // prefetch past the end
-    if (MODE == 0) {
-        const int64_t rc = row < mr.N ? row : mr.N - 1;
-        const uint8_t* qrow = mr.q + rc * row_bytes;
-#pragma unroll
-        for (int gl = 0; gl < NG; gl++) {
-            const int g = gbeg + (gl < gs ? gl : gs - 1);
-#pragma unroll
-            for (int h = 0; h < WPG; h++) {
-                const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
-                const uint4 v = load16_slow(qrow, off, row_bytes);
-                b.w[gl][h] = int4v_t{int(v.x), int(v.y), int(v.z), int(v.w)};
-            }
-        }
-    } else {
-        const rsrc_t rq = make_rsrc(mr.q, mr.N * row_bytes);
-        const uint32_t vq = uint32_t(row * row_bytes) + uint32_t(gbeg * (KIND == 1 ? 64 : 128) + kg * 16) + dead;
-#pragma unroll
-        for (int gl = 0; gl < NG; gl++) {
-            const uint32_t vo = vq + (gl < gs ? 0u : kOob);
-#pragma unroll
-            for (int h = 0; h < WPG; h++)
-                b.w[gl][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rq, vo, KIND == 1 ? gl * 64 : gl * 128 + h * 64, 0));
-        }
-    }
     const rsrc_t rs = make_rsrc(mr.scales, mr.N * G * 2);
     const rsrc_t rz = make_rsrc(mr.zeros, KIND == 1 ? mr.N * G : 0);
     const int64_t rcs = MODE == 0 ? (row < mr.N ? row : mr.N - 1) : row;
-    const uint32_t vs = uint32_t((rcs * G + gbeg) * 2) + dead;
-    const uint32_t vz = uint32_t(rcs * G + gbeg) + dead;
+    const uint32_t vs = uint32_t((rcs * G + gbeg) * 2);
+    const uint32_t vz = uint32_t(rcs * G + gbeg);
     if (MODE == 2) {
 #pragma unroll
         for (int q4 = 0; q4 < NG / 4; q4++) {
@@ -406,6 +381,40 @@ __device__ __forceinline__ void load_slice(Slice<KIND, NG>& b, const GemvParams&
 #pragma unroll
         for (int i = 0; i < NG / 4; i++)
             b.z[i] = zb[4 * i] | (zb[4 * i + 1] << 8) | (zb[4 * i + 2] << 16) | (zb[4 * i + 3] << 24);
+    }
+}
+
+template <int KIND, int NG, int MODE>
+__device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParams& p, const TileSel& ts, int gbeg,
+                                             int gs, int ln, int kg) {
+    constexpr int WPG = Slice<KIND, NG>::WPG;
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const MatRef& mr = ts.m;
+    const int64_t row = ts.row0 + ln;
+    if (MODE == 0) {
+        const int64_t rc = row < mr.N ? row : mr.N - 1;
+        const uint8_t* qrow = mr.q + rc * row_bytes;
+#pragma unroll
+        for (int gl = 0; gl < NG; gl++) {
+            const int g = gbeg + (gl < gs ? gl : gs - 1);
+#pragma unroll
+            for (int h = 0; h < WPG; h++) {
+                const int off = KIND == 1 ? g * 64 + kg * 16 : g * 128 + h * 64 + kg * 16;
+                const uint4 v = load16_slow(qrow, off, row_bytes);
+                b.w[gl][h] = int4v_t{int(v.x), int(v.y), int(v.z), int(v.w)};
+            }
+        }
+    } else {
+        const rsrc_t rq = make_rsrc(mr.q, mr.N * row_bytes);
+        const uint32_t vq = uint32_t(row * row_bytes) + uint32_t(gbeg * (KIND == 1 ? 64 : 128) + kg * 16);
+#pragma unroll
+        for (int gl = 0; gl < NG; gl++) {
+            const uint32_t vo = vq + (gl < gs ? 0u : kOob);
+#pragma unroll
+            for (int h = 0; h < WPG; h++)
+                b.w[gl][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rq, vo, KIND == 1 ? gl * 64 : gl * 128 + h * 64, 0));
+        }
     }
 }
 
@@ -454,32 +463,44 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 }
 
 // One activation row (the decode step).  Workgroup = KS waves (runtime,
-// blockDim.x / 64) on one 16-row tile at a time, wave w owning the K slice
-// [w*gs, w*gs + gs) of every tile; the workgroups walk the tiles of all
-// matrices of the launch in strides of gridDim.x (persistent).  At start each
-// wave converts its slice of the fp32 activations into byte limbs in LDS
-// (once per workgroup, while the first tile's weights are in flight).  Per
-// tile the next tile's slice is requested before the current one is
-// multiplied (two register buffers), and the KS slice partials are added
-// through LDS in slice order (deterministic; no cross-workgroup traffic).
-template <int KIND, int NG, int MODE, int TPW, int MAXW>
+// blockDim.x / 64) on one 16-row tile, wave w owning the K slice
+// [w*gs, w*gs + gs).  Each wave converts its slice of the fp32 activations
+// into byte limbs in LDS while its weights stream in.  With p.S == 2 (MODE
+// 2) the workgroup stages the tile's scales and zero points (16 consecutive
+// rows: one contiguous block each) in LDS with one 16-byte load per thread,
+// instead of every wave fetching the same lines for its slice.  The slice partials are added
+// through LDS by whichever wave finishes last (an LDS counter), in slice
+// order, so the sum is deterministic and no wave waits for the others.
+template <int KIND, int NG, int MODE, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
-    extern __shared__ __attribute__((aligned(16))) int8_t xs1[];  // limbs [G][384], meta [G]
+    // dynamic LDS: limbs [G][384], meta [G] int4, then (MODE 2) the tile's
+    // scales [16][G] bf16 and zero points [16][G] u8
+    extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
-    __shared__ float red[TPW][MAXW][16];
+    __shared__ float red[MAXW][16];
+    __shared__ int arrived;
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
     const int KS = int(blockDim.x) >> 6;
     const int G = int(p.G);
     const int gbeg = wave * p.gs < G ? wave * p.gs : G;
     const int gs = (gbeg + p.gs < G ? gbeg + p.gs : G) - gbeg;
     int4* ms1 = reinterpret_cast<int4*>(xs1 + G * kLimbRec);
-    auto tile_of = [&](int i) { return int(blockIdx.x) + i * int(gridDim.x); };
+    int8_t* tmeta = xs1 + G * (kLimbRec + 16);
+    const TileSel ts = select_tile(p, int(blockIdx.x));
+    const bool staged = MODE == 2 && p.S == 2;
 
     // 1. This wave's activations: pass t converts groups gbeg + 4t + kg,
     //    16 lanes (one DPP row) per group, 8 columns per lane.  Every wave
     //    requests them before any wave requests weights: the vector L1
     //    returns data in request order, so activations asked for behind the
     //    CU's weight misses would arrive only after them.
+    //    The bias of the rows this lane may store goes first (lanes 0..15 of
+    //    every wave: any wave may be the one that finishes the tile).
+    uint32_t bias;
+    {
+        const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
+        bias = __builtin_amdgcn_raw_buffer_load_b16(rb, lane < 16 ? uint32_t(ts.row0 + ln) * 2 : kOob, 0, 0);
+    }
     constexpr int XP = NG / 4;
     float xv[XP][8];
 #pragma unroll
@@ -487,27 +508,29 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
         const int g = 4 * t + kg < gs ? gbeg + 4 * t + kg : (gs > 0 ? gbeg + gs - 1 : 0);
         load_x8<MODE >= 1 ? 2 : 0>(p.x, int64_t(g) * kGroup + ln * 8, p.K, xv[t]);
     }
-    // The bias of the rows this lane may store (wave 0, lanes 0..15), bf16.
-    uint32_t bias[TPW];
-#pragma unroll
-    for (int i = 0; i < TPW; i++) {
-        const int t = tile_of(i);
-        const TileSel ts = select_tile(p, t < p.ntiles ? t : p.ntiles - 1);
-        const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
-        const bool mine = wave == 0 && lane < 16 && t < p.ntiles;
-        bias[i] = __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(ts.row0 + ln) * 2 : kOob, 0, 0);
-    }
     if (tid < 4) reinterpret_cast<uint32_t*>(xzero)[tid] = 0u;
+    if (tid == 0) arrived = 0;
     __syncthreads();
 
-    // 2. The first PD tiles' slices in flight (tiles past the end read zero
-    //    without touching memory), then the conversion while they stream in.
-    //    A wave stalls while the CU's memory queues are full, so it keeps
-    //    only PD tiles ahead and multiplies in between.
-    constexpr int PD = TPW < 2 ? TPW : 2;
-    Slice<KIND, NG> b[TPW];
-#pragma unroll
-    for (int i = 0; i < PD; i++) load_slice<KIND, NG, MODE>(b[i], p, tile_of(i), gbeg, gs, ln, kg);
+    // 2. Staged: thread i requests 16 bytes of the tile's scale block
+    //    (32 G bytes) and of its zero-point block (16 G bytes; rows past N
+    //    read zero); otherwise each wave its own slice's.  Then every wave's
+    //    weights, and the conversion while they stream in.
+    int4v_t mv_s = {0, 0, 0, 0}, mv_z = {0, 0, 0, 0};
+    const int64_t trows = ts.m.N - ts.row0 < 16 ? ts.m.N - ts.row0 : 16;
+    if (staged && wave * 64 < 2 * G) {
+        const rsrc_t rs = make_rsrc(ts.m.scales + ts.row0 * G, trows * G * 2);
+        mv_s = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rs, tid < 2 * G ? uint32_t(tid) * 16 : kOob, 0, 0));
+        if (KIND == 1 && wave * 64 < G) {
+            const rsrc_t rz = make_rsrc(ts.m.zeros + ts.row0 * G, trows * G);
+            mv_z = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rz, tid < G ? uint32_t(tid) * 16 : kOob, 0, 0));
+        }
+    }
+    Slice<KIND, NG> b;
+    if (!staged) load_meta<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln);
+    load_weights<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln, kg);
 #pragma unroll
     for (int t = 0; t < XP; t++) {
         if (4 * t >= gs) break;  // wave-uniform
@@ -517,37 +540,38 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
         if (st && ln == 0) ms1[g] = md;
     }
     // (each wave reads only its own limb records; the zero block is shared)
+    if (staged) {
+        if (wave * 64 < 2 * G) {
+            if (tid < 2 * G) reinterpret_cast<int4v_t*>(tmeta)[tid] = mv_s;
+            if (KIND == 1 && tid < G) reinterpret_cast<int4v_t*>(tmeta + 32 * G)[tid] = mv_z;
+        }
+        __syncthreads();
+        // this wave's words: rows ln, groups gbeg .. gbeg + NG (gbeg % 4 == 0)
+#pragma unroll
+        for (int q4 = 0; q4 < NG / 4; q4++) {
+            const int g = 4 * q4 < gs ? gbeg + 4 * q4 : gbeg;
+            const uint2 sv = *reinterpret_cast<const uint2*>(tmeta + (ln * G + g) * 2);
+            b.s[2 * q4] = sv.x;
+            b.s[2 * q4 + 1] = sv.y;
+            b.z[q4] = KIND == 1 ? *reinterpret_cast<const uint32_t*>(tmeta + 32 * G + ln * G + g) : 0u;
+        }
+    }
 
-    // 3. Tiles in order, each as its slice lands, then the request for the
-    //    tile PD ahead.  Slice partials are added through LDS in slice order
-    //    (rows k >= KS were never written and are discarded); all stores
-    //    come after the last load has been used.
-    float yv[TPW];
+    // 3. The slice as it lands; partials through LDS, the last wave to
+    //    arrive adds them in slice order (rows k >= KS were never written).
+    const float acc = slice_dot<KIND, NG>(b, xs1, ms1, xzero, gbeg, gs, ln, kg);
+    if (lane < 16) red[wave][lane] = acc;
+    int prior = 0;
+    if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    prior = __builtin_amdgcn_readfirstlane(prior);
+    if (prior != KS - 1 || lane >= 16) return;
+    float sum = red[0][ln];
 #pragma unroll
-    for (int i = 0; i < TPW; i++) {
-        const float acc = slice_dot<KIND, NG>(b[i], xs1, ms1, xzero, gbeg, gs, ln, kg);
-        if (lane < 16) red[i][wave][lane] = acc;
-        if (i + PD < TPW) load_slice<KIND, NG, MODE>(b[i + PD], p, tile_of(i + PD), gbeg, gs, ln, kg);
+    for (int k = 1; k < MAXW; k++) {
+        const float v = red[k][ln];
+        sum += k < KS ? v : 0.0f;
     }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < TPW; i++) {
-        float sum = red[i][0][ln];
-#pragma unroll
-        for (int k = 1; k < MAXW; k++) {
-            const float v = red[i][k][ln];
-            sum += k < KS ? v : 0.0f;
-        }
-        yv[i] = sum + __uint_as_float(bias[i] << 16);
-    }
-    if (wave == 0 && lane < 16) {
-#pragma unroll
-        for (int i = 0; i < TPW; i++) {
-            if (tile_of(i) >= p.ntiles) break;
-            const TileSel ts = select_tile(p, tile_of(i));
-            if (ts.row0 + lane < ts.m.N) ts.m.y[ts.row0 + lane] = yv[i];
-        }
-    }
+    if (ts.row0 + lane < ts.m.N) ts.m.y[ts.row0 + lane] = sum + __uint_as_float(bias << 16);
 }
 
 // ------------------------------------------------------------------ 2..32 rows
@@ -987,6 +1011,7 @@ int gemv1_mode(int64_t K, int64_t G, const float* x) {
 // Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
 // (ks), the slice capacity NG of the kernel instance, the grid and the tiles
 // per workgroup (tpw, 1 with the instances built here).
+
 struct G1Plan {
     int gs, ks, ng, grid, tpw;
 };
@@ -1020,11 +1045,11 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
     return pl;
 }
 
-template <int KIND, int NG, int TPW, int MAXW>
+template <int KIND, int NG, int MAXW>
 void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
-    if (mode == 2) gemv1_kernel<KIND, NG, 2, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
-    else if (mode == 1) gemv1_kernel<KIND, NG, 1, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
-    else gemv1_kernel<KIND, NG, 0, TPW, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+    if (mode == 2) gemv1_kernel<KIND, NG, 2, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+    else if (mode == 1) gemv1_kernel<KIND, NG, 1, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+    else gemv1_kernel<KIND, NG, 0, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
@@ -1042,19 +1067,30 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     p.x = x;
     p.M = 1;
     p.gs = pl.gs;
-    p.S = 1;
     p.ntiles = tiles;
-    const size_t lds = size_t(G) * (kLimbRec + 16);
+    size_t lds = size_t(G) * (kLimbRec + 16);
+    // Staged scales / zero points on wide launches (7B int4 gate|up 16.9 ->
+    // 15.9 us); narrow ones (under 4 workgroups per CU) lose more to the
+    // extra barrier than they save (o 4.8 -> 5.1 us).  Not where the 48 G
+    // bytes would cut the workgroups a CU holds (160 KiB of LDS, 32 waves
+    // at <= 64 VGPRs), or leave a staged word without a thread.
+    const size_t cu_lds = 160 * 1024, staged = lds + size_t(G) * 48, wlim = size_t(32 / pl.ks);
+    const size_t occ = std::min(cu_lds / lds, wlim), occ_staged = std::min(cu_lds / staged, wlim);
+    p.S = 1;
+    if (mode == 2 && tiles >= 4 * device_cu_count() && staged <= 64 * 1024 && occ_staged == occ && 2 * G <= 64 * pl.ks) {
+        p.S = 2;
+        lds = staged;
+    }
     const unsigned grid = unsigned(pl.grid);
     if (W[0].kind == 1) {
-        if (pl.ng == 4) launch_gemv1_m<1, 4, 1, 16>(p, mode, pl.ks, grid, lds, stream);
-        else if (pl.ng == 8) launch_gemv1_m<1, 8, 1, 16>(p, mode, pl.ks, grid, lds, stream);
-        else launch_gemv1_m<1, 12, 1, 16>(p, mode, pl.ks, grid, lds, stream);
+        if (pl.ng == 4) launch_gemv1_m<1, 4, 16>(p, mode, pl.ks, grid, lds, stream);
+        else if (pl.ng == 8) launch_gemv1_m<1, 8, 16>(p, mode, pl.ks, grid, lds, stream);
+        else launch_gemv1_m<1, 12, 16>(p, mode, pl.ks, grid, lds, stream);
     } else {
-        if (pl.ng == 4) launch_gemv1_m<0, 4, 1, 8>(p, mode, pl.ks, grid, lds, stream);
-        else if (pl.ng == 8) launch_gemv1_m<0, 8, 1, 8>(p, mode, pl.ks, grid, lds, stream);
-        else if (pl.ng == 12) launch_gemv1_m<0, 12, 1, 8>(p, mode, pl.ks, grid, lds, stream);
-        else launch_gemv1_m<0, 20, 1, 8>(p, mode, pl.ks, grid, lds, stream);
+        if (pl.ng == 4) launch_gemv1_m<0, 4, 8>(p, mode, pl.ks, grid, lds, stream);
+        else if (pl.ng == 8) launch_gemv1_m<0, 8, 8>(p, mode, pl.ks, grid, lds, stream);
+        else if (pl.ng == 12) launch_gemv1_m<0, 12, 8>(p, mode, pl.ks, grid, lds, stream);
+        else launch_gemv1_m<0, 20, 8>(p, mode, pl.ks, grid, lds, stream);
     }
     return hipGetLastError();
 }
