@@ -23,7 +23,7 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 hipError_t create_workspace(int dev, Workspace* ws) {
     const int64_t gmax = kMaxKp / kGroup;
-    const size_t xf = align256(sizeof(float) * kMaxKp);
+    const size_t xf = align256(sizeof(float) * 4 * kMaxKp);  // up to 4 rows copied by a prep
     // limbs (3 B per value) or f16 hi + lo (4 B per value)
     const size_t xq = align256(size_t(kMaxRowsGemv) * gmax * 4 * kGroup);
     const size_t meta = align256(sizeof(int4) * gmax * kMaxRowsGemv);

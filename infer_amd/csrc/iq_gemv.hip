@@ -418,14 +418,22 @@ __device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParam
     }
 }
 
-// Multiplies one tile's slice by the staged activation limbs: the A operand
-// carries the three limbs as rows 0..2 of the 16-row MFMA tile (lanes
-// l%16 = 0, 1, 2; the other lanes read a zero block), so two MFMAs per 128
-// columns give all three exact limb sums, in D rows 0..2 of lanes 0..15.
-template <int KIND, int NG>
+// Multiplies one tile's slice by the staged activation limbs.  R = 1: the A
+// operand carries the three limbs as rows 0..2 of the 16-row MFMA tile
+// (lanes l%16 = 0, 1, 2; the other lanes read a zero block), so two MFMAs per
+// 128 columns give all three exact limb sums, in D rows 0..2 of lanes 0..15.
+// R = 4: A row 4m + L = limb L of activation row m < M (rows 4m + 3 and rows
+// of m >= M zero), so the same two MFMAs give row m's limb sums in D rows
+// 4m .. 4m + 2, i.e. registers 0..2 of lanes 16m .. 16m + 15.  Returns the
+// running sum of activation row l/16 (R = 4) or row 0 (R = 1, lanes 0..15).
+template <int KIND, int NG, int R>
 __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_t* xs, const int4* ms,
-                                           const int8_t* xzero, int gbeg, int gs, int ln, int kg) {
+                                           const int8_t* xzero, int G, int M, int gbeg, int gs, int ln, int kg) {
     float acc = 0.0f;
+    const int am = R == 1 ? 0 : ln >> 2, aL = R == 1 ? ln : ln & 3;  // A row of this lane
+    const bool alive = aL < 3 && am < M;
+    const int8_t* xrow = xs + int64_t(am) * G * kLimbRec + aL * kGroup + kg * 16;
+    const int4* mrow = ms + (R == 1 ? 0 : kg) * G;
     // blocks of 4 groups: an early exit over at most 8 iterations still
     // unrolls fully (so the slice stays in registers)
 #pragma unroll
@@ -438,9 +446,9 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
             const int g = gbeg + (ok ? gl : 0);
             int4v_t a0, a1, b0, b1;
             {
-                const int8_t* pa = ln < 3 ? xs + g * kLimbRec + ln * kGroup + kg * 16 : xzero;
+                const int8_t* pa = alive ? xrow + g * kLimbRec : xzero;
                 a0 = *reinterpret_cast<const int4v_t*>(pa);
-                a1 = *reinterpret_cast<const int4v_t*>(pa + (ln < 3 ? 64 : 0));
+                a1 = *reinterpret_cast<const int4v_t*>(pa + (alive ? 64 : 0));
             }
             if (KIND == 1) {
                 const int4v_t v = b.w[gl][0];
@@ -455,7 +463,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
             const uint32_t sw = b.s[gl / 2];
             const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
             const int z = KIND == 1 ? int((b.z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
-            const float nacc = combine(acc, D[0], D[1], D[2], z, ms[g], sc);
+            const float nacc = combine(acc, D[0], D[1], D[2], z, mrow[g], sc);
             acc = ok ? nacc : acc;
         }
     }
@@ -471,21 +479,22 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // instead of every wave fetching the same lines for its slice.  The slice partials are added
 // through LDS by whichever wave finishes last (an LDS counter), in slice
 // order, so the sum is deterministic and no wave waits for the others.
-template <int KIND, int NG, int MODE, int MAXW>
+template <int KIND, int NG, int MODE, int MAXW, int R>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
-    // dynamic LDS: limbs [G][384], meta [G] int4, then (MODE 2) the tile's
-    // scales [16][G] bf16 and zero points [16][G] u8
+    // dynamic LDS: limbs [R][G][384], meta [R][G] int4, then (staged) the
+    // tile's scales [16][G] bf16 and zero points [16][G] u8
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
-    __shared__ float red[MAXW][16];
+    __shared__ float red[MAXW][16 * R];
     __shared__ int arrived;
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
     const int KS = int(blockDim.x) >> 6;
     const int G = int(p.G);
     const int gbeg = wave * p.gs < G ? wave * p.gs : G;
     const int gs = (gbeg + p.gs < G ? gbeg + p.gs : G) - gbeg;
-    int4* ms1 = reinterpret_cast<int4*>(xs1 + G * kLimbRec);
-    int8_t* tmeta = xs1 + G * (kLimbRec + 16);
+    const int M = R == 1 ? 1 : p.M;  // activation rows (R = 4: 1..4)
+    int4* ms1 = reinterpret_cast<int4*>(xs1 + R * G * kLimbRec);
+    int8_t* tmeta = xs1 + R * G * (kLimbRec + 16);
     const TileSel ts = select_tile(p, int(blockIdx.x));
     const bool staged = MODE == 2 && p.S == 2;
 
@@ -499,14 +508,18 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     uint32_t bias;
     {
         const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
-        bias = __builtin_amdgcn_raw_buffer_load_b16(rb, lane < 16 ? uint32_t(ts.row0 + ln) * 2 : kOob, 0, 0);
+        bias = __builtin_amdgcn_raw_buffer_load_b16(rb, lane < 16 * M ? uint32_t(ts.row0 + ln) * 2 : kOob, 0, 0);
     }
     constexpr int XP = NG / 4;
-    float xv[XP][8];
+    float xv[R][XP][8];
 #pragma unroll
-    for (int t = 0; t < XP; t++) {
-        const int g = 4 * t + kg < gs ? gbeg + 4 * t + kg : (gs > 0 ? gbeg + gs - 1 : 0);
-        load_x8<MODE >= 1 ? 2 : 0>(p.x, int64_t(g) * kGroup + ln * 8, p.K, xv[t]);
+    for (int m = 0; m < R; m++) {
+        if (m >= M) break;  // uniform
+#pragma unroll
+        for (int t = 0; t < XP; t++) {
+            const int g = 4 * t + kg < gs ? gbeg + 4 * t + kg : (gs > 0 ? gbeg + gs - 1 : 0);
+            load_x8<MODE >= 1 ? 2 : 0>(p.x + int64_t(m) * p.K, int64_t(g) * kGroup + ln * 8, p.K, xv[m][t]);
+        }
     }
     if (tid < 4) reinterpret_cast<uint32_t*>(xzero)[tid] = 0u;
     if (tid == 0) arrived = 0;
@@ -532,12 +545,16 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     if (!staged) load_meta<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln);
     load_weights<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln, kg);
 #pragma unroll
-    for (int t = 0; t < XP; t++) {
-        if (4 * t >= gs) break;  // wave-uniform
-        const int g = gbeg + 4 * t + kg;
-        const bool st = 4 * t + kg < gs;
-        const int4 md = convert_group<KIND == 1>(xv[t], ln, st, xs1 + (st ? g : gbeg) * kLimbRec);
-        if (st && ln == 0) ms1[g] = md;
+    for (int m = 0; m < R; m++) {
+        if (m >= M) break;  // uniform
+#pragma unroll
+        for (int t = 0; t < XP; t++) {
+            if (4 * t >= gs) break;  // wave-uniform
+            const int g = gbeg + 4 * t + kg;
+            const bool st = 4 * t + kg < gs;
+            const int4 md = convert_group<KIND == 1>(xv[m][t], ln, st, xs1 + (int64_t(m) * G + (st ? g : gbeg)) * kLimbRec);
+            if (st && ln == 0) ms1[m * G + g] = md;
+        }
     }
     // (each wave reads only its own limb records; the zero block is shared)
     if (staged) {
@@ -559,19 +576,19 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
 
     // 3. The slice as it lands; partials through LDS, the last wave to
     //    arrive adds them in slice order (rows k >= KS were never written).
-    const float acc = slice_dot<KIND, NG>(b, xs1, ms1, xzero, gbeg, gs, ln, kg);
-    if (lane < 16) red[wave][lane] = acc;
+    const float acc = slice_dot<KIND, NG, R>(b, xs1, ms1, xzero, G, M, gbeg, gs, ln, kg);
+    if (lane < 16 * R) red[wave][lane] = acc;
     int prior = 0;
     if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     prior = __builtin_amdgcn_readfirstlane(prior);
-    if (prior != KS - 1 || lane >= 16) return;
-    float sum = red[0][ln];
+    if (prior != KS - 1 || lane >= 16 * M) return;
+    float sum = red[0][lane];
 #pragma unroll
     for (int k = 1; k < MAXW; k++) {
-        const float v = red[k][ln];
+        const float v = red[k][lane];
         sum += k < KS ? v : 0.0f;
     }
-    if (ts.row0 + lane < ts.m.N) ts.m.y[ts.row0 + lane] = sum + __uint_as_float(bias << 16);
+    if (ts.row0 + ln < ts.m.N) ts.m.y[int64_t(kg) * ts.m.N + ts.row0 + ln] = sum + __uint_as_float(bias << 16);
 }
 
 // ------------------------------------------------------------------ 2..32 rows
@@ -1025,10 +1042,10 @@ struct G1Plan {
 // memory pipeline.  ng = 0 when the 1-row kernel does not apply (the
 // slices would exceed the capacity, or the LDS copy of the converted row
 // would exceed 64 KiB).
-G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
+G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     (void)cus;
     G1Plan pl{0, 0, 0, 0, 1};
-    if (G * (kLimbRec + 16) > 64 * 1024) return pl;
+    if (R * G * (kLimbRec + 16) > 64 * 1024) return pl;
     const int maxw = kind == 1 ? 16 : 8;
     pl.ng = kind == 1 ? 12 : 20;
     pl.gs = int((G + maxw - 1) / maxw);
@@ -1042,19 +1059,27 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus) {
     if (pl.gs > G) pl.gs = int(G);
     pl.ks = int((G + pl.gs - 1) / pl.gs);
     if (pl.gs > pl.ng || pl.ks > maxw) pl.ng = 0;
+    // 2..4 rows: 16-byte aligned rows (MODE 2) and at most 4 (int4) / 8
+    // (int8) groups per slice: the activations of 4 rows stay in registers
+    if (R > 1 && (mode != 2 || pl.ng > (kind == 1 ? 4 : 8))) pl.ng = 0;
     return pl;
 }
 
 template <int KIND, int NG, int MAXW>
 void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
-    if (mode == 2) gemv1_kernel<KIND, NG, 2, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
-    else if (mode == 1) gemv1_kernel<KIND, NG, 1, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
-    else gemv1_kernel<KIND, NG, 0, MAXW><<<grid, 64 * ks, lds, stream>>>(p);
+    if (p.M > 1) {
+        if constexpr (NG <= (KIND == 1 ? 4 : 8)) gemv1_kernel<KIND, NG, 2, MAXW, 4><<<grid, 64 * ks, lds, stream>>>(p);
+        return;
+    }
+    if (mode == 2) gemv1_kernel<KIND, NG, 2, MAXW, 1><<<grid, 64 * ks, lds, stream>>>(p);
+    else if (mode == 1) gemv1_kernel<KIND, NG, 1, MAXW, 1><<<grid, 64 * ks, lds, stream>>>(p);
+    else gemv1_kernel<KIND, NG, 0, MAXW, 1><<<grid, 64 * ks, lds, stream>>>(p);
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
+// M = 1, or 2..4 rows (a plan made for R = 4) of x at stride K.
 hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n,
-                        const G1Plan& pl, int mode, hipStream_t stream) {
+                        const G1Plan& pl, int mode, hipStream_t stream, int M = 1) {
     const int64_t K = W[0].cols, G = W[0].groups;
     GemvParams p{};
     int tiles = 0;
@@ -1065,10 +1090,10 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     p.nmat = n;
     p.K = K; p.G = G;
     p.x = x;
-    p.M = 1;
+    p.M = M;
     p.gs = pl.gs;
     p.ntiles = tiles;
-    size_t lds = size_t(G) * (kLimbRec + 16);
+    size_t lds = size_t(M > 1 ? 4 : 1) * G * (kLimbRec + 16);
     // Staged scales / zero points on wide launches (7B int4 gate|up 16.9 ->
     // 15.9 us); narrow ones (under 4 workgroups per CU) lose more to the
     // extra barrier than they save (o 4.8 -> 5.1 us).  Not where the 48 G
@@ -1582,13 +1607,14 @@ hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, flo
 
 }  // namespace
 
-// A 1-row preparation that the 1-row kernel will consume is a copy of x
-// (the kernel converts it itself); anything else is converted to limbs.
+// A preparation of 1..4 rows that the 1-row kernel will consume is a copy
+// of x (the kernel converts it itself); anything else is converted (f16
+// split or limbs).
 hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
     const int64_t G = (K + kGroup - 1) / kGroup;
     hipError_t e;
-    if (M == 1 && gemv1_plan(G, kind, gemv1_mode(K, G, ws->xf), 1, device_cu_count()).ng > 0) {
-        e = hipMemcpyAsync(ws->xf, x, sizeof(float) * size_t(K), hipMemcpyDeviceToDevice, stream);
+    if (M <= 4 && gemv1_plan(G, kind, gemv1_mode(K, G, ws->xf), 1, device_cu_count(), M > 1 ? 4 : 1).ng > 0) {
+        e = hipMemcpyAsync(ws->xf, x, sizeof(float) * size_t(M) * size_t(K), hipMemcpyDeviceToDevice, stream);
         ws->prep_copy = true;
         ws->prep_h = false;
     } else if (gemvh_applies(K, M)) {
@@ -1611,8 +1637,8 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
     if (ws->prep_copy) {
         const int64_t K = W[0].cols, G = W[0].groups;
         const int mode = gemv1_mode(K, G, ws->xf);
-        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count());
-        if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), M > 1 ? 4 : 1);
+        if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream, M);
         return hipErrorInvalidValue;
     }
     if (ws->prep_h) return launch_gemvh(W, bias, y, n, M, ws, stream);
@@ -1627,10 +1653,13 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
-    if (M == 1) {
+    if (M <= 4) {
+        // the 1-row kernel converts x itself; 2..4 rows share each weight
+        // operand (no preparation launch, and the workspace's preparation
+        // stays as it was)
         const int mode = gemv1_mode(K, G, x);
-        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count());
-        if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), M > 1 ? 4 : 1);
+        if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream, M);
     }
     ws->prep_copy = false;
     ws->prep_M = M;

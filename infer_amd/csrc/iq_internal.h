@@ -25,7 +25,7 @@ struct QView {
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
-    float* xf = nullptr;       // [kMaxKp] fp32: 1-row activation copied by a prep
+    float* xf = nullptr;       // [4][kMaxKp] fp32: 1..4 activation rows copied by a prep
     int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs, or the f16 hi/lo
                                // A operands [kMaxRowsGemv/16][kMaxKp/128][8 KiB] (gemvh)
     int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, sum X0, 256 sum X1 + sum X2, 0}
@@ -34,7 +34,7 @@ struct Workspace {
     int prep_M = 0;
     int64_t prep_K = 0;
     int prep_kind = -1;
-    bool prep_copy = false;   // the preparation is a copy of x in xf (1 row)
+    bool prep_copy = false;   // the preparation is a copy of x in xf (1..4 rows)
     bool prep_h = false;      // the preparation is the f16 hi/lo split for gemvh (xq, xmeta)
 };
 

@@ -159,6 +159,37 @@ def test_gemv_multi_direct(kind, M):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_gemv_few_rows_in_the_one_row_kernel(kind, M):
+    """2..4 rows through the 1-row kernel (rows packed 4 limbs apart on one
+    MFMA operand): ragged N, a bias, the 7B gate|up width in one call, and
+    an inf in one row leaving the other rows exact."""
+    rng = np.random.default_rng(151 + kind + M)
+    for K, Ns in ((3584, (1000, 37)), (3584, (18944, 18944)), (1536, (8960,))):
+        Ws = [QFix(rng, N, K, kind, sd=0.02) for N in Ns]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        bb, bd = bias_of(rng, Ns[0])
+        ys = [out_buffer(M, W.rows) for W in Ws]
+        say("gemv few rows", kind, M, K, Ns)
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], [bd] + [None] * (len(Ws) - 1), M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y) in enumerate(zip(Ws, ys)):
+            check_linear(y, x, W, bb if i == 0 else None, M, f"few rows[{i}] kind={kind} M={M} K={K}")
+    K, N = 3584, 512
+    W = QFix(rng, N, K, kind, sd=0.02)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[M - 1, 1000] = np.inf
+    y = out_buffer(M, N)
+    ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()[: M * N].reshape(M, N)
+    assert not np.any(np.isfinite(got[M - 1]))
+    ref, cond = O.linear_dq_f64(x[: M - 1], W.dq, None)
+    err = np.abs(got[: M - 1].astype(np.float64) - ref)
+    assert float((err / np.maximum(cond, 1e-30)).max()) <= 5e-6
+
+
+@pytest.mark.parametrize("kind", [0, 1])
 def test_gemv_unaligned_activation_row(kind):
     """1 row whose fp32 activations start 4 bytes past a 16-byte boundary."""
     rng = np.random.default_rng(61 + kind)
@@ -177,21 +208,22 @@ def test_gemv_unaligned_activation_row(kind):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-def test_gemv_prep_keeps_its_input(kind):
-    """A 1-row preparation holds the activations of the time of the call:
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_prep_keeps_its_input(kind, M):
+    """A 1..4-row preparation holds the activations of the time of the call:
     overwriting x afterwards does not change what gemv_prepped computes."""
-    rng = np.random.default_rng(71 + kind)
+    rng = np.random.default_rng(71 + kind + M)
     N, K = 512, 3584
     W = QFix(rng, N, K, kind, sd=0.02)
-    x = rng.standard_normal((1, K), dtype=np.float32)
+    x = rng.standard_normal((M, K), dtype=np.float32)
     xd = torch.from_numpy(x).cuda()
-    ops.gemv_prep(xd, 1, K, kind)
+    ops.gemv_prep(xd, M, K, kind)
     xd.fill_(1e30)
-    y = out_buffer(1, N)
-    say("gemv prep snapshot", kind)
-    ops.gemv_prepped(W.view, None, 1, K, N, y)
+    y = out_buffer(M, N)
+    say("gemv prep snapshot", kind, M)
+    ops.gemv_prepped(W.view, None, M, K, N, y)
     torch.cuda.synchronize()
-    check_linear(y, x, W, None, 1, f"prep snapshot kind={kind}")
+    check_linear(y, x, W, None, M, f"prep snapshot kind={kind} M={M}")
 
 
 @pytest.mark.parametrize("kind", [0, 1])
