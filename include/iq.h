@@ -68,10 +68,11 @@ int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64
 
 /* The two halves of iq_gemv, for callers that multiply one activation
  * block by several matrices (q/k/v, gate/up share their input):
- * iq_gemv_prep converts x [B][in] (fp32) once into the device workspace
- * (per row and 128-column group: a power-of-two scale 2^-k and the integer
- * rint(x * 2^k) as three signed byte limbs, in the column order that
- * `kind`'s weight unpacking produces);
+ * iq_gemv_prep takes x [B][in] (fp32) once into the device workspace: a
+ * copy for B <= 4 (the GEMV kernel converts it itself), otherwise per row
+ * and 128-column group a power-of-two scale 2^-k and x * 2^k as two fp16
+ * terms (or as three signed byte limbs of rint(x * 2^k)), in the column
+ * order that `kind`'s weight unpacking produces;
  * iq_gemv_prepped then runs the GEMV of any matrix of that kind and width on
  * the prepared block.  A prepared block stays valid until the next
  * iq_gemv / iq_gemv_prep on the device (stream order).  iq_gemv_prepped
@@ -91,11 +92,11 @@ int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const
                           int64_t in, float* const* ys, void* stream);
 
 /* iq_gemv for n <= 4 matrices of one kind and width sharing the activations
- * x [B][in]: at B = 1 one launch reads x and all n matrices (the activation
- * conversion happens inside the GEMV kernel); at other B, x is converted once
- * and each matrix runs its own launch.  Same matrix/bias conventions as
- * iq_gemv_prepped_multi; the prepared block of the workspace is overwritten
- * when B > 1.  No reference counterpart (see iq_gemv_prepped_multi). */
+ * x [B][in]: one GEMV launch reads x and all n matrices (at B <= 4 the
+ * activation conversion happens inside it; at larger B a conversion launch
+ * precedes it, and split-K shapes add a reduction launch).  Same matrix/bias
+ * conventions as iq_gemv_prepped_multi; the prepared block of the workspace
+ * may be overwritten.  No reference counterpart (see iq_gemv_prepped_multi). */
 int iq_gemv_multi(const float* x, const iq_view* const* Ws, int n, const uint16_t* const* biases, int B,
                   int64_t in, float* const* ys, void* stream);
 
