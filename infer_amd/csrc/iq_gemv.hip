@@ -481,8 +481,12 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // order, so the sum is deterministic and no wave waits for the others.
 template <int KIND, int NG, int MODE, int MAXW, int R>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
-    // dynamic LDS: limbs [R][G][384], meta [R][G] int4, then (staged) the
-    // tile's scales [16][G] bf16 and zero points [16][G] u8
+    // dynamic LDS: limbs [RR][G][384], meta [R][G] int4, then (staged) the
+    // tile's scales [16][G] bf16 and zero points [16][G] u8.  R = 8 runs
+    // two blocks of 4 rows through the same limb records (each wave reuses
+    // its own groups' records; the weights stay in registers).
+    constexpr int RR = R < 4 ? R : 4;  // rows per block
+    constexpr int RB = R / RR;         // blocks
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
     __shared__ float red[MAXW][16 * R];
@@ -492,9 +496,9 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     const int G = int(p.G);
     const int gbeg = wave * p.gs < G ? wave * p.gs : G;
     const int gs = (gbeg + p.gs < G ? gbeg + p.gs : G) - gbeg;
-    const int M = R == 1 ? 1 : p.M;  // activation rows (R = 4: 1..4)
-    int4* ms1 = reinterpret_cast<int4*>(xs1 + R * G * kLimbRec);
-    int8_t* tmeta = xs1 + R * G * (kLimbRec + 16);
+    const int M = R == 1 ? 1 : p.M;  // activation rows (R = 4: 1..4, R = 8: 5..8)
+    int4* ms1 = reinterpret_cast<int4*>(xs1 + RR * G * kLimbRec);
+    int8_t* tmeta = xs1 + (RR * kLimbRec + R * 16) * G;
     const TileSel ts = select_tile(p, int(blockIdx.x));
     const bool staged = MODE == 2 && p.S == 2;
 
@@ -508,7 +512,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     uint32_t bias;
     {
         const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
-        bias = __builtin_amdgcn_raw_buffer_load_b16(rb, lane < 16 * M ? uint32_t(ts.row0 + ln) * 2 : kOob, 0, 0);
+        bias = __builtin_amdgcn_raw_buffer_load_b16(rb, lane < 16 * (M < 4 ? M : 4) ? uint32_t(ts.row0 + ln) * 2 : kOob,
+                                                    0, 0);
     }
     constexpr int XP = NG / 4;
     float xv[R][XP][8];
@@ -544,18 +549,24 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     Slice<KIND, NG> b;
     if (!staged) load_meta<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln);
     load_weights<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln, kg);
+    // rows [m0, m0 + RR) into the limb records (row m at record row m - m0)
+    auto convert_rows = [&](int m0) {
 #pragma unroll
-    for (int m = 0; m < R; m++) {
-        if (m >= M) break;  // uniform
+        for (int mm = 0; mm < RR; mm++) {
+            const int m = m0 + mm;
+            if (m >= M) break;  // uniform
 #pragma unroll
-        for (int t = 0; t < XP; t++) {
-            if (4 * t >= gs) break;  // wave-uniform
-            const int g = gbeg + 4 * t + kg;
-            const bool st = 4 * t + kg < gs;
-            const int4 md = convert_group<KIND == 1>(xv[m][t], ln, st, xs1 + (int64_t(m) * G + (st ? g : gbeg)) * kLimbRec);
-            if (st && ln == 0) ms1[m * G + g] = md;
+            for (int t = 0; t < XP; t++) {
+                if (4 * t >= gs) break;  // wave-uniform
+                const int g = gbeg + 4 * t + kg;
+                const bool st = 4 * t + kg < gs;
+                const int4 md = convert_group<KIND == 1>(xv[m][t], ln, st,
+                                                         xs1 + (int64_t(mm) * G + (st ? g : gbeg)) * kLimbRec);
+                if (st && ln == 0) ms1[m * G + g] = md;
+            }
         }
-    }
+    };
+    convert_rows(0);
     // (each wave reads only its own limb records; the zero block is shared)
     if (staged) {
         if (wave * 64 < 2 * G) {
@@ -576,19 +587,31 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
 
     // 3. The slice as it lands; partials through LDS, the last wave to
     //    arrive adds them in slice order (rows k >= KS were never written).
-    const float acc = slice_dot<KIND, NG, R>(b, xs1, ms1, xzero, G, M, gbeg, gs, ln, kg);
-    if (lane < 16 * R) red[wave][lane] = acc;
+    float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, G, M, gbeg, gs, ln, kg);
+    if (lane < 16 * RR) red[wave][lane] = acc;
+    if constexpr (RB == 2) {
+        // rows 4..7: the wave overwrites its own records (its reads of them
+        // above come first in program order)
+        convert_rows(4);
+        acc = slice_dot<KIND, NG, RR>(b, xs1, ms1 + 4 * G, xzero, G, M - 4, gbeg, gs, ln, kg);
+        red[wave][64 + lane] = acc;
+    }
     int prior = 0;
     if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     prior = __builtin_amdgcn_readfirstlane(prior);
-    if (prior != KS - 1 || lane >= 16 * M) return;
-    float sum = red[0][lane];
+    if (prior != KS - 1) return;
 #pragma unroll
-    for (int k = 1; k < MAXW; k++) {
-        const float v = red[k][lane];
-        sum += k < KS ? v : 0.0f;
+    for (int rb = 0; rb < RB; rb++) {
+        const int m = 4 * rb + kg;  // lane group kg of block rb: row m
+        if (m >= M) break;
+        float sum = red[0][64 * rb + lane];
+#pragma unroll
+        for (int k = 1; k < MAXW; k++) {
+            const float v = red[k][64 * rb + lane];
+            sum += k < KS ? v : 0.0f;
+        }
+        if (ts.row0 + ln < ts.m.N) ts.m.y[int64_t(m) * ts.m.N + ts.row0 + ln] = sum + __uint_as_float(bias << 16);
     }
-    if (ts.row0 + ln < ts.m.N) ts.m.y[int64_t(kg) * ts.m.N + ts.row0 + ln] = sum + __uint_as_float(bias << 16);
 }
 
 // ------------------------------------------------------------------ 2..32 rows
@@ -1029,6 +1052,22 @@ int gemv1_mode(int64_t K, int64_t G, const float* x) {
 // (ks), the slice capacity NG of the kernel instance, the grid and the tiles
 // per workgroup (tpw, 1 with the instances built here).
 
+// Rows of the 1-row kernel instance for M activation rows, and its dynamic
+// LDS (limbs of up to 4 rows, meta records of all).
+int gemv1_rows(int M) { return M > 4 ? 8 : (M > 1 ? 4 : 1); }
+size_t gemv1_lds(int64_t G, int R) { return size_t(G) * ((R < 4 ? R : 4) * kLimbRec + R * 16); }
+
+// 1..4 rows always; 5..8 rows (two blocks of 4, the second converted after
+// the first is multiplied) only on narrow launches, measured at 7B: o (224
+// tiles) 10.1 -> 9.2 us at 8 rows and q|k|v (288) 12.2 -> 10.5 at 5, but
+// q|k|v 12.2 -> 13.1 at 8 rows and gate|up 35 -> 41 / 53 us at 5 / 8.
+bool gemv1_rows_preferred(int M, int tiles) {
+    if (M <= 4) return true;
+    if (M > 8) return false;
+    const int cus = device_cu_count();
+    return tiles <= cus || (M <= 6 && tiles < 4 * cus);
+}
+
 struct G1Plan {
     int gs, ks, ng, grid, tpw;
 };
@@ -1045,7 +1084,7 @@ struct G1Plan {
 G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     (void)cus;
     G1Plan pl{0, 0, 0, 0, 1};
-    if (R * G * (kLimbRec + 16) > 64 * 1024) return pl;
+    if (gemv1_lds(G, R) > 64 * 1024) return pl;
     const int maxw = kind == 1 ? 16 : 8;
     pl.ng = kind == 1 ? 12 : 20;
     pl.gs = int((G + maxw - 1) / maxw);
@@ -1059,14 +1098,19 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     if (pl.gs > G) pl.gs = int(G);
     pl.ks = int((G + pl.gs - 1) / pl.gs);
     if (pl.gs > pl.ng || pl.ks > maxw) pl.ng = 0;
-    // 2..4 rows: 16-byte aligned rows (MODE 2) and at most 4 (int4) / 8
-    // (int8) groups per slice: the activations of 4 rows stay in registers
-    if (R > 1 && (mode != 2 || pl.ng > (kind == 1 ? 4 : 8))) pl.ng = 0;
+    // 2..8 rows: 16-byte aligned rows (MODE 2) and at most 4 (int4, or 8
+    // rows) / 8 (int8) groups per slice: the activations of all rows stay in
+    // registers
+    if (R > 1 && (mode != 2 || pl.ng > (kind == 1 || R == 8 ? 4 : 8))) pl.ng = 0;
     return pl;
 }
 
 template <int KIND, int NG, int MAXW>
 void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
+    if (p.M > 4) {
+        if constexpr (NG <= 4) gemv1_kernel<KIND, NG, 2, MAXW, 8><<<grid, 64 * ks, lds, stream>>>(p);
+        return;
+    }
     if (p.M > 1) {
         if constexpr (NG <= (KIND == 1 ? 4 : 8)) gemv1_kernel<KIND, NG, 2, MAXW, 4><<<grid, 64 * ks, lds, stream>>>(p);
         return;
@@ -1077,7 +1121,7 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
-// M = 1, or 2..4 rows (a plan made for R = 4) of x at stride K.
+// M = 1, or 2..8 rows (a plan made for gemv1_rows(M)) of x at stride K.
 hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n,
                         const G1Plan& pl, int mode, hipStream_t stream, int M = 1) {
     const int64_t K = W[0].cols, G = W[0].groups;
@@ -1093,7 +1137,7 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     p.M = M;
     p.gs = pl.gs;
     p.ntiles = tiles;
-    size_t lds = size_t(M > 1 ? 4 : 1) * G * (kLimbRec + 16);
+    size_t lds = gemv1_lds(G, gemv1_rows(M));
     // Staged scales / zero points on wide launches (7B int4 gate|up 16.9 ->
     // 15.9 us); narrow ones (under 4 workgroups per CU) lose more to the
     // extra barrier than they save (o 4.8 -> 5.1 us).  Not where the 48 G
@@ -1613,7 +1657,7 @@ hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, flo
 hipError_t launch_xprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
     const int64_t G = (K + kGroup - 1) / kGroup;
     hipError_t e;
-    if (M <= 4 && gemv1_plan(G, kind, gemv1_mode(K, G, ws->xf), 1, device_cu_count(), M > 1 ? 4 : 1).ng > 0) {
+    if (M <= 4 && gemv1_plan(G, kind, gemv1_mode(K, G, ws->xf), 1, device_cu_count(), gemv1_rows(M)).ng > 0) {
         e = hipMemcpyAsync(ws->xf, x, sizeof(float) * size_t(M) * size_t(K), hipMemcpyDeviceToDevice, stream);
         ws->prep_copy = true;
         ws->prep_h = false;
@@ -1637,7 +1681,7 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
     if (ws->prep_copy) {
         const int64_t K = W[0].cols, G = W[0].groups;
         const int mode = gemv1_mode(K, G, ws->xf);
-        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), M > 1 ? 4 : 1);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), gemv1_rows(M));
         if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream, M);
         return hipErrorInvalidValue;
     }
@@ -1653,12 +1697,12 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
-    if (M <= 4) {
-        // the 1-row kernel converts x itself; 2..4 rows share each weight
+    if (gemv1_rows_preferred(M, total_tiles(W, n))) {
+        // the 1-row kernel converts x itself; 2..8 rows share each weight
         // operand (no preparation launch, and the workspace's preparation
         // stays as it was)
         const int mode = gemv1_mode(K, G, x);
-        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), M > 1 ? 4 : 1);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), gemv1_rows(M));
         if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream, M);
     }
     ws->prep_copy = false;

@@ -159,11 +159,12 @@ def test_gemv_multi_direct(kind, M):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 7, 8])
 def test_gemv_few_rows_in_the_one_row_kernel(kind, M):
-    """2..4 rows through the 1-row kernel (rows packed 4 limbs apart on one
-    MFMA operand): ragged N, a bias, the 7B gate|up width in one call, and
-    an inf in one row leaving the other rows exact."""
+    """2..8 rows through the 1-row kernel (rows packed 4 limbs apart on one
+    MFMA operand, two blocks of 4 past 4 rows): ragged N, a bias, the 7B
+    gate|up width in one call, and an inf in one row leaving the other rows
+    exact."""
     rng = np.random.default_rng(151 + kind + M)
     for K, Ns in ((3584, (1000, 37)), (3584, (18944, 18944)), (1536, (8960,))):
         Ws = [QFix(rng, N, K, kind, sd=0.02) for N in Ns]
