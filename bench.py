@@ -296,6 +296,16 @@ def profile_workload(torch, ops):
     torch.cuda.synchronize()
 
 
+def profile_gemm_workload(torch, ops):
+    """Fixed short workload for `rocprofv3 --pmc` runs of the prefill GEMM
+    (config 5, T = 1024, bf16 activations): int8 and int4 gate/up 18944x3584
+    and down 3584x18944, each launched 2 + 3 times by bench_gemm."""
+    for kind in (0, 1):
+        for N, K in ((I7, H7), (H7, I7)):
+            bench_gemm(torch, ops, kind, 1024, N, K, reps=3)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -305,6 +315,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", action="store_true",
                     help="short fixed workload for rocprofv3 counter runs (prints nothing)")
+    ap.add_argument("--profile-gemm", action="store_true",
+                    help="short fixed prefill-GEMM workload for rocprofv3 counter runs (prints nothing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -317,6 +329,9 @@ def main():
     ops.init(0)
     if args.profile:
         profile_workload(torch, ops)
+        return
+    if args.profile_gemm:
+        profile_gemm_workload(torch, ops)
         return
     t_setup = time.perf_counter()
 
