@@ -1048,10 +1048,6 @@ int gemv1_mode(int64_t K, int64_t G, const float* x) {
     return G % 4 ? 1 : 2;
 }
 
-// Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
-// (ks), the slice capacity NG of the kernel instance, the grid and the tiles
-// per workgroup (tpw, 1 with the instances built here).
-
 // Rows of the 1-row kernel instance for M activation rows, and its dynamic
 // LDS (limbs of up to 4 rows, meta records of all).
 int gemv1_rows(int M) { return M > 4 ? 8 : (M > 1 ? 4 : 1); }
@@ -1068,8 +1064,11 @@ bool gemv1_rows_preferred(int M, int tiles) {
     return tiles <= cus || (M <= 6 && tiles < 4 * cus);
 }
 
+// Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
+// (ks), the slice capacity NG of the kernel instance (0: not applicable) and
+// the grid (one workgroup per 16-row tile).
 struct G1Plan {
-    int gs, ks, ng, grid, tpw;
+    int gs, ks, ng, grid;
 };
 
 // Kernel instances: one 16-row tile per workgroup (measured faster than
@@ -1083,7 +1082,7 @@ struct G1Plan {
 // would exceed 64 KiB).
 G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     (void)cus;
-    G1Plan pl{0, 0, 0, 0, 1};
+    G1Plan pl{0, 0, 0, 0};
     if (gemv1_lds(G, R) > 64 * 1024) return pl;
     const int maxw = kind == 1 ? 16 : 8;
     pl.ng = kind == 1 ? 12 : 20;

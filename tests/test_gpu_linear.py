@@ -166,7 +166,8 @@ def test_gemv_few_rows_in_the_one_row_kernel(kind, M):
     gate|up width in one call, and an inf in one row leaving the other rows
     exact."""
     rng = np.random.default_rng(151 + kind + M)
-    for K, Ns in ((3584, (1000, 37)), (3584, (18944, 18944)), (1536, (8960,))):
+    # K = 6144: int8 slices of 8 groups (the 8-group instance at 2..4 rows)
+    for K, Ns in ((3584, (1000, 37)), (3584, (18944, 18944)), (1536, (8960,)), (6144, (700,))):
         Ws = [QFix(rng, N, K, kind, sd=0.02) for N in Ns]
         x = rng.standard_normal((M, K), dtype=np.float32)
         bb, bd = bias_of(rng, Ns[0])
