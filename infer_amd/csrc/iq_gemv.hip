@@ -265,6 +265,7 @@ struct GemvParams {
     float* part;
     int M, S, gs, nrb;
     int ntiles;  // 1-row kernel: 16-row tiles over all matrices
+    int kr, gr;  // 1-row kernel: K ranges (workgroups per tile) and groups per range
 };
 
 // 16 bytes of a row at byte offset `off`, zero past `row_bytes` (unaligned
@@ -428,12 +429,15 @@ __device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParam
 // running sum of activation row l/16 (R = 4) or row 0 (R = 1, lanes 0..15).
 template <int KIND, int NG, int R>
 __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_t* xs, const int4* ms,
-                                           const int8_t* xzero, int G, int M, int gbeg, int gs, int ln, int kg) {
+                                           const int8_t* xzero, int RS, int glo, int M, int gbeg, int gs, int ln,
+                                           int kg) {
+    // records of row m, group g at (m RS + g - glo) (RS records per row,
+    // the first of them group glo)
     float acc = 0.0f;
     const int am = R == 1 ? 0 : ln >> 2, aL = R == 1 ? ln : ln & 3;  // A row of this lane
     const bool alive = aL < 3 && am < M;
-    const int8_t* xrow = xs + int64_t(am) * G * kLimbRec + aL * kGroup + kg * 16;
-    const int4* mrow = ms + (R == 1 ? 0 : kg) * G;
+    const int xoff = (am * RS - glo) * kLimbRec + aL * kGroup + kg * 16;
+    const int moff = (R == 1 ? 0 : kg) * RS - glo;
     // blocks of 4 groups: an early exit over at most 8 iterations still
     // unrolls fully (so the slice stays in registers)
 #pragma unroll
@@ -446,7 +450,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
             const int g = gbeg + (ok ? gl : 0);
             int4v_t a0, a1, b0, b1;
             {
-                const int8_t* pa = alive ? xrow + g * kLimbRec : xzero;
+                const int8_t* pa = alive ? xs + (xoff + g * kLimbRec) : xzero;
                 a0 = *reinterpret_cast<const int4v_t*>(pa);
                 a1 = *reinterpret_cast<const int4v_t*>(pa + (alive ? 64 : 0));
             }
@@ -463,7 +467,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
             const uint32_t sw = b.s[gl / 2];
             const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
             const int z = KIND == 1 ? int((b.z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
-            const float nacc = combine(acc, D[0], D[1], D[2], z, mrow[g], sc);
+            const float nacc = combine(acc, D[0], D[1], D[2], z, ms[moff + g], sc);
             acc = ok ? nacc : acc;
         }
     }
@@ -479,7 +483,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // instead of every wave fetching the same lines for its slice.  The slice partials are added
 // through LDS by whichever wave finishes last (an LDS counter), in slice
 // order, so the sum is deterministic and no wave waits for the others.
-template <int KIND, int NG, int MODE, int MAXW, int R>
+template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // dynamic LDS: limbs [RR][G][384], meta [R][G] int4, then (staged) the
     // tile's scales [16][G] bf16 and zero points [16][G] u8.  R = 8 runs
@@ -494,13 +498,18 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
     const int KS = int(blockDim.x) >> 6;
     const int G = int(p.G);
-    const int gbeg = wave * p.gs < G ? wave * p.gs : G;
-    const int gs = (gbeg + p.gs < G ? gbeg + p.gs : G) - gbeg;
+    // K range of this workgroup: groups [glo, ghi); RS = LDS records per row
+    // (KSPLIT: several ranges per tile, 2..4 rows only)
+    const int kr = KSPLIT ? p.kr : 1, range = KSPLIT ? int(blockIdx.x) % kr : 0;
+    const int RS = KSPLIT ? p.gr : G, glo = range * RS, ghi = glo + RS < G ? glo + RS : G;
+    const int gbeg = glo + wave * p.gs < ghi ? glo + wave * p.gs : ghi;
+    const int gs = (gbeg + p.gs < ghi ? gbeg + p.gs : ghi) - gbeg;
     const int M = R == 1 ? 1 : p.M;  // activation rows (R = 4: 1..4, R = 8: 5..8)
-    int4* ms1 = reinterpret_cast<int4*>(xs1 + RR * G * kLimbRec);
-    int8_t* tmeta = xs1 + (RR * kLimbRec + R * 16) * G;
-    const TileSel ts = select_tile(p, int(blockIdx.x));
-    const bool staged = MODE == 2 && p.S == 2;
+    int4* ms1 = reinterpret_cast<int4*>(xs1 + RR * RS * kLimbRec);
+    int8_t* tmeta = xs1 + (RR * kLimbRec + R * 16) * RS;
+    const int tile = KSPLIT ? int(blockIdx.x) / kr : int(blockIdx.x);
+    const TileSel ts = select_tile(p, tile);
+    const bool staged = MODE == 2 && p.S == 2;  // (only with kr == 1)
 
     // 1. This wave's activations: pass t converts groups gbeg + 4t + kg,
     //    16 lanes (one DPP row) per group, 8 columns per lane.  Every wave
@@ -561,8 +570,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
                 const int g = gbeg + 4 * t + kg;
                 const bool st = 4 * t + kg < gs;
                 const int4 md = convert_group<KIND == 1>(xv[m][t], ln, st,
-                                                         xs1 + (int64_t(mm) * G + (st ? g : gbeg)) * kLimbRec);
-                if (st && ln == 0) ms1[m * G + g] = md;
+                                                         xs1 + (mm * RS + (st ? g : gbeg) - glo) * kLimbRec);
+                if (st && ln == 0) ms1[m * RS + g - glo] = md;
             }
         }
     };
@@ -587,13 +596,13 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
 
     // 3. The slice as it lands; partials through LDS, the last wave to
     //    arrive adds them in slice order (rows k >= KS were never written).
-    float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, G, M, gbeg, gs, ln, kg);
+    float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, RS, glo, M, gbeg, gs, ln, kg);
     if (lane < 16 * RR) red[wave][lane] = acc;
     if constexpr (RB == 2) {
         // rows 4..7: the wave overwrites its own records (its reads of them
         // above come first in program order)
         convert_rows(4);
-        acc = slice_dot<KIND, NG, RR>(b, xs1, ms1 + 4 * G, xzero, G, M - 4, gbeg, gs, ln, kg);
+        acc = slice_dot<KIND, NG, RR>(b, xs1, ms1 + 4 * RS, xzero, RS, glo, M - 4, gbeg, gs, ln, kg);
         red[wave][64 + lane] = acc;
     }
     int prior = 0;
@@ -610,7 +619,9 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
             const float v = red[k][64 * rb + lane];
             sum += k < KS ? v : 0.0f;
         }
-        if (ts.row0 + ln < ts.m.N) ts.m.y[int64_t(m) * ts.m.N + ts.row0 + ln] = sum + __uint_as_float(bias << 16);
+        if (ts.row0 + ln >= ts.m.N) continue;
+        if (kr == 1) ts.m.y[int64_t(m) * ts.m.N + ts.row0 + ln] = sum + __uint_as_float(bias << 16);
+        else p.part[(int64_t(range) * M + m) * (int64_t(p.ntiles) * 16) + int64_t(tile) * 16 + ln] = sum;
     }
 }
 
@@ -1065,10 +1076,10 @@ bool gemv1_rows_preferred(int M, int tiles) {
 }
 
 // Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
-// (ks), the slice capacity NG of the kernel instance (0: not applicable) and
-// the grid (one workgroup per 16-row tile).
+// (ks), the slice capacity NG of the kernel instance (0: not applicable),
+// the grid (kr workgroups per 16-row tile, each a K range of gr groups).
 struct G1Plan {
-    int gs, ks, ng, grid;
+    int gs, ks, ng, grid, kr, gr;
 };
 
 // Kernel instances: one 16-row tile per workgroup (measured faster than
@@ -1082,20 +1093,33 @@ struct G1Plan {
 // would exceed 64 KiB).
 G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     (void)cus;
-    G1Plan pl{0, 0, 0, 0};
-    if (gemv1_lds(G, R) > 64 * 1024) return pl;
+    G1Plan pl{0, 0, 0, 0, 1, int(G)};
+    // 2..4 rows: the limbs of a long row split K into ranges (workgroups per
+    // tile) whose records fit 64 KiB, multiples of 4 groups (7B down at 2
+    // rows: int4 27.0 -> 18.0, int8 30.2 -> 23.8 us); 1 row, and 5..8 rows
+    // (measured slower split: down 27 -> 32 us at 8 rows): one range
+    if (R == 4) {
+        while (gemv1_lds(pl.gr, R) > 64 * 1024 && pl.kr < 8) {
+            pl.kr++;
+            pl.gr = int((G + pl.kr - 1) / pl.kr + 3) / 4 * 4;
+        }
+        pl.kr = int((G + pl.gr - 1) / pl.gr);
+        if (pl.kr > 1 && int64_t(pl.kr) * 8 * ntiles * 16 > kPartialFloats) return G1Plan{0, 0, 0, 0, 1, int(G)};
+    }
+    if (gemv1_lds(pl.gr, R) > 64 * 1024) return pl;
+    const int64_t GR = pl.gr;
     const int maxw = kind == 1 ? 16 : 8;
     pl.ng = kind == 1 ? 12 : 20;
-    pl.gs = int((G + maxw - 1) / maxw);
+    pl.gs = int((GR + maxw - 1) / maxw);
     if (mode == 2) pl.gs = (pl.gs + 3) / 4 * 4;
     for (int c : {4, 8, 12})
         if (pl.gs <= c && c < pl.ng) {
             pl.ng = c;
             break;
         }
-    pl.grid = ntiles;
-    if (pl.gs > G) pl.gs = int(G);
-    pl.ks = int((G + pl.gs - 1) / pl.gs);
+    pl.grid = ntiles * pl.kr;
+    if (pl.gs > GR) pl.gs = int(GR);
+    pl.ks = int((GR + pl.gs - 1) / pl.gs);
     if (pl.gs > pl.ng || pl.ks > maxw) pl.ng = 0;
     // 2..8 rows: 16-byte aligned rows (MODE 2) and at most 4 (int4, or 8
     // rows) / 8 (int8) groups per slice: the activations of all rows stay in
@@ -1107,22 +1131,26 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
 template <int KIND, int NG, int MAXW>
 void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
     if (p.M > 4) {
-        if constexpr (NG <= 4) gemv1_kernel<KIND, NG, 2, MAXW, 8><<<grid, 64 * ks, lds, stream>>>(p);
+        if constexpr (NG <= 4) gemv1_kernel<KIND, NG, 2, MAXW, 8, false><<<grid, 64 * ks, lds, stream>>>(p);
         return;
     }
     if (p.M > 1) {
-        if constexpr (NG <= (KIND == 1 ? 4 : 8)) gemv1_kernel<KIND, NG, 2, MAXW, 4><<<grid, 64 * ks, lds, stream>>>(p);
+        if constexpr (NG <= (KIND == 1 ? 4 : 8)) {
+            if (p.kr > 1) gemv1_kernel<KIND, NG, 2, MAXW, 4, true><<<grid, 64 * ks, lds, stream>>>(p);
+            else gemv1_kernel<KIND, NG, 2, MAXW, 4, false><<<grid, 64 * ks, lds, stream>>>(p);
+        }
         return;
     }
-    if (mode == 2) gemv1_kernel<KIND, NG, 2, MAXW, 1><<<grid, 64 * ks, lds, stream>>>(p);
-    else if (mode == 1) gemv1_kernel<KIND, NG, 1, MAXW, 1><<<grid, 64 * ks, lds, stream>>>(p);
-    else gemv1_kernel<KIND, NG, 0, MAXW, 1><<<grid, 64 * ks, lds, stream>>>(p);
+    if (mode == 2) gemv1_kernel<KIND, NG, 2, MAXW, 1, false><<<grid, 64 * ks, lds, stream>>>(p);
+    else if (mode == 1) gemv1_kernel<KIND, NG, 1, MAXW, 1, false><<<grid, 64 * ks, lds, stream>>>(p);
+    else gemv1_kernel<KIND, NG, 0, MAXW, 1, false><<<grid, 64 * ks, lds, stream>>>(p);
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
-// M = 1, or 2..8 rows (a plan made for gemv1_rows(M)) of x at stride K.
+// M = 1, or 2..8 rows (a plan made for gemv1_rows(M)) of x at stride K;
+// part: the split-K partials (plans with kr > 1).
 hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n,
-                        const G1Plan& pl, int mode, hipStream_t stream, int M = 1) {
+                        const G1Plan& pl, int mode, hipStream_t stream, int M = 1, float* part = nullptr) {
     const int64_t K = W[0].cols, G = W[0].groups;
     GemvParams p{};
     int tiles = 0;
@@ -1136,7 +1164,10 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     p.M = M;
     p.gs = pl.gs;
     p.ntiles = tiles;
-    size_t lds = gemv1_lds(G, gemv1_rows(M));
+    p.kr = pl.kr;
+    p.gr = pl.gr;
+    p.part = part;
+    size_t lds = gemv1_lds(pl.gr, gemv1_rows(M));
     // Staged scales / zero points on wide launches (7B int4 gate|up 16.9 ->
     // 15.9 us); narrow ones (under 4 workgroups per CU) lose more to the
     // extra barrier than they save (o 4.8 -> 5.1 us).  Not where the 48 G
@@ -1145,7 +1176,8 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     const size_t cu_lds = 160 * 1024, staged = lds + size_t(G) * 48, wlim = size_t(32 / pl.ks);
     const size_t occ = std::min(cu_lds / lds, wlim), occ_staged = std::min(cu_lds / staged, wlim);
     p.S = 1;
-    if (mode == 2 && tiles >= 4 * device_cu_count() && staged <= 64 * 1024 && occ_staged == occ && 2 * G <= 64 * pl.ks) {
+    if (mode == 2 && pl.kr == 1 && tiles >= 4 * device_cu_count() && staged <= 64 * 1024 && occ_staged == occ &&
+        2 * G <= 64 * pl.ks) {
         p.S = 2;
         lds = staged;
     }
@@ -1160,6 +1192,13 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         else if (pl.ng == 12) launch_gemv1_m<0, 12, 8>(p, mode, pl.ks, grid, lds, stream);
         else launch_gemv1_m<0, 20, 8>(p, mode, pl.ks, grid, lds, stream);
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pl.kr == 1) return e;
+    // the K ranges' sums, in range order, + bias
+    GemvParams pr = p;
+    pr.S = pl.kr;
+    const int64_t cnt = int64_t(M) * tiles * 16;
+    gemvt_reduce_kernel<<<unsigned((cnt + 255) / 256), 256, 0, stream>>>(pr);
     return hipGetLastError();
 }
 
@@ -1681,8 +1720,13 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
         const int64_t K = W[0].cols, G = W[0].groups;
         const int mode = gemv1_mode(K, G, ws->xf);
         const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), gemv1_rows(M));
-        if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream, M);
-        return hipErrorInvalidValue;
+        if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream, M, ws->partials);
+        // (too many tiles for the split-K partials of this width): the
+        // general path on the copy, the preparation left as it was
+        const Workspace keep = *ws;
+        const hipError_t e = launch_gemv_multi(ws->xf, W, bias, y, n, M, ws, stream);
+        *ws = keep;
+        return e;
     }
     if (ws->prep_h) return launch_gemvh(W, bias, y, n, M, ws, stream);
     return launch_batched_multi(W, bias, y, n, M, ws, stream);
@@ -1702,7 +1746,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         // stays as it was)
         const int mode = gemv1_mode(K, G, x);
         const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), gemv1_rows(M));
-        if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream, M);
+        if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream, M, ws->partials);
     }
     ws->prep_copy = false;
     ws->prep_M = M;

@@ -162,12 +162,13 @@ def test_gemv_multi_direct(kind, M):
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 7, 8])
 def test_gemv_few_rows_in_the_one_row_kernel(kind, M):
     """2..8 rows through the 1-row kernel (rows packed 4 limbs apart on one
-    MFMA operand, two blocks of 4 past 4 rows): ragged N, a bias, the 7B
-    gate|up width in one call, and an inf in one row leaving the other rows
-    exact."""
+    MFMA operand, two blocks of 4 past 4 rows, long K split into ranges):
+    ragged N, a bias, the 7B gate|up width in one call, and an inf in one
+    row leaving the other rows exact."""
     rng = np.random.default_rng(151 + kind + M)
-    # K = 6144: int8 slices of 8 groups (the 8-group instance at 2..4 rows)
-    for K, Ns in ((3584, (1000, 37)), (3584, (18944, 18944)), (1536, (8960,)), (6144, (700,))):
+    # K = 6144: int8 slices of 8 groups (the 8-group instance at 2..4 rows);
+    # K = 18944: K split over several workgroups per tile + range reduction
+    for K, Ns in ((3584, (1000, 37)), (3584, (18944, 18944)), (1536, (8960,)), (6144, (700,)), (18944, (3584,))):
         Ws = [QFix(rng, N, K, kind, sd=0.02) for N in Ns]
         x = rng.standard_normal((M, K), dtype=np.float32)
         bb, bd = bias_of(rng, Ns[0])
@@ -211,11 +212,12 @@ def test_gemv_unaligned_activation_row(kind):
 
 @pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [1, 3])
-def test_gemv_prep_keeps_its_input(kind, M):
+@pytest.mark.parametrize("K", [3584, 18944])
+def test_gemv_prep_keeps_its_input(kind, M, K):
     """A 1..4-row preparation holds the activations of the time of the call:
     overwriting x afterwards does not change what gemv_prepped computes."""
     rng = np.random.default_rng(71 + kind + M)
-    N, K = 512, 3584
+    N = 512
     W = QFix(rng, N, K, kind, sd=0.02)
     x = rng.standard_normal((M, K), dtype=np.float32)
     xd = torch.from_numpy(x).cuda()
