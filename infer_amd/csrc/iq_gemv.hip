@@ -1121,10 +1121,10 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     if (pl.gs > GR) pl.gs = int(GR);
     pl.ks = int((GR + pl.gs - 1) / pl.gs);
     if (pl.gs > pl.ng || pl.ks > maxw) pl.ng = 0;
-    // 2..8 rows: 16-byte aligned rows (MODE 2) and at most 4 (int4, or 8
-    // rows) / 8 (int8) groups per slice: the activations of all rows stay in
-    // registers
-    if (R > 1 && (mode != 2 || pl.ng > (kind == 1 || R == 8 ? 4 : 8))) pl.ng = 0;
+    // 2..8 rows: 16-byte aligned rows (MODE 2; 2..4 rows also MODE 1) and
+    // at most 4 (int4, or 8 rows) / 8 (int8) groups per slice: the
+    // activations of all rows stay in registers
+    if (R > 1 && (mode == 0 || (R == 8 && mode != 2) || pl.ng > (kind == 1 || R == 8 ? 4 : 8))) pl.ng = 0;
     return pl;
 }
 
@@ -1136,8 +1136,13 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
     }
     if (p.M > 1) {
         if constexpr (NG <= (KIND == 1 ? 4 : 8)) {
-            if (p.kr > 1) gemv1_kernel<KIND, NG, 2, MAXW, 4, true><<<grid, 64 * ks, lds, stream>>>(p);
-            else gemv1_kernel<KIND, NG, 2, MAXW, 4, false><<<grid, 64 * ks, lds, stream>>>(p);
+            if (mode == 2) {
+                if (p.kr > 1) gemv1_kernel<KIND, NG, 2, MAXW, 4, true><<<grid, 64 * ks, lds, stream>>>(p);
+                else gemv1_kernel<KIND, NG, 2, MAXW, 4, false><<<grid, 64 * ks, lds, stream>>>(p);
+            } else {
+                if (p.kr > 1) gemv1_kernel<KIND, NG, 1, MAXW, 4, true><<<grid, 64 * ks, lds, stream>>>(p);
+                else gemv1_kernel<KIND, NG, 1, MAXW, 4, false><<<grid, 64 * ks, lds, stream>>>(p);
+            }
         }
         return;
     }
