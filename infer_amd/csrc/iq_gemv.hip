@@ -1621,8 +1621,12 @@ bool gemvh_applies(int64_t K, int M) {
 // per MFMA up to 8 rows, for wider calls up to 8 rows and for 1024..4095-tile
 // calls with short K (7B gate|up: 27..38 against 47..48 us); gemvh otherwise
 // (lm_head at 12..16 rows: 173 against 184 us).
-bool gemvh_preferred(int64_t K, int M, int tiles) {
+bool gemvh_preferred(int64_t K, int M, int tiles, int kind) {
     if (!gemvh_applies(K, M)) return false;
+    // int8 with long K: gemvt (7B down int8, K = 18944, at 16 / 8 rows:
+    // 38.3 -> 32.6 / 30.5 -> 29.3 us; not at K = 8960: 1.5B down 17 -> 24
+    // us; int4 stays on gemvh: 33.5 against 36.7 / 27.0 against 32.3)
+    if (kind == 0 && K / kGroup > 128) return false;
     if (tiles < 512) return true;
     if (M <= 8) return false;
     return !(tiles >= 1024 && tiles < 4096 && K / kGroup <= 64);
@@ -1757,7 +1761,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     ws->prep_M = M;
     ws->prep_K = K;
     ws->prep_kind = W[0].kind;
-    if (gemvh_preferred(K, M, total_tiles(W, n))) {
+    if (gemvh_preferred(K, M, total_tiles(W, n), W[0].kind)) {
         ws->prep_h = true;
         const hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;
