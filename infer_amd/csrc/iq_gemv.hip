@@ -1068,11 +1068,13 @@ size_t gemv1_lds(int64_t G, int R) { return size_t(G) * ((R < 4 ? R : 4) * kLimb
 // the first is multiplied) only on narrow launches, measured at 7B: o (224
 // tiles) 10.1 -> 9.2 us at 8 rows and q|k|v (288) 12.2 -> 10.5 at 5, but
 // q|k|v 12.2 -> 13.1 at 8 rows and gate|up 35 -> 41 / 53 us at 5 / 8.
-bool gemv1_rows_preferred(int M, int tiles) {
+bool gemv1_rows_preferred(int M, int tiles, int64_t G) {
     if (M <= 4) return true;
     if (M > 8) return false;
     const int cus = device_cu_count();
-    return tiles <= cus || (M <= 6 && tiles < 4 * cus);
+    // short rows convert fast: 1.5B gate (G = 12, 560 tiles) at 7 / 8 rows
+    // 11.7 -> 10.1 / 11.8 -> 10.7 us (int8)
+    return tiles <= cus || (tiles < 4 * cus && (M <= 6 || G <= 16));
 }
 
 // Shape of a 1-row launch: groups per wave slice (gs), waves per workgroup
@@ -1749,7 +1751,7 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
-    if (gemv1_rows_preferred(M, total_tiles(W, n))) {
+    if (gemv1_rows_preferred(M, total_tiles(W, n), G)) {
         // the 1-row kernel converts x itself; 2..8 rows share each weight
         // operand (no preparation launch, and the workspace's preparation
         // stays as it was)
