@@ -196,24 +196,36 @@ def kernel_roofline(torch, step, only_kind=None):
     return tot_b, tot_ms, n
 
 
-def cpu_baseline(torch, model, seconds=10.0):
+def cpu_baseline(torch, model, seconds=10.0, threads=1):
     """oracle/iq_oracle.c iqo_linear_q_f32 (= src/forward.cpp:35-47 over
     dequant(), one thread) on layer matrices of the same model, until about
-    `seconds` of CPU work; returns (GB/s of packed weights, sample text)."""
+    `seconds` of CPU work; returns (GB/s of packed weights, sample text).
+    threads > 1: each matrix's output rows split over that many host threads
+    (the C routine runs without the GIL; every output is computed exactly as
+    with one thread)."""
     import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
     from oracle import oracle as O
     rng = np.random.default_rng(0)
     done_b, t_tot, n = 0, 0.0, 0
     names = []
+    pool = ThreadPoolExecutor(threads) if threads > 1 else None
     for li, L in enumerate(model.layers):
         for name, out, inn, slot in model.shapes:
             W = L[name]
-            q = W.q.cpu().numpy()
+            q = W.q.cpu().numpy().reshape(W.rows, -1)
             s = W.scales.cpu().numpy().view(np.uint16).reshape(W.rows, W.groups)
             z = W.zeros.cpu().numpy().reshape(W.rows, W.groups) if W.zeros is not None else None
             x = rng.standard_normal((1, W.cols), dtype=np.float32)
             t0 = time.perf_counter()
-            O.linear_q_f32(x, q, s, z, int(W.kind), None, W.rows)
+            if pool is None:
+                O.linear_q_f32(x, q, s, z, int(W.kind), None, W.rows)
+            else:
+                cuts = [W.rows * i // threads for i in range(threads + 1)]
+                jobs = [pool.submit(O.linear_q_f32, x, q[a:b], s[a:b], None if z is None else z[a:b],
+                                    int(W.kind), None, b - a) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
+                for j in jobs:
+                    j.result()
             t_tot += time.perf_counter() - t0
             done_b += W.nbytes()
             n += 1
@@ -223,6 +235,44 @@ def cpu_baseline(torch, model, seconds=10.0):
         if t_tot >= seconds:
             break
     return done_b / t_tot / 1e9, f"{n} matrices ({names[0]}..{names[-1]}), {done_b / 1e6:.0f} MB packed, {t_tot:.1f} s"
+
+
+def cpu_quantize_rate():
+    """oracle iqo_quantize (src/quant.cpp:34-84 restated, one thread) on a
+    3584 x 3584 bf16 matrix, int8 and int4: GB/s of bf16 read."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(1)
+    w = O.seeded_bf16(rng, (3584, 3584), 0.02)
+    out = {}
+    for kind, kn in ((0, "int8"), (1, "int4")):
+        t0 = time.perf_counter()
+        O.quantize(w, kind)
+        dt = time.perf_counter() - t0
+        out[kn] = {"ms": round(dt * 1e3, 1), "GBps": round(w.nbytes / dt / 1e9, 3)}
+    out["sample"] = "3584 x 3584 bf16, 1 thread"
+    return out
+
+
+def hbm_copy_rate(torch, reps=20):
+    """A plain device copy of 2 GiB (torch copy_): bytes read + written per
+    second, the measured HBM ceiling beside the nominal 8 TB/s."""
+    a = torch.empty(512 << 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del a, b
+    torch.cuda.empty_cache()
+    return round(2 * (2 << 30) / (ms * 1e-3) / 1e9, 1)
 
 
 def bench_gemm(torch, ops, kind, T, N, K, reps=10, seed=5, fp32x=False):
@@ -377,6 +427,13 @@ def main():
         cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": "oracle iqo_linear_q_f32 (src/forward.cpp:35-47 over dequant(), scalar fp32, "
                          "1 thread) on the 7B int4 layer matrices at 1 row: " + cpu_sample}
+        # the same port over the host's cores (at most 16, the box's share)
+        nth = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
+        cpu_all, cpu_all_sample = cpu_baseline(torch, m4, args.cpu_seconds / 2, threads=nth)
+        detail["cpu_baseline_all_cores"] = {"value": round(cpu_all, 4), "unit": "GB/s", "cores": nth,
+                                            "kind": "port", "sample": cpu_all_sample}
+        # CPU quantize (the oracle's restatement of src/quant.cpp:34-84), one thread
+        detail["cpu_quantize"] = cpu_quantize_rate()
         del m4, st
         torch.cuda.empty_cache()
 
@@ -426,6 +483,7 @@ def main():
         # config 1: int8 8960x1536, 1 row, rotated over 64 copies
         us, gbs = bench_gemv_single(torch, ops, 0, I15, H15, 1, copies=64)
         detail["cfg1_int8_8960x1536_m1"] = {"us": round(us, 2), "GBps": round(gbs, 1)}
+        detail["hbm_copy_2GiB_GBps"] = hbm_copy_rate(torch)
         # config 2: 1.5B int4 layer set x 28, 1 row
         m15 = Model(torch, ops, 1, H15, I15, 12 * 128, 2 * 128, L15, seed=15)
         s15 = Step(torch, ops, m15, 1)
