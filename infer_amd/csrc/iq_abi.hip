@@ -216,7 +216,10 @@ int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, i
     if (!x || !y) return IQ_ENULL;
     if (T < 1) return IQ_ESHAPE;
     if ((T + 127) / 128 * ((out + 127) / 128) > 0x7fffffff) return IQ_ETOOLARGE;
-    return from_hip(iq::launch_gemm(x, nullptr, to_qview(W), bias, T, y, static_cast<hipStream_t>(stream)));
+    iq::Workspace* ws = nullptr;
+    const hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(iq::launch_gemm(x, nullptr, to_qview(W), bias, T, y, ws->partials, static_cast<hipStream_t>(stream)));
 }
 
 int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int64_t T,
@@ -226,7 +229,10 @@ int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int
     if (!x || !y) return IQ_ENULL;
     if (T < 1) return IQ_ESHAPE;
     if ((T + 127) / 128 * ((out + 127) / 128) > 0x7fffffff) return IQ_ETOOLARGE;
-    return from_hip(iq::launch_gemm(nullptr, x, to_qview(W), bias, T, y, static_cast<hipStream_t>(stream)));
+    iq::Workspace* ws = nullptr;
+    const hipError_t e = iq::get_workspace(&ws);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(iq::launch_gemm(nullptr, x, to_qview(W), bias, T, y, ws->partials, static_cast<hipStream_t>(stream)));
 }
 
 int iq_linear(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,

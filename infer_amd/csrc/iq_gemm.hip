@@ -39,6 +39,9 @@ struct GemmParams {
     float* y;
     int64_t T, N, K, G;
     int tiles_m, tiles_n;
+    int splits;      // K ranges (workgroups per output tile); > 1: range sums go to part
+    int64_t kchunk;  // columns per K range (a multiple of 128)
+    float* part;     // [splits][T][N] fp32
 };
 
 __device__ __forceinline__ uint32_t bf16_pair_from_f32(float a, float b) {
@@ -65,14 +68,21 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
     // contiguous run of tiles (a bijection on [0, ntiles)).
     const int ntiles = p.tiles_m * p.tiles_n;
-    const int b = blockIdx.x;
+    const int split = int(blockIdx.x) / ntiles;  // K range of this workgroup
+    const int b = int(blockIdx.x) - split * ntiles;
     const int xcd = b % 8, base = ntiles / 8, extra = ntiles % 8;
     const int t = xcd * base + (xcd < extra ? xcd : extra) + b / 8;
     const int tm = t % p.tiles_m, tn = t / p.tiles_m;
     const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
 
     const int64_t row_bytes = KIND == 1 ? p.K / 2 : p.K;
-    const int nk = int((p.K + BK - 1) / BK);
+    // K range [kbeg, kbeg + klen): the sources below are based at kbeg, so
+    // the loop runs over klen columns as over a whole row
+    const int64_t kbeg = int64_t(split) * p.kchunk;
+    const int64_t klen = p.K - kbeg < p.kchunk ? p.K - kbeg : p.kchunk;
+    const int64_t gbeg = kbeg / kGroup, glen = (klen + kGroup - 1) / kGroup;
+    const int nk = int((klen + BK - 1) / BK);
+    const int64_t range_bytes = KIND == 1 ? (klen + 1) / 2 : klen;
 
     // ---- register staging of one K step
     constexpr int XCH = XF32 ? 8 : 4;           // 16-byte activation chunks per thread
@@ -96,9 +106,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         const int row = KIND == 1 ? c >> 1 : c >> 2;
         const int64_t n = n0 + row;
         wok[i] = row < BN && n < p.N;
-        wrow[i] = p.q + (wok[i] ? n : 0) * row_bytes;
+        wrow[i] = p.q + (wok[i] ? n : 0) * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg);
         wcol[i] = KIND == 1 ? (c & 1) * 16 : (c & 3) * 16;  // byte offset inside the step
-        if (KIND == 1) zrow = p.zeros + (wok[i] ? n : 0) * p.G;
+        if (KIND == 1) zrow = p.zeros + (wok[i] ? n : 0) * p.G + gbeg;
     }
     const void* xrow[XCH];
     bool xok[XCH];
@@ -109,8 +119,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         const int row = XF32 ? c >> 4 : c >> 3;
         const int64_t m = m0 + row;
         xok[i] = m < p.T;
-        xrow[i] = XF32 ? static_cast<const void*>(p.xf + (xok[i] ? m : 0) * p.K)
-                       : static_cast<const void*>(p.xb + (xok[i] ? m : 0) * p.K);
+        xrow[i] = XF32 ? static_cast<const void*>(p.xf + (xok[i] ? m : 0) * p.K + kbeg)
+                       : static_cast<const void*>(p.xb + (xok[i] ? m : 0) * p.K + kbeg);
         xcol[i] = XF32 ? (c & 15) * 4 : (c & 7) * 8;  // element offset inside the step
     }
 
@@ -130,14 +140,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
                 const float* xp = static_cast<const float*>(xrow[i]);
                 float f[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) f[e] = (xok[i] && k + e < p.K) ? xp[k + e] : 0.0f;
+                for (int e = 0; e < 4; e++) f[e] = (xok[i] && k + e < klen) ? xp[k + e] : 0.0f;
                 xr[i] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
             } else {
                 const uint16_t* xp = static_cast<const uint16_t*>(xrow[i]);
                 uint32_t h[4] = {0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    if (xok[i] && k + e < p.K) h[e / 2] |= uint32_t(xp[k + e]) << (16 * (e & 1));
+                    if (xok[i] && k + e < klen) h[e / 2] |= uint32_t(xp[k + e]) << (16 * (e & 1));
                 xr[i] = make_uint4(h[0], h[1], h[2], h[3]);
             }
         }
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
                 uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 16; e++)
-                    if (off + e < row_bytes) w[e / 4] |= uint32_t(wrow[i][off + e]) << (8 * (e % 4));
+                    if (off + e < range_bytes) w[e / 4] |= uint32_t(wrow[i][off + e]) << (8 * (e % 4));
                 wr[i] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
@@ -248,7 +258,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     // second step).
     auto load_scales = [&](int64_t g, float (&s)[NJ]) {
 #pragma unroll
-        for (int j = 0; j < NJ; j++) s[j] = (nval[j] && g < p.G) ? bf16_to_f32(p.scales[ncol[j] * p.G + g]) : 0.0f;
+        for (int j = 0; j < NJ; j++)
+            s[j] = (nval[j] && g < glen) ? bf16_to_f32(p.scales[ncol[j] * p.G + gbeg + g]) : 0.0f;
     };
     float s_cur[NJ], s_nxt[NJ];
     load_scales(0, s_cur);
@@ -315,24 +326,54 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         if (!nval[j]) continue;
-        const float bv = p.bias ? bf16_to_f32(p.bias[ncol[j]]) : 0.0f;
+        const float bv = p.bias && p.splits == 1 ? bf16_to_f32(p.bias[ncol[j]]) : 0.0f;
+        float* dst = p.splits == 1 ? p.y : p.part + int64_t(split) * p.T * p.N;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-                if (m < p.T) p.y[m * p.N + ncol[j]] = acc[i][j][r] + bv;
+                if (m < p.T) dst[m * p.N + ncol[j]] = acc[i][j][r] + bv;
             }
     }
 }
 
+// y[t, n] = sum over K ranges s of part[s][t][n] (in range order) + bias[n].
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ part, int S, int64_t T,
+                                                          int64_t N, const uint16_t* __restrict__ bias,
+                                                          float* __restrict__ y) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= T * N) return;
+    float sum = 0.0f;
+    for (int s = 0; s < S; s++) sum += part[int64_t(s) * T * N + i];
+    y[i] = sum + (bias ? bf16_to_f32(bias[i % N]) : 0.0f);
+}
+
 template <int KIND, bool XF32, int NJ>
 void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
-    const unsigned grid = unsigned(p.tiles_m * p.tiles_n);
+    const unsigned grid = unsigned(p.tiles_m * p.tiles_n * p.splits);
     if (fastw && fastx) gemm_kernel<KIND, XF32, true, true, NJ><<<grid, kThreads, 0, stream>>>(p);
     else if (fastw) gemm_kernel<KIND, XF32, true, false, NJ><<<grid, kThreads, 0, stream>>>(p);
     else if (fastx) gemm_kernel<KIND, XF32, false, true, NJ><<<grid, kThreads, 0, stream>>>(p);
     else gemm_kernel<KIND, XF32, false, false, NJ><<<grid, kThreads, 0, stream>>>(p);
+}
+
+// Few output tiles (short T): split K into ranges of whole 128-column groups
+// so that the CUs have two workgroups each, the range sums added by
+// gemm_reduce_kernel; needs the fast (aligned) paths and room for the sums.
+void plan_splits(GemmParams& p, bool fast, int64_t part_floats) {
+    p.splits = 1;
+    p.kchunk = p.K;
+    const int tiles = p.tiles_m * p.tiles_n, want = 2 * device_cu_count();
+    if (!fast || !p.part || tiles >= want) return;
+    int S = (want + tiles - 1) / tiles;
+    S = S > 16 ? 16 : S;
+    while (S > 1 && int64_t(S) * p.T * p.N > part_floats) S--;
+    const int64_t G = p.K / kGroup;
+    if (S < 2 || G < 2) return;
+    const int64_t gch = (G + S - 1) / S;
+    p.kchunk = gch * kGroup;
+    p.splits = int((G + gch - 1) / gch);
 }
 
 template <int KIND, bool XF32>
@@ -341,18 +382,25 @@ void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
     const int t128 = p.tiles_m * int((p.N + 127) / 128);
     if (t128 >= 2 * device_cu_count()) {
         p.tiles_n = int((p.N + 127) / 128);
+        plan_splits(p, fastw && fastx, kPartialFloats);
         launch_gemm_t<KIND, XF32, 2>(p, fastw, fastx, stream);
     } else {
         p.tiles_n = int((p.N + 63) / 64);
+        plan_splits(p, fastw && fastx, kPartialFloats);
         launch_gemm_t<KIND, XF32, 1>(p, fastw, fastx, stream);
+    }
+    if (p.splits > 1) {
+        const int64_t n = p.T * p.N;
+        gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
     }
 }
 
 }  // namespace
 
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
-                       const uint16_t* bias, int64_t T, float* y, hipStream_t stream) {
+                       const uint16_t* bias, int64_t T, float* y, float* part, hipStream_t stream) {
     GemmParams p;
+    p.part = part;
     p.xf = x_f32; p.xb = x_bf16;
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
     p.T = T; p.N = W.rows; p.K = W.cols; p.G = W.groups;

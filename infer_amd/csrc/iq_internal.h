@@ -63,8 +63,9 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
 // shapes prepare x once into the workspace, then one launch per matrix.
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream);
+// part: the workspace's split-K partials (short T splits K over workgroups).
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
-                       const uint16_t* bias, int64_t T, float* y, hipStream_t stream);
+                       const uint16_t* bias, int64_t T, float* y, float* part, hipStream_t stream);
 
 // Device properties used by the dispatch heuristics.
 int device_cu_count();
