@@ -5,7 +5,9 @@
 //
 // Tiling: a 256-thread workgroup (4 waves, 2x2) owns a 128 (activation rows)
 // x 128 (output features) tile; each wave a 64x64 block = 2x2 MFMA
-// f32_32x32x16_bf16 tiles.  K advances 64 columns per step through
+// f32_32x32x16_bf16 tiles (64-row and 64-column variants for short T and
+// narrow matrices; K split over workgroups when the tiles would leave CUs
+// idle, the range sums added by a reduction).  K advances 64 columns per step through
 // double-buffered LDS: the next step's activation and weight bytes are
 // loaded into registers while the current step's MFMAs run, then written to
 // the other buffer -- the weights dequantised on the way in (int8 code, or
@@ -25,7 +27,7 @@ namespace iq {
 
 namespace {
 
-constexpr int BM = 128, BK = 64, LDSW = BK + 8;  // LDS row pitch (bf16)
+constexpr int BK = 64, LDSW = BK + 8;  // LDS row pitch (bf16)
 constexpr int kThreads = 256;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -55,9 +57,11 @@ __device__ __forceinline__ uint32_t bf16_pair_int(int a, int b) {
 
 // NJ: 32-column MFMA tiles per wave along the output features (tile width
 // BN = 64 NJ): 2 for wide matrices, 1 when 128-wide tiles would leave CUs idle.
-template <int KIND, bool XF32, bool FASTW, bool FASTX, int NJ>
+// BM: activation rows per tile, 128, or 64 for short T (each wave 32 rows).
+template <int KIND, bool XF32, bool FASTW, bool FASTX, int NJ, int BM>
 __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     constexpr int BN = 64 * NJ;
+    constexpr int NI = BM / 64;  // 32-row MFMA tiles per wave along the rows
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t Al[XF32 ? 2 : 1][XF32 ? BM : 1][LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][LDSW];
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     const int64_t range_bytes = KIND == 1 ? (klen + 1) / 2 : klen;
 
     // ---- register staging of one K step
-    constexpr int XCH = XF32 ? 8 : 4;           // 16-byte activation chunks per thread
+    constexpr int XCH = XF32 ? BM / 16 : BM / 32;  // 16-byte activation chunks per thread
     constexpr int WCH = KIND == 1 ? 1 : NJ;     // 16-byte weight chunks per thread
     struct Regs {
         uint4 xr[XCH];
@@ -236,9 +240,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         }
     };
 
-    float16_t acc[2][NJ], P[2][NJ];
+    float16_t acc[NI][NJ], P[NI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < NI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++)
 #pragma unroll
@@ -281,11 +285,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
             const int kof = ks * 16 + 8 * (lane >> 5);
-            bf16x8_t a[2], al[2], bw[NJ];
+            bf16x8_t a[NI], al[NI], bw[NJ];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * 64 + i * 32 + (lane & 31)][kof]);
-                if (XF32) al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[XF32 ? buf : 0][XF32 ? wm * 64 + i * 32 + (lane & 31) : 0][kof]);
+            for (int i = 0; i < NI; i++) {
+                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * (BM / 2) + i * 32 + (lane & 31)][kof]);
+                if (XF32) al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[XF32 ? buf : 0][XF32 ? wm * (BM / 2) + i * 32 + (lane & 31) : 0][kof]);
             }
 #pragma unroll
             for (int j = 0; j < NJ; j++)
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
             // the group's first k slice starts its partial sums from zero
             const bool first = PAR == 0 && ks == 0;
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < NI; i++)
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
                     P[i][j] = mfma32_bf16(a[i], bw[j], first ? float16_t{} : P[i][j]);
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < NI; i++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) acc[i][j][r] = __builtin_fmaf(s_cur[j], P[i][j][r], acc[i][j][r]);
                 s_cur[j] = s_nxt[j];
@@ -329,10 +333,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         const float bv = p.bias && p.splits == 1 ? bf16_to_f32(p.bias[ncol[j]]) : 0.0f;
         float* dst = p.splits == 1 ? p.y : p.part + int64_t(split) * p.T * p.N;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < NI; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
                 if (m < p.T) dst[m * p.N + ncol[j]] = acc[i][j][r] + bv;
             }
     }
@@ -350,12 +354,13 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
 }
 
 template <int KIND, bool XF32, int NJ>
-void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
+void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t stream) {
     const unsigned grid = unsigned(p.tiles_m * p.tiles_n * p.splits);
-    if (fastw && fastx) gemm_kernel<KIND, XF32, true, true, NJ><<<grid, kThreads, 0, stream>>>(p);
-    else if (fastw) gemm_kernel<KIND, XF32, true, false, NJ><<<grid, kThreads, 0, stream>>>(p);
-    else if (fastx) gemm_kernel<KIND, XF32, false, true, NJ><<<grid, kThreads, 0, stream>>>(p);
-    else gemm_kernel<KIND, XF32, false, false, NJ><<<grid, kThreads, 0, stream>>>(p);
+    if (bm == 64) gemm_kernel<KIND, XF32, true, true, NJ, 64><<<grid, kThreads, 0, stream>>>(p);  // (fast paths only)
+    else if (fastw && fastx) gemm_kernel<KIND, XF32, true, true, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
+    else if (fastw) gemm_kernel<KIND, XF32, true, false, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
+    else if (fastx) gemm_kernel<KIND, XF32, false, true, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
+    else gemm_kernel<KIND, XF32, false, false, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
 }
 
 // Few output tiles (short T): split K into ranges of whole 128-column groups
@@ -377,17 +382,17 @@ void plan_splits(GemmParams& p, bool fast, int64_t part_floats) {
 }
 
 template <int KIND, bool XF32>
-void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, hipStream_t stream) {
+void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t stream) {
     // 128-wide tiles unless they leave CUs without two workgroups to run
     const int t128 = p.tiles_m * int((p.N + 127) / 128);
     if (t128 >= 2 * device_cu_count()) {
         p.tiles_n = int((p.N + 127) / 128);
         plan_splits(p, fastw && fastx, kPartialFloats);
-        launch_gemm_t<KIND, XF32, 2>(p, fastw, fastx, stream);
+        launch_gemm_t<KIND, XF32, 2>(p, fastw, fastx, bm, stream);
     } else {
         p.tiles_n = int((p.N + 63) / 64);
         plan_splits(p, fastw && fastx, kPartialFloats);
-        launch_gemm_t<KIND, XF32, 1>(p, fastw, fastx, stream);
+        launch_gemm_t<KIND, XF32, 1>(p, fastw, fastx, bm, stream);
     }
     if (p.splits > 1) {
         const int64_t n = p.T * p.N;
@@ -404,16 +409,23 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
     p.xf = x_f32; p.xb = x_bf16;
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
     p.T = T; p.N = W.rows; p.K = W.cols; p.G = W.groups;
-    p.tiles_m = int((T + BM - 1) / BM);
     const bool fastw = (p.K % kGroup == 0);
     const uintptr_t xa = x_f32 ? reinterpret_cast<uintptr_t>(x_f32) : reinterpret_cast<uintptr_t>(x_bf16);
     const bool fastx = (p.K % BK == 0) && (xa % 16 == 0);
+    // 64-row tiles for short T (less MFMA work on padding rows, more tiles):
+    // 7B int8, fp32 activations, gate 18944 x 3584 at T = 33 / 64 / 128 /
+    // 256: 115 / 113 / 137 / 202 -> 55 / 58 / 97 / 139 us; down 3584 x
+    // 18944 at T = 64 / 256: 115 / 186 -> 58 / 170 us, but at T = 128 (a
+    // narrow matrix, already split over K) 93 -> 103: kept at 128 rows there
+    const bool short_t = T <= 64 || (T > 128 && T <= 256) || (T <= 128 && W.rows >= 8192);
+    const int bm = (short_t && fastw && fastx) ? 64 : 128;
+    p.tiles_m = int((T + bm - 1) / bm);
     if (x_f32) {
-        if (W.kind == 1) launch_gemm_nj<1, true>(p, fastw, fastx, stream);
-        else launch_gemm_nj<0, true>(p, fastw, fastx, stream);
+        if (W.kind == 1) launch_gemm_nj<1, true>(p, fastw, fastx, bm, stream);
+        else launch_gemm_nj<0, true>(p, fastw, fastx, bm, stream);
     } else {
-        if (W.kind == 1) launch_gemm_nj<1, false>(p, fastw, fastx, stream);
-        else launch_gemm_nj<0, false>(p, fastw, fastx, stream);
+        if (W.kind == 1) launch_gemm_nj<1, false>(p, fastw, fastx, bm, stream);
+        else launch_gemm_nj<0, false>(p, fastw, fastx, bm, stream);
     }
     return hipGetLastError();
 }

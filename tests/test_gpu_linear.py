@@ -96,7 +96,8 @@ def test_gemm_fp32(kind, T):
 @pytest.mark.parametrize("kind", [0, 1])
 def test_gemm_bf16x(kind):
     rng = np.random.default_rng(9)
-    for T, N, K in ((1024, 512, 3584), (200, 384, 18944), (37, 130, 130)):
+    # (48, 700, 3584): 64-row tiles with K split over workgroups
+    for T, N, K in ((1024, 512, 3584), (200, 384, 18944), (37, 130, 130), (48, 700, 3584)):
         W = QFix(rng, N, K, kind, sd=0.02)
         xb = O.seeded_bf16(rng, (T, K), 1.0)
         x = O.bf16_to_f32(xb)
