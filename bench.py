@@ -480,6 +480,15 @@ def main():
             ms, tf = bench_gemm(torch, ops, 0, 1024, N, K, fp32x=True)
             detail[f"prefill_int8_{nm}_1024_fp32x"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
                                                        "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        # the reference's prefill chunks (32 < T <= 256), fp32 activations
+        # (launch_gemm_tiled_q), int8: us and weight GB/s
+        chunk = {}
+        for T in (64, 256):
+            for (N, K, nm) in ((I7, H7, "gate"), (H7, I7, "down")):
+                ms, tf = bench_gemm(torch, ops, 0, T, N, K, fp32x=True)
+                chunk[f"T{T}_{nm}"] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1),
+                                       "weights_GBps": round(N * K / (ms * 1e-3) / 1e9, 1)}
+        detail["prefill_chunks_int8_fp32x"] = chunk
         # config 1: int8 8960x1536, 1 row, rotated over 64 copies
         us, gbs = bench_gemv_single(torch, ops, 0, I15, H15, 1, copies=64)
         detail["cfg1_int8_8960x1536_m1"] = {"us": round(us, 2), "GBps": round(gbs, 1)}
