@@ -395,6 +395,17 @@ def main():
     step_bytes = st.bytes
     value = step_bytes / (ms_wall * 1e-3) / 1e9
     log(f"int4 M=1: {ms_wall * 1e3:.1f} us/step wall, {ms_ev * 1e3:.1f} us events, {value:.0f} GB/s")
+    # per-replay spread (after the timed region): 50 replays, each between
+    # its own pair of events
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(50)]
+    for a, b in evs:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    step_stats = {"replays": len(per), "median_us": round(per[len(per) // 2], 1), "min_us": round(per[0], 1),
+                  "max_us": round(per[-1], 1)}
 
     # roofline of the dominant kernel (int4 GEMV, 1 row)
     rb, rms, rn = kernel_roofline(torch, st, only_kind=1)
@@ -413,7 +424,7 @@ def main():
                 "algorithmic_bytes_per_launch": int(rb / max(rn, 1))}
     del g
 
-    detail = {}
+    detail = {"7b_int4_m1_step_spread": step_stats}
     cpu = None
     if not args.quick:
         st16 = Step(torch, ops, m4, 16)
