@@ -1047,12 +1047,7 @@ void launch_gemvb_t(const GemvParams& p, bool vec, unsigned grid, size_t lds, hi
 #undef IQ_GB
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
-
-// MODE of the 1-row kernel (see load_slice); 16-byte paths also need a
+// MODE of the 1-row kernel (see load_meta / load_weights); 16-byte paths also need a
 // 16-byte aligned activation row.
 int gemv1_mode(int64_t K, int64_t G, const float* x) {
     if (K % kGroup || reinterpret_cast<uintptr_t>(x) % 16) return 0;
@@ -1245,7 +1240,7 @@ hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, floa
     p.bias = bias; p.y = y; p.part = ws->partials;
     p.M = M;
     const int gc = (kind == 1 && M <= 16) ? 8 : 4;  // groups per chunk (LDS: 2 * gc * M * 384 B max)
-    static const int target = env_int("IQ_GEMV_WAVES", 2048);
+    constexpr int target = 2048;  // waves per 256 CUs the slices aim for
     p.nrb = int((N + 127) / 128);
     const int64_t want_s = (int64_t(target) * device_cu_count() / 256 + int64_t(p.nrb) * 8 - 1) / (int64_t(p.nrb) * 8);
     int S = int(want_s < 1 ? 1 : want_s);
