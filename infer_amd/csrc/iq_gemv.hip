@@ -1746,12 +1746,11 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
-    if (M > 16 && W[0].rows * K <= (int64_t(16) << 20)) {
-        // 17..32 rows on small matrices: the prefill GEMM's 64-row tiles
-        // beat two 16-row GEMV blocks (1.5B gate 8960 x 1536 at 24 / 32
-        // rows: 23.1 / 23.0 -> 17.6 / 18.5 us int8, 21.6 -> 19.5 / 20.5
-        // int4; down 1536 x 8960: 28 -> 18 / 21 us); on 7B shapes the GEMV
-        // blocks are as fast or faster
+    if (M > 16) {
+        // 17..32 rows: the prefill GEMM's 64-row tiles beat two 16-row GEMV
+        // blocks (1.5B gate 8960 x 1536 at 32 rows: 23.0 -> 16.2 us int8;
+        // 7B down 3584 x 18944 at 24 / 32 rows: 50.1 / 54.0 -> 37.4 / 38.4
+        // us int8, gate 18944 x 3584 int4: 47.5 / 53.0 -> 44.7 / 46.7)
         for (int i = 0; i < n; i++) {
             const hipError_t e = launch_gemm(x, nullptr, W[i], bias[i], M, y[i], ws->partials, stream);
             if (e != hipSuccess) return e;
