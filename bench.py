@@ -370,7 +370,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the quantized-weight path is single-GPU here, see DESIGN.md for how it would shard.",
+              "the quantized-weight path runs on one GPU here (output rows would split across GPUs).",
               file=sys.stderr)
         sys.exit(2)
 
