@@ -20,8 +20,10 @@
  * synchronising.  Return value: 0 on success, a negative IQ_E* code when the
  * arguments are rejected on the host (nothing was enqueued), or a positive
  * hipError_t when the HIP runtime reported an error.  No exception crosses
- * this boundary.  Calls that share a device share one workspace: calls on
- * different streams of one device must not overlap in time.
+ * this boundary.  The library keeps one workspace (activation operands,
+ * split-K partial sums; about 35 MB) per (device, stream) pair, allocated on
+ * the first call that needs it: calls on different streams may overlap, and
+ * calls on one stream are ordered by the stream.
  */
 #ifndef IQ_H
 #define IQ_H
@@ -74,9 +76,11 @@ int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64
  * terms (or as three signed byte limbs of rint(x * 2^k)), in the column
  * order that `kind`'s weight unpacking produces;
  * iq_gemv_prepped then runs the GEMV of any matrix of that kind and width on
- * the prepared block.  A prepared block stays valid until the next
- * iq_gemv / iq_gemv_prep on the device (stream order).  iq_gemv_prepped
- * returns IQ_ESHAPE when (B, in, kind) differ from the last preparation.
+ * the prepared block.  A prepared block belongs to the stream it was made
+ * on and stays valid until the next iq_gemv_prep on that stream, or until
+ * an iq_gemv / iq_gemv_multi / iq_linear on that stream reuses its buffers.
+ * iq_gemv_prepped returns IQ_ESHAPE when there is no valid preparation or
+ * (B, in, kind) differ from it.
  * No reference counterpart: the reference's launcher re-reads x per matrix. */
 int iq_gemv_prep(const float* x, int B, int64_t in, int kind, void* stream);
 int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
@@ -131,9 +135,16 @@ int iq_embedding(const iq_view* table, const int64_t* ids, int64_t T, int64_t H,
 int iq_quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, int kind, uint8_t* q,
                 uint16_t* scales, uint8_t* zeros, void* stream);
 
-/* Reserve the per-device workspace (done lazily by the first call that needs
- * it).  Call before capturing a graph.  Returns 0 or an error code. */
+/* Reserve the workspace of (device, null stream) (done lazily by the first
+ * call that needs it).  Call before capturing a graph.  Returns 0 or an
+ * error code. */
 int iq_init(int device);
+
+/* Reserve the workspace of (device, stream): call before capturing a graph
+ * on a stream other than the null stream, since capture forbids the
+ * allocation.  Library set-up, no reference counterpart (the reference's
+ * launchers keep no workspace). */
+int iq_init_stream(int device, void* stream);
 
 /* Static description of an error code (never NULL). */
 const char* iq_error_string(int code);

@@ -5,7 +5,9 @@
 // (src/quant.cpp:35-36 kind / odd int4 cols; src/quant.cpp:204-205 shape
 // mismatch) and adds the checks a C boundary needs (null pointers, sizes the
 // kernels assume).  Nothing is enqueued when a check fails.
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "../../include/iq.h"
 #include "iq_internal.h"
@@ -16,12 +18,15 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
-Workspace g_ws[kMaxDevices];
+// One workspace per (device, stream); entries live until the process ends
+// (a stream handle that is destroyed and reused maps to the same buffers,
+// which is safe because work on a destroyed stream has completed).
+std::map<std::pair<int, hipStream_t>, Workspace*> g_ws;
 int g_cus[kMaxDevices];
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-hipError_t create_workspace(int dev, Workspace* ws) {
+hipError_t create_workspace(Workspace* ws) {
     const int64_t gmax = kMaxKp / kGroup;
     const size_t xf = align256(sizeof(float) * 4 * kMaxKp);  // up to 4 rows copied by a prep
     // limbs (3 B per value) or f16 hi + lo (4 B per value)
@@ -39,23 +44,29 @@ hipError_t create_workspace(int dev, Workspace* ws) {
     ws->xq = reinterpret_cast<int8_t*>(p + xf);
     ws->xmeta = reinterpret_cast<int4*>(p + xf + xq);
     ws->partials = reinterpret_cast<float*>(p + xf + xq + meta);
-    (void)dev;
     return hipSuccess;
 }
 
 }  // namespace
 
-hipError_t get_workspace(Workspace** out) {
+hipError_t get_workspace(hipStream_t stream, Workspace** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_mu);
-    if (!g_ws[dev].base) {
-        e = create_workspace(dev, &g_ws[dev]);
-        if (e != hipSuccess) return e;
+    Workspace*& ws = g_ws[std::make_pair(dev, stream)];
+    if (!ws) {
+        Workspace* w = new Workspace();
+        e = create_workspace(w);
+        if (e != hipSuccess) {
+            delete w;
+            g_ws.erase(std::make_pair(dev, stream));
+            return e;
+        }
+        ws = w;
     }
-    *out = &g_ws[dev];
+    *out = ws;
     return hipSuccess;
 }
 
@@ -75,6 +86,9 @@ int device_cu_count() {
 namespace {
 
 int from_hip(hipError_t e) { return e == hipSuccess ? IQ_OK : int(e); }
+
+// Status of a workspace request: allocation failure is IQ_ENOMEM.
+int ws_status(hipError_t e) { return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e); }
 
 // Shared view checks; `in`/`out` must match the matrix (quant.cpp:204-205).
 int check_view(const iq_view* W, int64_t in, int64_t out) {
@@ -105,7 +119,7 @@ iq::QView to_qview(const iq_view* W) {
 
 extern "C" {
 
-int iq_init(int device) {
+int iq_init_stream(int device, void* stream) {
     int cur = 0;
     hipError_t e = hipGetDevice(&cur);
     if (e != hipSuccess) return from_hip(e);
@@ -114,11 +128,13 @@ int iq_init(int device) {
         if (e != hipSuccess) return from_hip(e);
     }
     iq::Workspace* ws = nullptr;
-    e = iq::get_workspace(&ws);
+    e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
     (void)iq::device_cu_count();
     if (device != cur) (void)hipSetDevice(cur);
-    return from_hip(e);
+    return ws_status(e);
 }
+
+int iq_init(int device) { return iq_init_stream(device, nullptr); }
 
 int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
             float* y, void* stream) {
@@ -128,8 +144,8 @@ int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64
     if (B < 1 || B > iq::kMaxRowsGemv) return IQ_ESHAPE;
     if (W->groups * IQ_GROUP > iq::kMaxKp) return IQ_ETOOLARGE;
     iq::Workspace* ws = nullptr;
-    hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     return from_hip(iq::launch_gemv(x, to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
 }
 
@@ -140,8 +156,8 @@ int iq_gemv_prep(const float* x, int B, int64_t in, int kind, void* stream) {
     if (kind == IQ_INT4 && (in % 2)) return IQ_ESHAPE;
     if ((in + IQ_GROUP - 1) / IQ_GROUP * IQ_GROUP > iq::kMaxKp) return IQ_ETOOLARGE;
     iq::Workspace* ws = nullptr;
-    hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     return from_hip(iq::launch_xprep(x, B, in, kind, ws, static_cast<hipStream_t>(stream)));
 }
 
@@ -151,8 +167,8 @@ int iq_gemv_prepped(const iq_view* W, const uint16_t* bias, int B, int64_t in, i
     if (rc) return rc;
     if (!y) return IQ_ENULL;
     iq::Workspace* ws = nullptr;
-    hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     if (B != ws->prep_M || in != ws->prep_K || W->kind != ws->prep_kind) return IQ_ESHAPE;
     return from_hip(iq::launch_gemv_prepped(to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
 }
@@ -187,8 +203,8 @@ int iq_gemv_prepped_multi(const iq_view* const* Ws, int n, const uint16_t* const
     const int rc = gather_views(Ws, n, biases, in, ys, v, b, y);
     if (rc) return rc;
     iq::Workspace* ws = nullptr;
-    hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     if (B != ws->prep_M || in != ws->prep_K || Ws[0]->kind != ws->prep_kind) return IQ_ESHAPE;
     return from_hip(iq::launch_gemv_prepped_multi(v, b, y, n, B, ws, static_cast<hipStream_t>(stream)));
 }
@@ -204,8 +220,8 @@ int iq_gemv_multi(const float* x, const iq_view* const* Ws, int n, const uint16_
     if (B < 1 || B > iq::kMaxRowsGemv) return IQ_ESHAPE;
     if (Ws[0]->groups * IQ_GROUP > iq::kMaxKp) return IQ_ETOOLARGE;
     iq::Workspace* ws = nullptr;
-    hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return e == hipErrorOutOfMemory ? IQ_ENOMEM : from_hip(e);
+    hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     return from_hip(iq::launch_gemv_multi(x, v, b, y, n, B, ws, static_cast<hipStream_t>(stream)));
 }
 
@@ -217,8 +233,8 @@ int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, i
     if (T < 1) return IQ_ESHAPE;
     if ((T + 127) / 128 * ((out + 127) / 128) > 0x7fffffff) return IQ_ETOOLARGE;
     iq::Workspace* ws = nullptr;
-    const hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return from_hip(e);
+    const hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     return from_hip(iq::launch_gemm(x, nullptr, to_qview(W), bias, T, y, ws->partials, static_cast<hipStream_t>(stream)));
 }
 
@@ -230,8 +246,8 @@ int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int
     if (T < 1) return IQ_ESHAPE;
     if ((T + 127) / 128 * ((out + 127) / 128) > 0x7fffffff) return IQ_ETOOLARGE;
     iq::Workspace* ws = nullptr;
-    const hipError_t e = iq::get_workspace(&ws);
-    if (e != hipSuccess) return from_hip(e);
+    const hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return ws_status(e);
     return from_hip(iq::launch_gemm(nullptr, x, to_qview(W), bias, T, y, ws->partials, static_cast<hipStream_t>(stream)));
 }
 

@@ -34,12 +34,14 @@
 //    cross-workgroup traffic).  A wave requests all weight words, scales and
 //    zero points of a batch of groups before it waits, stages the batch's
 //    activation limbs in its own LDS slot and runs the MFMAs.
-//  * gemv (2..32 rows): workgroup = 4 waves x R tiles of 16 rows on one slice
-//    of K; the slice's activation limbs are staged once per workgroup in
-//    LDS and shared by all 4R tiles.  Slices are split across workgroups
-//    when the matrix is too short to fill the GPU; the last workgroup of a
-//    row block adds the slice partials in slice order (deterministic) and
-//    resets its counter, so no clearing is needed between launches.
+//  * gemvt / gemvb (2..16 rows): a workgroup stages the activation limbs of
+//    one K range in LDS once and shares them over many 16-row tiles.  When a
+//    matrix is too short to fill the GPU, K is split into ranges over
+//    several workgroups; each writes fp32 partial sums to the workspace and
+//    a separate reduce launch (gemvt_reduce_kernel / gemv_reduce_kernel)
+//    adds them in range order, so the result is deterministic and no
+//    counter has to be cleared between launches.
+//  * gemvh (2..32 rows, f16 split activations): see gemvh_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -1765,17 +1767,14 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         const G1Plan pl = gemv1_plan(G, W[0].kind, mode, total_tiles(W, n), device_cu_count(), gemv1_rows(M));
         if (pl.ng > 0) return launch_gemv1(x, W, bias, y, n, pl, mode, stream, M, ws->partials);
     }
-    ws->prep_copy = false;
-    ws->prep_M = M;
-    ws->prep_K = K;
-    ws->prep_kind = W[0].kind;
+    // The conversion below overwrites xq / xmeta: a preparation held there
+    // (not a copy in xf) is gone, so iq_gemv_prepped must refuse to run on it.
+    if (!ws->prep_copy) ws->invalidate_prep();
     if (gemvh_preferred(K, M, total_tiles(W, n), W[0].kind)) {
-        ws->prep_h = true;
         const hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;
         return launch_gemvh(W, bias, y, n, M, ws, stream);
     }
-    ws->prep_h = false;
     hipError_t e = launch_xprep_limbs(x, M, K, W[0].kind, ws, stream);
     if (e != hipSuccess) return e;
     return launch_batched_multi(W, bias, y, n, M, ws, stream);

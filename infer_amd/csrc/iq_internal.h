@@ -36,14 +36,24 @@ struct Workspace {
     int prep_kind = -1;
     bool prep_copy = false;   // the preparation is a copy of x in xf (1..4 rows)
     bool prep_h = false;      // the preparation is the f16 hi/lo split for gemvh (xq, xmeta)
+    // Forget the preparation (its buffers were reused by a direct call).
+    void invalidate_prep() {
+        prep_M = 0;
+        prep_K = 0;
+        prep_kind = -1;
+        prep_copy = false;
+        prep_h = false;
+    }
 };
 
 constexpr int kMaxRowsGemv = 32;            // GpuBatch::kMaxRows (kernels/batch_gpu.h:80)
 constexpr int64_t kMaxKp = 131072;          // padded K limit of the GEMV
 constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K partials
 
-// Returns the workspace of the current device, allocating it on first use.
-hipError_t get_workspace(Workspace** ws);
+// Returns the workspace of (current device, stream), allocating it on first
+// use.  Every stream has its own, so calls on different streams never share
+// activation or partial-sum buffers; calls on one stream are ordered by it.
+hipError_t get_workspace(hipStream_t stream, Workspace** ws);
 
 hipError_t launch_quantize(const uint16_t* w, int64_t rows, int64_t cols, int kind, uint8_t* q,
                            uint16_t* scales, uint8_t* zeros, hipStream_t stream);

@@ -369,77 +369,122 @@ void QuantWriter::write(const std::string& path) const {
 }
 
 // ------------------------------------------------------------------ reader
+// A read-only file mapping; the QuantFile keeps it while its views live.
+namespace {
+
+struct Span {
+    const uint8_t* p = nullptr;
+    size_t n = 0;
+};
+
+// Maps `path` read-only; returns the mapping (nullptr for an empty file).
+Span map_readonly(const std::string& path) {
+    const int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0) throw std::runtime_error("llmq: " + path + ": cannot be opened");
+    struct stat st;
+    const bool sized = fstat(fd, &st) == 0;
+    void* m = nullptr;
+    if (sized && st.st_size > 0) m = mmap(nullptr, size_t(st.st_size), PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (!sized) throw std::runtime_error("llmq: " + path + ": cannot stat");
+    if (m == MAP_FAILED) throw std::runtime_error("llmq: " + path + ": cannot be mapped");
+    return Span{static_cast<const uint8_t*>(m), size_t(st.st_size)};
+}
+
+// The fixed preamble: 8 magic bytes, then the header length (u64 LE).
+constexpr size_t kPreamble = 16;
+
+uint64_t le64(const uint8_t* b) {
+    uint64_t v = 0;
+    for (int i = 7; i >= 0; i--) v = (v << 8) | b[i];
+    return v;
+}
+
+QKind kind_of_dtype(const std::string& d, const std::string& where) {
+    for (QKind k : {QKind::kInt8, QKind::kInt4, QKind::kBf16})
+        if (d == qkind_name(k)) return k;
+    throw std::runtime_error("llmq: " + where + ": dtype \"" + d + "\" is not int8, int4 or bf16");
+}
+
+}  // namespace
+
 QuantFile::~QuantFile() {
     if (map_) munmap(map_, map_size_);
 }
 
 void QuantFile::open(const std::string& path) {
-    if (map_) {
-        munmap(map_, map_size_);
-        map_ = nullptr;
-        tensors_.clear();
-        offset_.clear();
-        kind_ = QKind::kBf16;
-    }
-    const int fd = ::open(path.c_str(), O_RDONLY);
-    if (fd < 0) throw std::runtime_error("cannot open " + path);
-    struct stat st;
-    if (fstat(fd, &st) != 0) {
-        ::close(fd);
-        throw std::runtime_error("fstat " + path);
-    }
-    map_size_ = size_t(st.st_size);
-    map_ = map_size_ ? mmap(nullptr, map_size_, PROT_READ, MAP_PRIVATE, fd, 0) : nullptr;
-    ::close(fd);
-    if (map_ == MAP_FAILED) {
-        map_ = nullptr;
-        throw std::runtime_error("mmap " + path);
-    }
-    const auto* base = static_cast<const uint8_t*>(map_);
-    if (map_size_ < 16 || std::memcmp(base, "LLMQ0001", 8) != 0) throw std::runtime_error("not an .llmq file: " + path);
-    uint64_t hl = 0;
-    for (int i = 0; i < 8; i++) hl |= uint64_t(base[8 + i]) << (8 * i);
-    if (hl > map_size_ - 16) throw std::runtime_error("truncated header: " + path);
-    const JVal h = parse_json(reinterpret_cast<const char*>(base + 16), reinterpret_cast<const char*>(base + 16 + hl));
-    if (h.type != JVal::kObj) throw std::runtime_error("bad header in " + path);
-    const uint8_t* blob = base + 16 + hl;
-    const size_t blob_size = map_size_ - 16 - hl;
-    auto range = [&](const JVal& r, size_t need, size_t* begin) {
-        if (r.type != JVal::kArr || r.arr.size() != 2) throw std::runtime_error("bad range in " + path);
-        const int64_t b = r.arr[0].as_int(), e = r.arr[1].as_int();
-        if (b < 0 || e < b || size_t(e) > blob_size) throw std::runtime_error("bad range in " + path);
-        if (size_t(e - b) != need) throw std::runtime_error("range size mismatch in " + path);
-        if (begin) *begin = size_t(b);
-        return blob + b;
+    // Parse everything into locals first; the object changes only when the
+    // whole file is valid (a failed open leaves the previous file in place).
+    Span file = map_readonly(path);
+    struct Unmap {
+        Span* s;
+        ~Unmap() { if (s && s->p) munmap(const_cast<uint8_t*>(s->p), s->n); }
+    } guard{&file};
+    auto bad = [&](const std::string& why) { return std::runtime_error("llmq: " + path + ": " + why); };
+
+    if (file.n < kPreamble || std::memcmp(file.p, "LLMQ0001", 8) != 0) throw bad("missing LLMQ0001 magic");
+    const uint64_t header_len = le64(file.p + 8);
+    if (header_len > file.n - kPreamble) throw bad("header runs past the end of the file");
+    const char* hb = reinterpret_cast<const char*>(file.p + kPreamble);
+    const JVal header = parse_json(hb, hb + header_len);
+    if (header.type != JVal::kObj) throw bad("header is not a JSON object");
+    const Span blob{file.p + kPreamble + header_len, file.n - kPreamble - header_len};
+
+    // [begin, end) of one payload, checked against the blob and its expected size.
+    auto payload = [&](const JVal& r, size_t expect, const std::string& name) -> size_t {
+        if (r.type != JVal::kArr || r.arr.size() != 2) throw bad(name + ": a byte range must be [begin, end]");
+        const int64_t lo = r.arr[0].as_int(), hi = r.arr[1].as_int();
+        if (lo < 0 || hi < lo || uint64_t(hi) > blob.n) throw bad(name + ": byte range outside the data");
+        if (uint64_t(hi - lo) != expect) throw bad(name + ": byte range does not match the shape");
+        return size_t(lo);
     };
-    for (const auto& kv : h.obj) {
-        const JVal& j = kv.second;
+
+    std::map<std::string, QTensor> tensors;
+    std::map<std::string, size_t> first_byte;
+    QKind file_kind = QKind::kBf16;
+    for (const auto& entry : header.obj) {
+        const std::string& name = entry.first;
+        const JVal& e = entry.second;
         QTensor t;
-        const std::string& d = j.at("dtype").as_str();
-        t.kind = d == "int8" ? QKind::kInt8 : d == "int4" ? QKind::kInt4 : QKind::kBf16;
-        if (t.kind == QKind::kBf16 && d != "bf16") throw std::runtime_error("unknown dtype " + d + " in " + path);
-        const JVal& sh = j.at("shape");
-        if (sh.type != JVal::kArr) throw std::runtime_error("bad shape in " + path);
-        t.rows = sh.arr.size() >= 1 ? sh.arr[0].as_int() : 0;
-        t.cols = sh.arr.size() >= 2 ? sh.arr[1].as_int() : 1;
-        int64_t n = 1;
-        for (const JVal& x : sh.arr) n *= x.as_int();
-        size_t first = 0;
+        t.kind = kind_of_dtype(e.at("dtype").as_str(), name);
+        const JVal& shape = e.at("shape");
+        if (shape.type != JVal::kArr || shape.arr.empty()) throw bad(name + ": shape must be a non-empty array");
+        int64_t count = 1;
+        for (const JVal& d : shape.arr) count *= d.as_int();
+        t.rows = shape.arr[0].as_int();
+        t.cols = shape.arr.size() > 1 ? shape.arr[1].as_int() : 1;
         if (t.kind == QKind::kBf16) {
-            t.bf16 = reinterpret_cast<const uint16_t*>(range(j.at("data"), size_t(n) * 2, &first));
+            const size_t at = payload(e.at("data"), size_t(count) * 2, name);
+            t.bf16 = reinterpret_cast<const uint16_t*>(blob.p + at);
+            first_byte[name] = at;
         } else {
-            const JVal* g = j.find("group");
-            if (g && g->as_int() != kGroup) throw std::runtime_error("group size mismatch in " + path);
-            if (t.kind == QKind::kInt4 && t.cols % 2) throw std::runtime_error("odd int4 width in " + path);
-            t.q = range(j.at("data"), t.q_bytes(), &first);
-            t.scales = reinterpret_cast<const uint16_t*>(range(j.at("scales"), size_t(t.rows * t.groups()) * 2, nullptr));
-            if (const JVal* z = j.find("zeros")) t.zeros = range(*z, size_t(t.rows * t.groups()), nullptr);
-            if (t.kind == QKind::kInt4 && !t.zeros) throw std::runtime_error("int4 tensor without zeros in " + path);
-            kind_ = t.kind;
+            if (const JVal* g = e.find("group"); g && g->as_int() != kGroup)
+                throw bad(name + ": group size " + std::to_string(g->as_int()) + " (this build reads 128)");
+            if (t.kind == QKind::kInt4 && (t.cols & 1)) throw bad(name + ": int4 rows need an even width");
+            const size_t meta = size_t(t.rows) * size_t(t.groups());
+            const size_t qa = payload(e.at("data"), t.q_bytes(), name);
+            t.q = blob.p + qa;
+            t.scales = reinterpret_cast<const uint16_t*>(blob.p + payload(e.at("scales"), meta * 2, name));
+            const JVal* z = e.find("zeros");
+            if (t.kind == QKind::kInt4) {
+                if (!z) throw bad(name + ": int4 needs zero points");
+                t.zeros = blob.p + payload(*z, meta, name);
+            } else if (z) {
+                t.zeros = blob.p + payload(*z, meta, name);
+            }
+            first_byte[name] = qa;
+            file_kind = t.kind;
         }
-        tensors_[kv.first] = t;
-        offset_[kv.first] = first;
+        tensors.emplace(name, t);
     }
+
+    if (map_) munmap(map_, map_size_);
+    map_ = const_cast<uint8_t*>(file.p);
+    map_size_ = file.n;
+    guard.s = nullptr;  // ownership moves to the object
+    tensors_ = std::move(tensors);
+    offset_ = std::move(first_byte);
+    kind_ = file_kind;
 }
 
 const QTensor& QuantFile::get(const std::string& name) const {
@@ -464,33 +509,43 @@ std::vector<std::string> QuantFile::names_in_file() const {
 }
 
 // ------------------------------------------------------------------ config
+// The integer fields are required; the optional ones have the documented
+// Hugging Face defaults (head_dim = hidden / heads; attention_bias is true
+// for Qwen2, whose config class always uses q/k/v biases).
 ModelConfig ModelConfig::from_file(const std::string& path) {
     const std::string text = read_file(path);
     const JVal j = parse_json(text.data(), text.data() + text.size());
+    auto bad = [&](const std::string& why) { return std::runtime_error("config " + path + ": " + why); };
     ModelConfig c;
-    const JVal& archs = j.at("architectures");
-    if (archs.type != JVal::kArr || archs.arr.empty()) throw std::runtime_error("empty architectures in " + path);
-    c.architecture = archs.arr[0].as_str();
-    c.hidden_size = j.at("hidden_size").as_int();
-    c.num_hidden_layers = j.at("num_hidden_layers").as_int();
-    c.num_attention_heads = j.at("num_attention_heads").as_int();
-    c.num_key_value_heads = j.at("num_key_value_heads").as_int();
-    c.intermediate_size = j.at("intermediate_size").as_int();
-    c.vocab_size = j.at("vocab_size").as_int();
-    c.rope_theta = j.at("rope_theta").as_double();
+
+    static const std::pair<const char*, int64_t ModelConfig::*> kInts[] = {
+        {"hidden_size", &ModelConfig::hidden_size},
+        {"intermediate_size", &ModelConfig::intermediate_size},
+        {"num_attention_heads", &ModelConfig::num_attention_heads},
+        {"num_hidden_layers", &ModelConfig::num_hidden_layers},
+        {"num_key_value_heads", &ModelConfig::num_key_value_heads},
+        {"vocab_size", &ModelConfig::vocab_size},
+    };
+    for (const auto& f : kInts) c.*(f.second) = j.at(f.first).as_int();
     c.rms_norm_eps = j.at("rms_norm_eps").as_double();
+    c.rope_theta = j.at("rope_theta").as_double();
+
+    const JVal& archs = j.at("architectures");
+    if (archs.type != JVal::kArr || archs.arr.empty()) throw bad("\"architectures\" names no class");
+    c.architecture = archs.arr.front().as_str();
+
+    if (c.num_attention_heads <= 0 || c.num_key_value_heads <= 0) throw bad("head counts must be positive");
+    if (c.num_attention_heads % c.num_key_value_heads)
+        throw bad("query heads must be a multiple of the key/value heads");
+    const int64_t per_head = c.hidden_size / c.num_attention_heads;
+    const JVal* hd = j.find("head_dim");
+    c.head_dim = (hd && hd->type == JVal::kNum) ? hd->as_int() : per_head;
+    if (c.head_dim != per_head) throw bad("head_dim differs from hidden_size / num_attention_heads");
+
     const JVal* tie = j.find("tie_word_embeddings");
     c.tie_word_embeddings = tie && tie->type == JVal::kBool && tie->b;
-    if (c.num_attention_heads <= 0 || c.num_key_value_heads <= 0) throw std::runtime_error("bad head counts in " + path);
-    const int64_t derived = c.hidden_size / c.num_attention_heads;
-    const JVal* hd = j.find("head_dim");
-    c.head_dim = hd && hd->type == JVal::kNum ? hd->as_int() : derived;
-    if (c.head_dim != derived) throw std::runtime_error("head_dim inconsistent with hidden_size/num_heads");
     const JVal* ab = j.find("attention_bias");
-    if (ab && ab->type == JVal::kBool) c.attention_bias = ab->b;
-    else c.attention_bias = c.architecture == "Qwen2ForCausalLM";  // Qwen2 always has QKV bias
-    if (c.num_attention_heads % c.num_key_value_heads != 0)
-        throw std::runtime_error("num_heads not divisible by num_kv_heads (GQA requires it)");
+    c.attention_bias = (ab && ab->type == JVal::kBool) ? ab->b : c.architecture == "Qwen2ForCausalLM";
     return c;
 }
 
@@ -499,46 +554,66 @@ std::string QuantModel::file_for(const std::string& dir, QKind kind) {
     return dir + (kind == QKind::kInt4 ? "/model.q4.llmq" : "/model.q8.llmq");
 }
 
+namespace {
+
+// Sizes a tensor's rows / cols are checked against.
+enum Dim { kHidden, kQOut, kKvOut, kInter, kVocab, kOne };
+
+struct Want {
+    const char* suffix;           // tensor name after "model.layers.<i>."
+    QTensor QLayer::*field;
+    Dim rows, cols;               // cols == kOne: a bf16 vector
+    bool bias_only;               // present only with attention biases
+};
+
+// Every tensor a decoder layer reads, with the shape it must have.
+const Want kLayerTensors[] = {
+    {"self_attn.q_proj.weight", &QLayer::q_w, kQOut, kHidden, false},
+    {"self_attn.k_proj.weight", &QLayer::k_w, kKvOut, kHidden, false},
+    {"self_attn.v_proj.weight", &QLayer::v_w, kKvOut, kHidden, false},
+    {"self_attn.o_proj.weight", &QLayer::o_w, kHidden, kQOut, false},
+    {"mlp.gate_proj.weight", &QLayer::gate_w, kInter, kHidden, false},
+    {"mlp.up_proj.weight", &QLayer::up_w, kInter, kHidden, false},
+    {"mlp.down_proj.weight", &QLayer::down_w, kHidden, kInter, false},
+    {"input_layernorm.weight", &QLayer::input_ln, kHidden, kOne, false},
+    {"post_attention_layernorm.weight", &QLayer::post_attn_ln, kHidden, kOne, false},
+    {"self_attn.q_proj.bias", &QLayer::q_b, kQOut, kOne, true},
+    {"self_attn.k_proj.bias", &QLayer::k_b, kKvOut, kOne, true},
+    {"self_attn.v_proj.bias", &QLayer::v_b, kKvOut, kOne, true},
+};
+
+}  // namespace
+
 void QuantModel::load(const std::string& dir, QKind k) {
-    cfg = ModelConfig::from_file(dir + "/config.json");
-    kind = k;
+    const ModelConfig c = ModelConfig::from_file(dir + "/config.json");
+    const int64_t size[] = {c.hidden_size, c.num_attention_heads * c.head_dim, c.num_key_value_heads * c.head_dim,
+                            c.intermediate_size, c.vocab_size, 1};
     file_.open(file_for(dir, k));
-    auto mat = [&](const std::string& n, int64_t rows, int64_t cols) {
-        const QTensor& t = file_.get(n);
-        if (t.rows != rows || t.cols != cols || t.kind != k) throw std::runtime_error("shape/kind mismatch for " + n);
+    // One tensor of the file, checked: matrices must be of kind k, vectors bf16.
+    auto take = [&](const std::string& name, Dim rows, Dim cols) -> QTensor {
+        const QTensor& t = file_.get(name);
+        const bool vec = cols == kOne;
+        const QKind want = vec ? QKind::kBf16 : k;
+        if (t.kind != want)
+            throw std::runtime_error(name + ": stored as " + qkind_name(t.kind) + ", expected " + qkind_name(want));
+        if (t.rows != size[rows] || (!vec && t.cols != size[cols]))
+            throw std::runtime_error(name + ": stored shape " + std::to_string(t.rows) + "x" + std::to_string(t.cols) +
+                                     " does not match config.json");
         return t;
     };
-    auto vec = [&](const std::string& n, int64_t len) {
-        const QTensor& t = file_.get(n);
-        if (t.kind != QKind::kBf16 || t.rows != len) throw std::runtime_error("bad bf16 tensor " + n);
-        return t;
-    };
-    const int64_t H = cfg.hidden_size, q_out = cfg.num_attention_heads * cfg.head_dim,
-                  kv_out = cfg.num_key_value_heads * cfg.head_dim, I = cfg.intermediate_size;
-    embed_tokens = mat("model.embed_tokens.weight", cfg.vocab_size, H);
-    lm_head = QTensor{};
-    if (!cfg.tie_word_embeddings) lm_head = mat("lm_head.weight", cfg.vocab_size, H);
-    final_norm = vec("model.norm.weight", H);
-    layers.assign(size_t(cfg.num_hidden_layers), QLayer{});
-    for (int64_t i = 0; i < cfg.num_hidden_layers; i++) {
-        const std::string p = "model.layers." + std::to_string(i) + ".";
-        QLayer& L = layers[size_t(i)];
-        L.q_w = mat(p + "self_attn.q_proj.weight", q_out, H);
-        L.k_w = mat(p + "self_attn.k_proj.weight", kv_out, H);
-        L.v_w = mat(p + "self_attn.v_proj.weight", kv_out, H);
-        L.o_w = mat(p + "self_attn.o_proj.weight", H, q_out);
-        L.gate_w = mat(p + "mlp.gate_proj.weight", I, H);
-        L.up_w = mat(p + "mlp.up_proj.weight", I, H);
-        L.down_w = mat(p + "mlp.down_proj.weight", H, I);
-        L.input_ln = vec(p + "input_layernorm.weight", H);
-        L.post_attn_ln = vec(p + "post_attention_layernorm.weight", H);
-        L.has_bias = cfg.attention_bias;
-        if (L.has_bias) {
-            L.q_b = vec(p + "self_attn.q_proj.bias", q_out);
-            L.k_b = vec(p + "self_attn.k_proj.bias", kv_out);
-            L.v_b = vec(p + "self_attn.v_proj.bias", kv_out);
-        }
+    std::vector<QLayer> ls(size_t(c.num_hidden_layers));
+    for (size_t i = 0; i < ls.size(); i++) {
+        const std::string prefix = "model.layers." + std::to_string(i) + ".";
+        ls[i].has_bias = c.attention_bias;
+        for (const Want& w : kLayerTensors)
+            if (!w.bias_only || c.attention_bias) ls[i].*(w.field) = take(prefix + w.suffix, w.rows, w.cols);
     }
+    embed_tokens = take("model.embed_tokens.weight", kVocab, kHidden);
+    lm_head = c.tie_word_embeddings ? QTensor{} : take("lm_head.weight", kVocab, kHidden);
+    final_norm = take("model.norm.weight", kHidden, kOne);
+    layers = std::move(ls);
+    cfg = c;
+    kind = k;
 }
 
 // ------------------------------------------------------------------ device

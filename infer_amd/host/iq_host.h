@@ -33,20 +33,23 @@ constexpr int kGroup = IQ_GROUP;  // src/quant.h:34
 enum class QKind { kBf16, kInt8, kInt4 };  // src/quant.h:36
 const char* qkind_name(QKind k);
 
-// One quantised [rows x cols] matrix (or bf16 vector), as views into a
-// buffer or a mapped file (src/quant.h:40-49).
+// Non-owning view of one packed matrix or bf16 vector (src/quant.h:40-49).
+// Pointer sizes: codes q_bytes(); scales and (int4) zero points
+// rows x groups() entries each; bf16 holds rows x cols values when kind is
+// kBf16 (the layer norms and the attention biases) and is null otherwise.
 struct QTensor {
     QKind kind = QKind::kBf16;
     int64_t rows = 0, cols = 0;
-    const uint8_t* q = nullptr;        // int8: rows*cols bytes; int4: rows*cols/2
-    const uint16_t* scales = nullptr;  // bf16, rows * groups
-    const uint8_t* zeros = nullptr;    // int4 only, rows * groups
-    const uint16_t* bf16 = nullptr;    // kBf16 only (norms, biases)
+    const uint8_t* q = nullptr;
+    const uint16_t* scales = nullptr;
+    const uint8_t* zeros = nullptr;
+    const uint16_t* bf16 = nullptr;
     int64_t groups() const { return (cols + kGroup - 1) / kGroup; }
     size_t q_bytes() const { return kind == QKind::kInt4 ? size_t(rows) * cols / 2 : size_t(rows) * cols; }
 };
 
-// Owning quantised matrix (src/quant.h:52-58).
+// A packed matrix that owns its bytes, e.g. what quantize() returns
+// (src/quant.h:52-58).
 struct QMatrix {
     QKind kind = QKind::kInt8;
     int64_t rows = 0, cols = 0;
@@ -55,9 +58,12 @@ struct QMatrix {
     QTensor view() const;
 };
 
-// Quantise a bf16 [rows x cols] host matrix (src/quant.h:61), on the GPU.
+// Packs a host bf16 matrix [rows x cols] with the GPU quantiser; the bytes
+// equal the reference's CPU quantiser's (src/quant.h:61).  int4 requires an
+// even column count.
 QMatrix quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, QKind kind);
-// Dequantised value of one element (src/quant.h:63, src/quant.cpp:86-93).
+// s * q (int8) or s * (q - z) (int4) of element (r, c): the value every
+// kernel multiplies by (src/quant.h:63, src/quant.cpp:86-93).
 float dequant(const QTensor& t, int64_t r, int64_t c);
 
 // .llmq writer (src/quant.h:66-77): 8-byte magic "LLMQ0001", u64 header
@@ -83,8 +89,10 @@ private:
     std::vector<Entry> entries_;
 };
 
-// .llmq reader (src/quant.h:80-96): maps the file; views stay valid while
-// the QuantFile lives.
+// .llmq reader (src/quant.h:80-96).  open() maps the file read-only and
+// indexes its header; the QTensor views point into the mapping, so they are
+// valid until the next open() or the destructor.  A file that fails
+// validation throws and leaves the previously opened file in place.
 class QuantFile {
 public:
     QuantFile() = default;
@@ -94,9 +102,9 @@ public:
     void open(const std::string& path);
     bool has(const std::string& name) const { return tensors_.count(name) > 0; }
     const QTensor& get(const std::string& name) const;
-    std::vector<std::string> names() const;         // sorted
+    std::vector<std::string> names() const;          // sorted
     std::vector<std::string> names_in_file() const;  // in blob (write) order
-    QKind kind() const { return kind_; }
+    QKind kind() const { return kind_; }             // kind of the packed matrices
 
 private:
     void* map_ = nullptr;
@@ -116,21 +124,27 @@ struct ModelConfig {
     static ModelConfig from_file(const std::string& path);
 };
 
-// A model whose matrices come from a .llmq file (src/quant.h:99-115).
+// The views of one decoder layer.  Without attention biases the three bias
+// views stay empty (rows == 0).
 struct QLayer {
     QTensor q_w, k_w, v_w, o_w, gate_w, up_w, down_w;
-    QTensor q_b, k_b, v_b;  // kBf16; rows == 0 when absent
+    QTensor q_b, k_b, v_b;
     QTensor input_ln, post_attn_ln;
     bool has_bias = false;
 };
+// Every tensor of a quantised model, as views into its .llmq file, which the
+// model keeps open (src/quant.h:99-115).  With tied embeddings lm_head is
+// empty and embed_tokens doubles as the output projection.
 struct QuantModel {
     ModelConfig cfg;
-    QTensor embed_tokens;  // quantised [vocab x hidden]; the LM head when tied
-    QTensor lm_head;       // quantised, rows == 0 when tied
+    QTensor embed_tokens;
+    QTensor lm_head;
     QTensor final_norm;
     std::vector<QLayer> layers;
     QKind kind = QKind::kInt8;
-    // Loads <model_dir>/config.json + <model_dir>/model.<q8|q4>.llmq.
+    // Reads model_dir/config.json, then the int8 or int4 container that
+    // file_for() names, checking every tensor's kind and shape against the
+    // config.
     void load(const std::string& model_dir, QKind kind);
     static std::string file_for(const std::string& model_dir, QKind kind);
 

@@ -58,6 +58,7 @@ SIGNATURES = {
     "iq_embedding": ([_VP, _P, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_quantize": ([_P, _I64, _I64, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
     "iq_init": ([ctypes.c_int], ctypes.c_int),
+    "iq_init_stream": ([ctypes.c_int, _P], ctypes.c_int),
     "iq_error_string": ([ctypes.c_int], ctypes.c_char_p),
     "iq_version": ([], ctypes.c_char_p),
 }
@@ -262,5 +263,9 @@ def linear(x, W, bias=None, stream=None):
     return y
 
 
-def init(device=0):
-    _check(lib().iq_init(int(device)), "iq_init")
+def init(device=0, stream=None):
+    """Reserve the workspace of (device, stream) before a graph capture."""
+    if stream is None:
+        _check(lib().iq_init(int(device)), "iq_init")
+    else:
+        _check(lib().iq_init_stream(int(device), ctypes.c_void_p(stream.cuda_stream)), "iq_init_stream")

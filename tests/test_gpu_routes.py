@@ -1,0 +1,196 @@
+"""Parity of the kernel instances behind the benchmark's full-size numbers,
+through the C ABI, against the oracle's float64 product over dequant()
+(tests/test_ops_gpu.cu:664-692 semantics, same tolerances as
+tests/gpu_util.check_linear), plus the workspace contract.
+
+The matrices here are packed directly with random codes, scales and zero
+points (any bytes are a valid packed matrix, src/quant.h:40-58), so the
+full Qwen2.5-7B shapes need no host quantisation; outputs are checked on a
+seeded sample of output features, with every row of the activation block.
+
+Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
+  * prefill GEMM at T = 1024 on 18944 x 3584: 8 row tiles x 148 column
+    tiles >= 2 x CUs, i.e. the 128 x 128 tile instance (NJ = 2, BM = 128),
+    bf16 and fp32 activations, int8 and int4;
+  * gate|up (2 x 18944 x 3584) in one iq_gemv_multi call at 9, 12 and 16
+    rows (the staged-limb gemvt kernel) and at 1 row;
+  * the int8 lm_head 152064 x 3584 at 1 and 16 rows;
+  * every other 7B decode matrix at 16 rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+from infer_amd import ops
+from oracle import oracle as O
+from tests.gpu_util import CANARY, KGEMV_TOL, MAX_REL, out_buffer, say
+
+pytestmark = pytest.mark.gpu
+
+
+class Packed:
+    """A random packed [rows x cols] matrix (codes, bf16 scales, u8 zeros)
+    on the device, with its host copy for sampled dequantisation."""
+
+    def __init__(self, rng, rows, cols, kind):
+        G = O.groups(cols)
+        self.kind, self.rows, self.cols = kind, rows, cols
+        nq = rows * cols // 2 if kind == 1 else rows * cols
+        if kind == 1:
+            self.q = rng.integers(0, 256, nq, dtype=np.uint8)
+            self.z = rng.integers(0, 16, (rows, G), dtype=np.uint8)
+        else:
+            # int8 codes -127..127 (src/quant.cpp:56-57 never writes -128)
+            self.q = rng.integers(-127, 128, nq, dtype=np.int16).astype(np.int8).view(np.uint8)
+            self.z = None
+        self.s = O.f32_to_bf16(rng.uniform(2e-4, 8e-4, (rows, G)).astype(np.float32))
+        self.view = ops.upload_q(kind, rows, cols, self.q, self.s, self.z)
+
+    def dq_rows(self, idx):
+        """dequant() of output features idx (src/quant.cpp:86-93)."""
+        K = self.cols
+        rb = K // 2 if self.kind == 1 else K
+        q = self.q.reshape(self.rows, rb)[idx]
+        z = None if self.z is None else self.z[idx]
+        return O.dequant_matrix(q, self.s[idx], z, self.kind, len(idx), K)
+
+
+def sample_rows(rng, N, n=192):
+    """Sampled output features: both ends, a tile boundary and random ones."""
+    idx = set(rng.choice(N, size=min(n, N), replace=False).tolist())
+    idx.update([0, 1, 15, 16, N - 1, N - 17, N - 16])
+    return np.array(sorted(i for i in idx if 0 <= i < N), np.int64)
+
+
+def check_sampled(y_dev, x, W, T, rng, what, bias_bits=None):
+    N = W.rows
+    y = y_dev.detach().cpu().numpy().reshape(-1)
+    got = y[: T * N].reshape(T, N)
+    assert np.all(y[T * N:] == CANARY), f"{what}: wrote past y"
+    idx = sample_rows(rng, N)
+    ref, cond = O.linear_dq_f64(x[:T], W.dq_rows(idx), None if bias_bits is None else bias_bits[idx])
+    g = got[:, idx].astype(np.float64)
+    assert np.all(np.isfinite(g)), what
+    err = np.abs(g - ref)
+    worst = float((err / np.maximum(cond, 1e-30)).max())
+    rel = float(err.max() / max(np.abs(ref).max(), 1e-30))
+    say(f"  {what}: cond err {worst:.3g}, max rel {rel:.3g}")
+    assert worst <= KGEMV_TOL, f"{what}: conditioning error {worst:.3g}"
+    assert rel <= MAX_REL, f"{what}: max rel error {rel:.3g}"
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("xtype", ["bf16", "fp32"])
+def test_prefill_gemm_t1024_wide(kind, xtype):
+    """Config 5's gate/up shape (T = 1024, 18944 x 3584): the 128 x 128
+    output-tile instance, chosen when row tiles x column tiles >= 2 x CUs."""
+    rng = np.random.default_rng(1024 + kind + (10 if xtype == "fp32" else 0))
+    T, N, K = 1024, 18944, 3584
+    W = Packed(rng, N, K, kind)
+    y = out_buffer(T, N)
+    say("gemm T=1024 wide", kind, xtype)
+    if xtype == "bf16":
+        xb = O.seeded_bf16(rng, (T, K), 1.0)
+        x = O.bf16_to_f32(xb)
+        ops.launch_gemm_bf16x(torch.from_numpy(xb.view(np.int16)).cuda(), W.view, None, T, K, N, y)
+    else:
+        x = rng.standard_normal((T, K), dtype=np.float32)
+        ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x, W, T, rng, f"gemm T=1024 {xtype} kind={kind}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [1, 9, 12, 16])
+def test_gate_up_7b_multi(kind, M):
+    """gate|up of one 7B layer in one iq_gemv_multi call (2 x 18944 x 3584)."""
+    rng = np.random.default_rng(900 + 20 * kind + M)
+    K = 3584
+    Ws = [Packed(rng, 18944, K, kind) for _ in range(2)]
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("gate|up 7B multi", kind, M)
+    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], None, M, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y) in enumerate(zip(Ws, ys)):
+        check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_lm_head_int8(M):
+    """The int8 lm_head 152064 x 3584 (9504 tiles)."""
+    rng = np.random.default_rng(152064 + M)
+    N, K = 152064, 3584
+    W = Packed(rng, N, K, 0)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    y = out_buffer(M, N)
+    say("lm_head int8", M)
+    ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x, W, M, rng, f"lm_head M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_decode_set_7b_16_rows(kind):
+    """The remaining 7B decode calls at 16 rows: q|k|v (one call, biases),
+    o, and down (K = 18944)."""
+    rng = np.random.default_rng(716 + kind)
+    M = 16
+    for K, Ns in ((3584, (3584, 512, 512)), (3584, (3584,)), (18944, (3584,))):
+        Ws = [Packed(rng, N, K, kind) for N in Ns]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        bias_bits = [O.seeded_bf16(rng, (N,), 0.5) for N in Ns]
+        bds = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+        ys = [out_buffer(M, W.rows) for W in Ws]
+        say("7B decode set 16 rows", kind, K, Ns)
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bds, M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y) in enumerate(zip(Ws, ys)):
+            check_sampled(y, x, W, M, rng, f"7B K={K} N={Ns[i]} kind={kind}", bias_bits[i])
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [8, 16])
+def test_direct_call_invalidates_preparation(kind, M):
+    """A direct GEMV that converts its own activations into the workspace
+    makes a later iq_gemv_prepped on the older preparation fail (IQ_ESHAPE)
+    instead of multiplying the wrong activations; a fresh preparation works."""
+    rng = np.random.default_rng(55 + kind + M)
+    K, N = 3584, 3584
+    W = Packed(rng, N, K, kind)
+    x1 = rng.standard_normal((M, K), dtype=np.float32)
+    x2 = rng.standard_normal((M, K), dtype=np.float32)
+    y = out_buffer(M, N)
+    say("prep invalidation", kind, M)
+    ops.gemv_prep(torch.from_numpy(x1).cuda(), M, K, kind)
+    ops.gemv_multi(torch.from_numpy(x2).cuda(), [W.view], None, M, K, [y])
+    with pytest.raises(RuntimeError, match="shape"):
+        ops.gemv_prepped(W.view, None, M, K, N, y)
+    ops.gemv_prep(torch.from_numpy(x1).cuda(), M, K, kind)
+    ops.gemv_prepped(W.view, None, M, K, N, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x1, W, M, rng, f"re-prepared kind={kind} M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_two_streams_have_separate_workspaces(kind):
+    """Preparations on two streams do not disturb each other: each stream's
+    iq_gemv_prepped multiplies that stream's activations."""
+    rng = np.random.default_rng(77 + kind)
+    M, K, N = 12, 3584, 4096
+    W = Packed(rng, N, K, kind)
+    xs = [rng.standard_normal((M, K), dtype=np.float32) for _ in range(2)]
+    xd = [torch.from_numpy(x).cuda() for x in xs]
+    ys = [out_buffer(M, N) for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        ops.init(0, s)
+    torch.cuda.synchronize()
+    say("two streams", kind)
+    ops.gemv_prep(xd[0], M, K, kind, stream=streams[0])
+    ops.gemv_prep(xd[1], M, K, kind, stream=streams[1])
+    ops.gemv_prepped(W.view, None, M, K, N, ys[1], stream=streams[1])
+    ops.gemv_prepped(W.view, None, M, K, N, ys[0], stream=streams[0])
+    torch.cuda.synchronize()
+    for i in range(2):
+        check_sampled(ys[i], xs[i], W, M, rng, f"stream {i} kind={kind}")
