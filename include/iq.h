@@ -68,6 +68,18 @@ typedef struct iq_view {
 int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64_t in,
             int64_t out, float* y, void* stream);
 
+/* iq_gemv without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops and harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same contract and
+ * kernels as iq_gemv, limited to in <= 32768 (IQ_ETOOLARGE beyond), with
+ * its scratch (activation operands and split-K partial sums, ~20.1 MiB) in
+ * a static device array of the library that each device holds until the
+ * process ends.  Every call on a device shares that array, whatever the
+ * stream: calls that overlap in time on one device race, so order them
+ * (e.g. one stream).  No state carries from one call to the next. */
+int iq_gemv_noalloc(const float* x, const iq_view* W, const uint16_t* bias, int B, int64_t in,
+                    int64_t out, float* y, void* stream);
+
 /* The two halves of iq_gemv, for callers that multiply one activation
  * block by several matrices (q/k/v, gate/up share their input):
  * iq_gemv_prep takes x [B][in] (fp32) once into the device workspace: a

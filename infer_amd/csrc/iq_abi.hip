@@ -47,7 +47,57 @@ hipError_t create_workspace(Workspace* ws) {
     return hipSuccess;
 }
 
+// Workspace sizes of iq_gemv_noalloc: activations of up to kStaticMaxK
+// columns x 32 rows, and the same split-K partial-sum capacity as a
+// workspace of get_workspace().
+constexpr int64_t kStaticMaxK = 32768;
+constexpr size_t kStaticXq = size_t(kMaxRowsGemv) * (kStaticMaxK / kGroup) * 4 * kGroup;  // 4 MiB
+constexpr size_t kStaticMeta = sizeof(int4) * (kStaticMaxK / kGroup) * kMaxRowsGemv;       // 128 KiB
+constexpr size_t kStaticPart = sizeof(float) * kPartialFloats;                              // 16 MiB
+constexpr size_t kStaticBytes = kStaticXq + kStaticMeta + kStaticPart;
+
 }  // namespace
+}  // namespace iq
+
+// The scratch of iq_gemv_noalloc: part of the code object, so every device
+// the library runs on holds its own copy until the process ends.  Host code
+// never passes `scratch` itself to a kernel (on the host it is only a
+// stand-in symbol): it uses the device address that hipGetSymbolAddress
+// returns for the current device (static_workspace below).
+static __device__ __align__(256) unsigned char scratch[iq::kStaticBytes];
+
+namespace iq {
+namespace {
+
+Workspace g_static_ws[kMaxDevices];
+bool g_static_ready[kMaxDevices];
+
+}  // namespace
+
+hipError_t static_workspace(Workspace** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_static_ready[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!ptr) return hipErrorInvalidSymbol;
+        char* p = static_cast<char*>(ptr);
+        Workspace& w = g_static_ws[dev];
+        w.base = ptr;
+        w.bytes = kStaticBytes;
+        w.xf = nullptr;  // no preparation API on this workspace
+        w.xq = reinterpret_cast<int8_t*>(p);
+        w.xmeta = reinterpret_cast<int4*>(p + kStaticXq);
+        w.partials = reinterpret_cast<float*>(p + kStaticXq + kStaticMeta);
+        g_static_ready[dev] = true;
+    }
+    *out = &g_static_ws[dev];
+    return hipSuccess;
+}
 
 hipError_t get_workspace(hipStream_t stream, Workspace** out) {
     int dev = 0;
@@ -129,6 +179,7 @@ int iq_init_stream(int device, void* stream) {
     }
     iq::Workspace* ws = nullptr;
     e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e == hipSuccess) e = iq::static_workspace(&ws);  // iq_gemv_noalloc's scratch address
     (void)iq::device_cu_count();
     if (device != cur) (void)hipSetDevice(cur);
     return ws_status(e);
@@ -146,6 +197,19 @@ int iq_gemv(const float* x, const iq_view* W, const uint16_t* bias, int B, int64
     iq::Workspace* ws = nullptr;
     hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
     if (e != hipSuccess) return ws_status(e);
+    return from_hip(iq::launch_gemv(x, to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
+}
+
+int iq_gemv_noalloc(const float* x, const iq_view* W, const uint16_t* bias, int B, int64_t in, int64_t out,
+                    float* y, void* stream) {
+    int rc = check_view(W, in, out);
+    if (rc) return rc;
+    if (!x || !y) return IQ_ENULL;
+    if (B < 1 || B > iq::kMaxRowsGemv) return IQ_ESHAPE;
+    if (W->groups * IQ_GROUP > iq::kStaticMaxK) return IQ_ETOOLARGE;
+    iq::Workspace* ws = nullptr;
+    const hipError_t e = iq::static_workspace(&ws);
+    if (e != hipSuccess) return from_hip(e);
     return from_hip(iq::launch_gemv(x, to_qview(W), bias, B, y, ws, static_cast<hipStream_t>(stream)));
 }
 

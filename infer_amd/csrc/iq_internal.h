@@ -54,6 +54,10 @@ constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K parti
 // use.  Every stream has its own, so calls on different streams never share
 // activation or partial-sum buffers; calls on one stream are ordered by it.
 hipError_t get_workspace(hipStream_t stream, Workspace** ws);
+// The workspace of iq_gemv_noalloc on the current device: views into the
+// library's static device array (no allocation; shared by every call on
+// the device).
+hipError_t static_workspace(Workspace** ws);
 
 hipError_t launch_quantize(const uint16_t* w, int64_t rows, int64_t cols, int kind, uint8_t* q,
                            uint16_t* scales, uint8_t* zeros, hipStream_t stream);

@@ -48,6 +48,7 @@ _I64 = ctypes.c_int64
 _VP = ctypes.POINTER(IqView)
 SIGNATURES = {
     "iq_gemv": ([_P, _VP, _P, ctypes.c_int, _I64, _I64, _P, _P], ctypes.c_int),
+    "iq_gemv_noalloc": ([_P, _VP, _P, ctypes.c_int, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_gemv_prep": ([_P, ctypes.c_int, _I64, ctypes.c_int, _P], ctypes.c_int),
     "iq_gemv_prepped": ([_VP, _P, ctypes.c_int, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_gemv_prepped_multi": ([_P, ctypes.c_int, _P, ctypes.c_int, _I64, _P, _P], ctypes.c_int),
@@ -194,6 +195,13 @@ def launch_gemv_batched_q(x, W, bias, B, in_, out, y, stream=None):
     """y[b, o] = sum_c dequant(W, o, c) x[b, c] (+ bias[o]) for b < B <= 32."""
     rc = lib().iq_gemv(_ptr(x), W.c, _bias_ptr(bias), int(B), int(in_), int(out), _ptr(y), _stream(stream))
     _check(rc, "iq_gemv")
+
+
+def gemv_noalloc(x, W, bias, B, in_, out, y, stream=None):
+    """launch_gemv_batched_q on the library's static scratch (no allocation;
+    in <= 32768; calls that overlap on one device race)."""
+    rc = lib().iq_gemv_noalloc(_ptr(x), W.c, _bias_ptr(bias), int(B), int(in_), int(out), _ptr(y), _stream(stream))
+    _check(rc, "iq_gemv_noalloc")
 
 
 def gemv_prep(x, B, in_, kind, stream=None):
