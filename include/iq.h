@@ -47,7 +47,9 @@ enum {
     IQ_ENULL = -3,      /* a required pointer is NULL */
     IQ_ETOOLARGE = -4,  /* problem exceeds the workspace limits */
     IQ_ENOMEM = -5,     /* workspace allocation failed */
-    IQ_EDEVICE = -6     /* no usable gfx950 device */
+    IQ_EDEVICE = -6,    /* no usable gfx950 device, or not the chain's device */
+    IQ_EALIAS = -7,     /* a chain stage rewrites memory an earlier stage used */
+    IQ_ETIMEOUT = -8    /* a chain's grid barrier gave up waiting */
 };
 
 /* gpu::QuantView (kernels/ops/ops.cuh:166-172), byte-compatible on LP64:
@@ -146,6 +148,59 @@ int iq_embedding(const iq_view* table, const int64_t* ids, int64_t T, int64_t H,
  * zeros in the layout above.  int4 needs even cols (as the reference). */
 int iq_quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, int kind, uint8_t* q,
                 uint16_t* scales, uint8_t* zeros, void* stream);
+
+/* ---------------------------------------------------------------- chains
+ * A chain runs a program of dependent 1-row GEMV stages in one persistent
+ * launch: the quantised linears of a decode step in the order of
+ * GpuBatch::Impl::launch_sequence (kernels/batch_gpu.cu:186-215), each
+ * stage reading what earlier stages wrote.  No reference counterpart as an
+ * entry point: the reference issues each stage as its own launch
+ * (launch_gemv_batched_q, launch_rmsnorm, launch_swiglu, launch_residual_add).
+ *
+ * Stage = y_i = f_out( dequant(W_i) . f_in(x) + bias_i ), i < n <= 3, all W_i
+ * of one kind and width K (K % 256 == 0, K <= 24576), x 16-byte aligned:
+ *   f_in   IQ_IN_PLAIN    x[k]
+ *          IQ_IN_RMSNORM  x[k] / sqrt(mean(x^2) + eps) * norm[k], norm bf16
+ *                         (src/forward.cpp:21-31)
+ *          IQ_IN_GQA      x[(k / (head_dim * group)) * head_dim + k % head_dim]:
+ *                         the attention output of a sequence of one token,
+ *                         whose softmax over its single key is 1, so every
+ *                         query head receives the value row of its key/value
+ *                         head (x = v, K / group values)
+ *   f_out  IQ_OUT_STORE     y_i[o] = acc + bias_i[o]
+ *          IQ_OUT_RESIDUAL  y_0[o] = residual[o] + acc  (n == 1)
+ *          IQ_OUT_SWIGLU    y_0[o] = silu(acc_0 + b_0) * (acc_1 + b_1), n == 2
+ *                           (gate, up; kernels/ops/elementwise.cu:6-11)
+ * Single assignment: no stage may write memory that it or an earlier stage
+ * of the chain reads or writes (IQ_EALIAS); inputs of the first stages may
+ * be written by earlier launches.  Outputs are fp32 vectors of W_i->rows. */
+enum { IQ_IN_PLAIN = 0, IQ_IN_RMSNORM = 1, IQ_IN_GQA = 2 };
+enum { IQ_OUT_STORE = 0, IQ_OUT_RESIDUAL = 1, IQ_OUT_SWIGLU = 2 };
+
+typedef struct iq_stage {
+    int32_t in_op, out_op, n;
+    int32_t gqa_head_dim, gqa_group;  /* IQ_IN_GQA */
+    float eps;                        /* IQ_IN_RMSNORM */
+    const float* x;
+    const uint16_t* norm;             /* IQ_IN_RMSNORM: bf16 [K], 16-byte aligned */
+    const float* residual;            /* IQ_OUT_RESIDUAL: [rows] */
+    iq_view W[3];
+    const uint16_t* bias[3];          /* bf16 or NULL */
+    float* y[3];                      /* IQ_OUT_SWIGLU: y[0] only */
+} iq_stage;
+
+typedef struct iq_chain iq_chain;
+
+/* Validates the n stages and uploads the program for the current device
+ * (allocates; the run allocates nothing). */
+int iq_chain_create(const iq_stage* stages, int n, iq_chain** out);
+/* Enqueues one run of the whole program on `stream` (two launches: a
+ * counter reset and the cooperative chain kernel). */
+int iq_chain_run(const iq_chain* chain, void* stream);
+/* Synchronises the device; IQ_ETIMEOUT if a barrier of the last run gave
+ * up (its outputs are then undefined), else 0. */
+int iq_chain_status(const iq_chain* chain);
+void iq_chain_destroy(iq_chain* chain);
 
 /* Reserve the workspace of (device, null stream) (done lazily by the first
  * call that needs it).  Call before capturing a graph.  Returns 0 or an

@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HOST_CXX_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
                   "-I" + os.path.join(os.path.dirname(HERE), "include"), "-I" + os.path.join(HERE, "host"),
                   "-I" + os.path.join(ROCM, "include")]
-SOURCES = ["iq_abi.hip", "iq_quant.hip", "iq_gemv.hip", "iq_gemm.hip"]
+SOURCES = ["iq_abi.hip", "iq_quant.hip", "iq_gemv.hip", "iq_gemm.hip", "iq_chain.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

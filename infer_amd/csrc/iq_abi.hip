@@ -350,7 +350,9 @@ const char* iq_error_string(int code) {
         case IQ_ENULL: return "iq: required pointer is NULL";
         case IQ_ETOOLARGE: return "iq: problem exceeds workspace limits";
         case IQ_ENOMEM: return "iq: workspace allocation failed";
-        case IQ_EDEVICE: return "iq: no usable device";
+        case IQ_EDEVICE: return "iq: no usable device (or not the device the chain was made on)";
+        case IQ_EALIAS: return "iq: a chain stage writes memory that it or an earlier stage uses";
+        case IQ_ETIMEOUT: return "iq: a chain barrier gave up waiting (outputs undefined)";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

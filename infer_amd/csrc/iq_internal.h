@@ -81,6 +81,10 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
                        const uint16_t* bias, int64_t T, float* y, float* part, hipStream_t stream);
 
+// A validated stage program on the device (iq_chain.hip).
+struct Chain;
+void chain_destroy(Chain* ch);
+
 // Device properties used by the dispatch heuristics.
 int device_cu_count();
 

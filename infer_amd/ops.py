@@ -42,6 +42,24 @@ class IqView(ctypes.Structure):
     ]
 
 
+class IqStage(ctypes.Structure):
+    """iq_stage (include/iq.h): one stage of a chain."""
+    _fields_ = [
+        ("in_op", ctypes.c_int32),
+        ("out_op", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("gqa_head_dim", ctypes.c_int32),
+        ("gqa_group", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("x", ctypes.c_void_p),
+        ("norm", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
+        ("W", IqView * 3),
+        ("bias", ctypes.c_void_p * 3),
+        ("y", ctypes.c_void_p * 3),
+    ]
+
+
 # Every function include/iq.h declares, with its ctypes signature.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -58,6 +76,10 @@ SIGNATURES = {
     "iq_linear": ([_P, _VP, _P, _I64, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_embedding": ([_VP, _P, _I64, _I64, _P, _P], ctypes.c_int),
     "iq_quantize": ([_P, _I64, _I64, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
+    "iq_chain_create": ([ctypes.POINTER(IqStage), ctypes.c_int, ctypes.POINTER(_P)], ctypes.c_int),
+    "iq_chain_run": ([_P, _P], ctypes.c_int),
+    "iq_chain_status": ([_P], ctypes.c_int),
+    "iq_chain_destroy": ([_P], None),
     "iq_init": ([ctypes.c_int], ctypes.c_int),
     "iq_init_stream": ([ctypes.c_int, _P], ctypes.c_int),
     "iq_error_string": ([ctypes.c_int], ctypes.c_char_p),

@@ -140,3 +140,61 @@ def seeded_bf16(rng, shape, sd):
     """Synthetic weights: fp32 ~N(0, sd) rounded RNE to bf16 (src/f16.h:41-51),
     the form llm::quantize consumes (src/quant.h:61)."""
     return f32_to_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(sd))
+
+
+# ---------------------------------------------------------------- decode step
+# The reference's CPU forward (src/forward.cpp:160-262) for one token at
+# position 0, on dequantised weights, in float64 (the truth the fp32 GPU
+# chain is compared with).  Pieces: rmsnorm (src/forward.cpp:21-31), linear
+# (:35-47), silu (src/forward_internal.h:41-42), attention over one cached
+# key (softmax weight 1: every query head takes its kv head's value row).
+
+def rmsnorm_f64(x, w_bf16, eps):
+    """src/forward.cpp:21-31: x / sqrt(mean(x^2) + eps) * w."""
+    x = np.asarray(x, np.float64)
+    scale = 1.0 / np.sqrt(np.mean(x * x) + float(eps))
+    return x * scale * bf16_to_f32(w_bf16).astype(np.float64)
+
+
+def silu_f64(z):
+    """src/forward_internal.h:41-42: z / (1 + exp(-z))."""
+    z = np.asarray(z, np.float64)
+    return z / (1.0 + np.exp(-z))
+
+
+def attention_single_key(v, n_heads, n_kv_heads, head_dim):
+    """Attention output of a sequence of one token (src/forward.cpp
+    attention() with T = 1): softmax over one score is 1, so query head h
+    gets value row h // (n_heads / n_kv_heads)."""
+    v = np.asarray(v).reshape(n_kv_heads, head_dim)
+    grp = n_heads // n_kv_heads
+    return np.repeat(v, grp, axis=0).reshape(-1)
+
+
+def decode_first_token_f64(model, token):
+    """Every intermediate of the forward of `token` at position 0.  model:
+    cfg dict (hidden, heads, kv_heads, head_dim, eps), embed_dq [V, H],
+    head_dq, final_norm (bf16 bits), layers: dicts of dequantised q, k, v,
+    o, gate, up, down (float arrays [out, in]), bf16 bits input_ln, post_ln,
+    optional q_b, k_b, v_b."""
+    c = model["cfg"]
+    h = np.asarray(model["embed_dq"][token], np.float64)
+    out = {"h0": h, "layers": []}
+    for Lw in model["layers"]:
+        n = rmsnorm_f64(h, Lw["input_ln"], c["eps"])
+        r = {"h": h}
+        for name in ("q", "k", "v"):
+            y = np.asarray(Lw[name], np.float64) @ n
+            if Lw.get(name + "_b") is not None:
+                y = y + bf16_to_f32(Lw[name + "_b"]).astype(np.float64)
+            r[name] = y
+        ctx = attention_single_key(r["v"], c["heads"], c["kv_heads"], c["head_dim"])
+        h1 = h + np.asarray(Lw["o"], np.float64) @ ctx
+        n2 = rmsnorm_f64(h1, Lw["post_ln"], c["eps"])
+        act = silu_f64(np.asarray(Lw["gate"], np.float64) @ n2) * (np.asarray(Lw["up"], np.float64) @ n2)
+        h2 = h1 + np.asarray(Lw["down"], np.float64) @ act
+        r.update(h1=h1, act=act, h2=h2)
+        out["layers"].append(r)
+        h = h2
+    out["logits"] = np.asarray(model["head_dq"], np.float64) @ rmsnorm_f64(h, model["final_norm"], c["eps"])
+    return out

@@ -220,3 +220,97 @@ def test_embedding_is_dequant():
         out = O.embedding(q, s, z, kind, 256, ids)
         dq = O.dequant_matrix(q, s, z, kind, 50, 256)
         assert np.array_equal(out, dq[ids])
+
+
+# ---------------------------------------------------------------- decode step pieces
+ONE_BF16 = np.uint16(0x3F80)
+
+
+def test_rmsnorm_closed_forms():
+    """src/forward.cpp:21-31 pinned by closed forms: [3, 4] has mean square
+    12.5; a constant vector maps to its sign (eps = 0); scale invariance;
+    the weight multiplies elementwise.  A 'sum instead of mean' or a dropped
+    weight fails one of these."""
+    w = np.full(2, ONE_BF16)
+    y = O.rmsnorm_f64(np.array([3.0, 4.0]), w, 0.0)
+    assert np.allclose(y, np.array([3.0, 4.0]) / np.sqrt(12.5), rtol=1e-15)
+    c = np.full(64, -2.5)
+    assert np.allclose(O.rmsnorm_f64(c, np.full(64, ONE_BF16), 0.0), -1.0, rtol=1e-15)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(256)
+    wb = O.f32_to_bf16(rng.uniform(0.5, 1.5, 256).astype(np.float32))
+    a = O.rmsnorm_f64(x, wb, 0.0)
+    assert np.allclose(O.rmsnorm_f64(x * 1e3, wb, 0.0), a, rtol=1e-12)
+    assert np.allclose(a / O.bf16_to_f32(wb), O.rmsnorm_f64(x, np.full(256, ONE_BF16), 0.0), rtol=1e-12)
+    # eps enters inside the root: x = [1] * 4, eps = 3 -> 1 / 2
+    assert np.allclose(O.rmsnorm_f64(np.ones(4), np.full(4, ONE_BF16), 3.0), 0.5, rtol=1e-15)
+
+
+def test_silu_closed_forms():
+    """src/forward_internal.h:41-42: silu(0) = 0, silu(z) - silu(-z) = z,
+    silu(1) = 1 / (1 + e^-1), silu(z) -> z for large z."""
+    z = np.linspace(-8, 8, 33)
+    assert O.silu_f64(0.0) == 0.0
+    assert np.allclose(O.silu_f64(z) - O.silu_f64(-z), z, rtol=1e-14, atol=1e-14)
+    assert abs(O.silu_f64(1.0) - 0.7310585786300049) < 1e-15
+    assert abs(O.silu_f64(40.0) - 40.0) < 1e-12
+
+
+def test_single_key_attention_is_the_value_row():
+    """Brute force: scaled dot-product attention with one cached key (any q,
+    k) and GQA head sharing gives each query head its kv head's value row."""
+    rng = np.random.default_rng(2)
+    nh, nkv, hd = 8, 2, 16
+    q = rng.standard_normal((nh, hd))
+    k = rng.standard_normal((nkv, hd))
+    v = rng.standard_normal((nkv, hd))
+    out = np.zeros((nh, hd))
+    for h in range(nh):
+        kv = h // (nh // nkv)
+        s = np.array([q[h] @ k[kv] / np.sqrt(hd)])
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p[0] * v[kv]
+    assert np.allclose(O.attention_single_key(v.reshape(-1), nh, nkv, hd), out.reshape(-1), rtol=1e-15)
+
+
+def _tiny_decode_model(rng, zero_o_down=False):
+    H, I, nh, nkv, hd, V = 32, 48, 4, 2, 8, 20
+    cfg = dict(hidden=H, inter=I, heads=nh, kv_heads=nkv, head_dim=hd, vocab=V, layers=2, eps=1e-6)
+    bf = lambda n: O.f32_to_bf16(rng.uniform(0.5, 1.5, n).astype(np.float32))
+    layers = []
+    for _ in range(2):
+        Lw = {"q": rng.standard_normal((nh * hd, H)), "k": rng.standard_normal((nkv * hd, H)),
+              "v": rng.standard_normal((nkv * hd, H)), "o": rng.standard_normal((H, nh * hd)),
+              "gate": rng.standard_normal((I, H)), "up": rng.standard_normal((I, H)),
+              "down": rng.standard_normal((H, I)), "input_ln": bf(H), "post_ln": bf(H)}
+        if zero_o_down:
+            Lw["o"] = np.zeros_like(Lw["o"])
+            Lw["down"] = np.zeros_like(Lw["down"])
+        layers.append(Lw)
+    return dict(cfg=cfg, embed_dq=rng.standard_normal((V, H)), head_dq=rng.standard_normal((V, H)),
+                final_norm=bf(H), layers=layers)
+
+
+def test_decode_wiring_invariants():
+    """The residual stream of src/forward.cpp:200-246: with o and down zero
+    the hidden state stays the embedding row through every layer and the
+    logits are head . rmsnorm(embedding); q/k/v read rmsnorm(h, input_ln);
+    h1 = h + o . attn; h2 = h1 + down . act."""
+    rng = np.random.default_rng(3)
+    m = _tiny_decode_model(rng, zero_o_down=True)
+    r = O.decode_first_token_f64(m, 5)
+    for Lr in r["layers"]:
+        assert np.array_equal(Lr["h2"], m["embed_dq"][5])
+    assert np.allclose(r["logits"], m["head_dq"] @ O.rmsnorm_f64(m["embed_dq"][5], m["final_norm"], 1e-6))
+    m = _tiny_decode_model(rng)
+    r = O.decode_first_token_f64(m, 3)
+    L0, W0 = r["layers"][0], m["layers"][0]
+    n = O.rmsnorm_f64(m["embed_dq"][3], W0["input_ln"], 1e-6)
+    assert np.allclose(L0["q"], W0["q"] @ n) and np.allclose(L0["v"], W0["v"] @ n)
+    ctx = O.attention_single_key(L0["v"], 4, 2, 8)
+    assert np.allclose(L0["h1"], m["embed_dq"][3] + W0["o"] @ ctx)
+    n2 = O.rmsnorm_f64(L0["h1"], W0["post_ln"], 1e-6)
+    assert np.allclose(L0["act"], O.silu_f64(W0["gate"] @ n2) * (W0["up"] @ n2))
+    assert np.allclose(L0["h2"], L0["h1"] + W0["down"] @ L0["act"])
+    assert np.array_equal(r["layers"][1]["h"], L0["h2"])
