@@ -48,8 +48,7 @@ enum {
     IQ_ETOOLARGE = -4,  /* problem exceeds the workspace limits */
     IQ_ENOMEM = -5,     /* workspace allocation failed */
     IQ_EDEVICE = -6,    /* no usable gfx950 device, or not the chain's device */
-    IQ_EALIAS = -7,     /* a chain stage rewrites memory an earlier stage used */
-    IQ_ETIMEOUT = -8    /* a chain's grid barrier gave up waiting */
+    IQ_EALIAS = -7      /* a chain stage's output overlaps its input */
 };
 
 /* gpu::QuantView (kernels/ops/ops.cuh:166-172), byte-compatible on LP64:
@@ -150,30 +149,32 @@ int iq_quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, int kind, ui
                 uint16_t* scales, uint8_t* zeros, void* stream);
 
 /* ---------------------------------------------------------------- chains
- * A chain runs a program of dependent 1-row GEMV stages in one persistent
- * launch: the quantised linears of a decode step in the order of
- * GpuBatch::Impl::launch_sequence (kernels/batch_gpu.cu:186-215), each
- * stage reading what earlier stages wrote.  No reference counterpart as an
- * entry point: the reference issues each stage as its own launch
- * (launch_gemv_batched_q, launch_rmsnorm, launch_swiglu, launch_residual_add).
+ * A chain is a program of dependent 1-row GEMV stages: the quantised
+ * linears of a decode step in the order of GpuBatch::Impl::launch_sequence
+ * (kernels/batch_gpu.cu:186-215), each stage reading what earlier stages
+ * wrote, with the elementwise work between them fused into the stages.
+ * A run is one launch per stage on one stream (capturable into a HIP
+ * graph).  No reference counterpart as an entry point: the reference
+ * issues launch_gemv_batched_q, launch_rmsnorm, launch_swiglu and
+ * launch_residual_add separately.
  *
  * Stage = y_i = f_out( dequant(W_i) . f_in(x) + bias_i ), i < n <= 3, all W_i
- * of one kind and width K (K % 256 == 0, K <= 24576), x 16-byte aligned:
+ * of one kind and width K (K % 256 == 0; int4 K <= 24576, int8 K <= 20480,
+ * halved for IQ_OUT_SWIGLU), x 16-byte aligned:
  *   f_in   IQ_IN_PLAIN    x[k]
  *          IQ_IN_RMSNORM  x[k] / sqrt(mean(x^2) + eps) * norm[k], norm bf16
- *                         (src/forward.cpp:21-31)
+ *                         (src/forward.cpp:21-31); K <= 16384
  *          IQ_IN_GQA      x[(k / (head_dim * group)) * head_dim + k % head_dim]:
  *                         the attention output of a sequence of one token,
  *                         whose softmax over its single key is 1, so every
  *                         query head receives the value row of its key/value
  *                         head (x = v, K / group values)
  *   f_out  IQ_OUT_STORE     y_i[o] = acc + bias_i[o]
- *          IQ_OUT_RESIDUAL  y_0[o] = residual[o] + acc  (n == 1)
+ *          IQ_OUT_RESIDUAL  y_0[o] = residual[o] + (acc + bias_0[o])  (n == 1)
  *          IQ_OUT_SWIGLU    y_0[o] = silu(acc_0 + b_0) * (acc_1 + b_1), n == 2
  *                           (gate, up; kernels/ops/elementwise.cu:6-11)
- * Single assignment: no stage may write memory that it or an earlier stage
- * of the chain reads or writes (IQ_EALIAS); inputs of the first stages may
- * be written by earlier launches.  Outputs are fp32 vectors of W_i->rows. */
+ * A stage's outputs may not overlap its own inputs (IQ_EALIAS).  Outputs
+ * are fp32 vectors of W_i->rows. */
 enum { IQ_IN_PLAIN = 0, IQ_IN_RMSNORM = 1, IQ_IN_GQA = 2 };
 enum { IQ_OUT_STORE = 0, IQ_OUT_RESIDUAL = 1, IQ_OUT_SWIGLU = 2 };
 
@@ -191,15 +192,11 @@ typedef struct iq_stage {
 
 typedef struct iq_chain iq_chain;
 
-/* Validates the n stages and uploads the program for the current device
- * (allocates; the run allocates nothing). */
+/* Validates the n stages and records their launch shapes for the current
+ * device (host memory only; the run allocates nothing). */
 int iq_chain_create(const iq_stage* stages, int n, iq_chain** out);
-/* Enqueues one run of the whole program on `stream` (two launches: a
- * counter reset and the cooperative chain kernel). */
+/* Enqueues one run of the whole program on `stream`. */
 int iq_chain_run(const iq_chain* chain, void* stream);
-/* Synchronises the device; IQ_ETIMEOUT if a barrier of the last run gave
- * up (its outputs are then undefined), else 0. */
-int iq_chain_status(const iq_chain* chain);
 void iq_chain_destroy(iq_chain* chain);
 
 /* Reserve the workspace of (device, null stream) (done lazily by the first

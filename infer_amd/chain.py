@@ -1,5 +1,5 @@
-"""Stage programs of dependent 1-row GEMVs in one persistent launch
-(include/iq.h, iq_chain_*), and the decode step built from them.
+"""Stage programs of dependent 1-row GEMVs (include/iq.h, iq_chain_*), and
+the decode step built from them.
 
 DecodeStep is the quantised part of the reference's decode step,
 GpuBatch::Impl::launch_sequence (kernels/batch_gpu.cu:186-215), for one
@@ -15,8 +15,8 @@ sequence of one token (position 0): the quantised embedding gather
 and logits = rmsnorm(h, final_norm) . W_head^T.  At position 0 the
 attention over the single cached key has softmax weight 1, so attn is the
 value row of each query head's key/value head (IQ_IN_GQA); RoPE changes q
-and k only.  Every intermediate vector has its own buffer (the chain's
-single-assignment rule), so all of them can be inspected after a step.
+and k only.  Every intermediate vector has its own buffer (static
+single-assignment), so all of them can be inspected after a step.
 """
 import ctypes
 
@@ -76,10 +76,6 @@ class Chain:
 
     def run(self, stream=None):
         ops._check(_lib().iq_chain_run(self._h, ops._stream(stream)), "iq_chain_run")
-
-    def status(self):
-        """Synchronises; raises if a grid barrier of the last run gave up."""
-        ops._check(_lib().iq_chain_status(self._h), "iq_chain_status")
 
     def close(self):
         if getattr(self, "_h", None):

@@ -351,8 +351,7 @@ const char* iq_error_string(int code) {
         case IQ_ETOOLARGE: return "iq: problem exceeds workspace limits";
         case IQ_ENOMEM: return "iq: workspace allocation failed";
         case IQ_EDEVICE: return "iq: no usable device (or not the device the chain was made on)";
-        case IQ_EALIAS: return "iq: a chain stage writes memory that it or an earlier stage uses";
-        case IQ_ETIMEOUT: return "iq: a chain barrier gave up waiting (outputs undefined)";
+        case IQ_EALIAS: return "iq: a chain stage's output overlaps its input";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

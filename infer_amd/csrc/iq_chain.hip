@@ -1,50 +1,41 @@
-// iq_chain.hip -- a chain of dependent 1-row quantised GEMVs in one
-// persistent launch: the quantised part of the reference's decode step
+// iq_chain.hip -- a chain of dependent 1-row quantised GEMV stages: the
+// quantised part of the reference's decode step
 // (GpuBatch::Impl::launch_sequence, kernels/batch_gpu.cu:186-215) as a
-// program of stages, each stage one linear call site (q|k|v, o, gate|up
-// with the SwiGLU of kernels/ops/elementwise.cu:6-11 as its epilogue, down,
-// the LM head) whose input is the output of an earlier stage.
+// program, each stage one linear call site (q|k|v, o, gate|up, down, the
+// LM head) whose input is the output of an earlier stage, with the
+// elementwise work around it fused in:
+//   prologue  RMSNorm of the input (launch_rmsnorm, src/forward.cpp:21-31),
+//             or the single-key attention output (value row of each query
+//             head's key/value head);
+//   epilogue  bias, residual add (launch_residual_add), or SwiGLU of a
+//             gate / up tile pair (launch_swiglu, kernels/ops/elementwise.cu:6-11).
+// One launch per stage, stream-ordered (the caller captures a run in a HIP
+// graph); the reference needs 3-5 launches per stage for the same work.
 //
-// Why one launch: a decode-step GEMV streams 7-70 MB and is over in 4-16 us,
-// of which 3-5 us per launch are ramp-up, the first-load latency and the
-// tail of the last workgroups.  Here one workgroup per CU stays resident for
-// the whole program; between dependent stages it crosses a grid barrier, and
-// because the weights of a GEMV do not depend on its input, each workgroup
-// requests the weights of its first slices of stage s+1 before it waits for
-// the other workgroups to finish stage s.  The HBM stream continues across
-// the barrier instead of draining and refilling at every kernel boundary.
+// The stage kernel is the 1-row GEMV's arithmetic (iq_limbs.h): a workgroup
+// owns one 16-row output tile (or a gate tile with the up tile of the same
+// rows); its waves split K into slices of whole 128-column groups, each
+// wave requests its activations first, then its scales, zero points and
+// weights (16-byte loads), converts its activation slice into byte limbs
+// in LDS while the weights stream in, and multiplies codes by limbs on
+// v_mfma_i32_16x16x64_i8 (exact int32 sums); combine() applies scale, zero
+// point and the activation exponent in fp32.  The slice sums are added in
+// wave order through LDS by the wave that finishes last (deterministic).
 //
-// Arithmetic per slice is the 1-row GEMV's (iq_limbs.h): the stage input is
-// converted once per workgroup into byte limbs in LDS, codes x limbs on
-// v_mfma_i32_16x16x64_i8 give exact int32 sums, combine() applies scale,
-// zero point and the activation exponent in fp32.
+// RMSNorm needs the whole input vector: every thread of the workgroup loads
+// a part of it (16-byte loads, issued before the weights), the sum of
+// squares is reduced in double through LDS in a fixed order, and the raw
+// vector stays in LDS for the waves' slices.
 //
-// Work split.  A stage's work units are 16-row output tiles (or, for the
-// SwiGLU epilogue, a gate tile with the up tile of the same rows); unit u
-// belongs to workgroup u mod W.  A unit's K range is cut into slices of
-// kSliceGroups 128-column groups; the 16 waves of a workgroup take 16
-// consecutive slices of the workgroup's list at a time, each holding the
-// next slice's weights in registers while it multiplies the current one.
-// Slice sums go to LDS and are added per tile in slice order (deterministic)
-// when the stage's slices are done.
-//
-// Coherence without cache maintenance.  The L2 is per XCD and not coherent
-// across XCDs, so: (1) every stage output is stored with agent-scope
-// (write-through) stores and waited for before the workgroup arrives at the
-// barrier; (2) every vector a stage reads was written by an earlier stage of
-// the same launch and is never written again in it (the host checks this
-// single-assignment rule), so no XCD can hold a stale copy of a line it
-// reads: the launch starts with invalidated L2s, and each line is first
-// touched after its producer's stores reached memory.
-//
-// Grid barrier: one counter, incremented once per workgroup and stage,
-// polled by one thread per workgroup; the launch is cooperative (every
-// workgroup resident), and the poll gives up after a bounded number of
-// sleeps (flag set, kernel exits normally) so that a broken launch cannot
-// hang the device.
+// A persistent variant (one cooperative launch for the whole program, grid
+// barriers between stages, next-stage weights requested before each
+// barrier) was built and measured slower: 2.75 ms against 1.16 ms for the
+// 7B step, because the barrier's atomics, the write-through stores and the
+// next input's loads wait in the same memory queues as the megabytes of
+// weights in flight (2-4 us each), and the stage's loop of dependent
+// slices kept too few bytes in flight per CU.
 #include <algorithm>
 #include <cstring>
-#include <mutex>
 #include <vector>
 
 #include "../../include/iq.h"
@@ -54,11 +45,8 @@ namespace iq {
 
 namespace {
 
-constexpr int kWaves = 16;         // waves per workgroup
-// A wave slice is 64 bytes of codes per lane: 4 groups of int4 or 2 of int8.
-constexpr int kSliceDw = 4;        // 16-byte weight registers per slice
-constexpr int kMaxPasses = 3;      // conversion passes (64 groups each): K <= 24576
 constexpr int kMaxStageMats = 3;
+constexpr int kMaxWaves = 16;
 
 struct CMat {
     const uint8_t* q;
@@ -70,346 +58,380 @@ struct CMat {
     int32_t tile0;  // first tile of this matrix in the stage's tile numbering
 };
 
+// One stage as the kernel sees it (a kernel argument: read through the
+// scalar cache).
 struct CStage {
     CMat mat[kMaxStageMats];
     const float* x;
     const uint16_t* norm;
     const float* res;
     float eps;
-    int32_t kind, in_op, out_op, nmat;
+    int32_t in_op, out_op, nmat;
     int32_t K, G;
-    int32_t units;   // work units
-    int32_t tpu;     // tiles per unit (2: SwiGLU pair)
-    int32_t chunks;  // slices per tile
-    int32_t gsl;     // groups per slice (4 int4, 2 int8)
+    int32_t units;    // workgroups: tiles, or gate / up tile pairs
+    int32_t tpu;      // tiles per unit (2: SwiGLU pair)
+    int32_t ks;       // waves per tile
+    int32_t gs;       // groups per wave slice (even; the last slice may be shorter)
     int32_t gqa_hd, gqa_span;  // IQ_IN_GQA: head_dim, head_dim * group
+    // RMSNorm input: per-16-row-tile sums of squares of x written by the
+    // stage that produced x (ssq_n of them), or null (then the kernel sums
+    // the whole input itself)
+    const float* ssq_in;
+    int32_t ssq_n;
+    // per-tile sums of squares of this stage's output (for a later RMSNorm), or null
+    float* ssq_out;
 };
 
-struct CParams {
-    const CStage* st;
-    int nst;
-    int* bar;        // [0] arrival counter, [1] timeout flag
-    int spin_limit;  // sleeps before a barrier wait gives up
+// Host record of a stage: the kernel argument and its launch shape.
+struct HostStage {
+    CStage st;
+    int kind;
+    int ng;  // slice capacity of the kernel instance
+    size_t lds;
 };
 
-// Weights, scales and zero points of one wave slice.
-// int4: w[g] = the lane's 16 bytes of group g < 4; int8: w[2g], w[2g + 1]
-// for g < 2.
-struct SliceRegs {
-    int4v_t w[kSliceDw];
-    uint32_t s[2];  // bf16 scales, groups (0,1) and (2,3)
-    uint32_t z;     // int4 zero points, one byte per group
-};
-
-// The slice a wave handles: tile, K groups [g0, g0 + gs), LDS slot.
-struct SliceRef {
-    int valid;
-    int slot;   // index into the workgroup's slice sums
-    int mat;
-    int64_t row0;
-    int g0, gs;
-};
-
-__device__ __forceinline__ int units_of(const CStage& st, int wg, int W) {
-    return st.units > wg ? (st.units - wg + W - 1) / W : 0;
+__device__ __forceinline__ CMat stage_mat(const CStage& st, int m) {
+    return m == 0 ? st.mat[0] : (m == 1 ? st.mat[1] : st.mat[2]);
 }
 
-__device__ __forceinline__ SliceRef slice_ref(const CStage& st, int wg, int W, int idx) {
-    SliceRef r{0, idx, 0, 0, 0, 0};
-    const int per_unit = st.tpu * st.chunks;
-    const int nsl = units_of(st, wg, W) * per_unit;
-    if (idx >= nsl) return r;
-    const int j = idx / per_unit, rem = idx - j * per_unit;
-    const int p = rem / st.chunks, c = rem - p * st.chunks;
-    const int u = wg + j * W;
-    int m = 0, tile;
-    if (st.tpu == 2) {
-        m = p;
-        tile = u;  // tile u of gate (p = 0) and of up (p = 1)
-    } else {
-        tile = u;
-        for (int i = 1; i < kMaxStageMats; i++)
-            if (i < st.nmat && tile >= st.mat[i].tile0) m = i;
-        tile -= st.mat[m].tile0;
-    }
-    r.valid = 1;
-    r.mat = m;
-    r.row0 = int64_t(tile) * 16;
-    r.g0 = c * st.gsl;
-    r.gs = st.G - r.g0 < st.gsl ? st.G - r.g0 : st.gsl;
-    return r;
-}
-
-// Requests one slice's weights, scales and zero points (rows past N and
-// groups past the slice read zero without a memory access).
-__device__ __forceinline__ void load_slice(SliceRegs& b, const CStage& st, const SliceRef& r, int ln, int kg) {
-    const CMat& m = st.mat[r.mat];
-    const int64_t row = r.row0 + ln;
-    const int G = st.G;
-    const int kind = st.kind;
-    const int64_t rb = kind == 1 ? st.K / 2 : st.K;
-    const rsrc_t rq = make_rsrc(m.q, r.valid ? int64_t(m.N) * rb : 0);
-    const rsrc_t rs = make_rsrc(m.scales, r.valid ? int64_t(m.N) * G * 2 : 0);
-    const rsrc_t rz = make_rsrc(m.zeros, (r.valid && kind == 1) ? int64_t(m.N) * G : 0);
-    const uint32_t vq = uint32_t(row * rb) + uint32_t(r.g0 * (kind == 1 ? 64 : 128) + kg * 16);
-    if (kind == 1) {
-#pragma unroll
-        for (int gl = 0; gl < 4; gl++)
-            b.w[gl] = __builtin_bit_cast(
-                int4v_t, __builtin_amdgcn_raw_buffer_load_b128(rq, vq + (gl < r.gs ? 0u : kOob), gl * 64, 0));
-    } else {
-#pragma unroll
-        for (int gl = 0; gl < 2; gl++)
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-                b.w[2 * gl + h] = __builtin_bit_cast(
-                    int4v_t, __builtin_amdgcn_raw_buffer_load_b128(rq, vq + (gl < r.gs ? 0u : kOob), gl * 128 + h * 64, 0));
-    }
-    // G is even and g0 even: scales of groups (2i, 2i + 1) are one 4-byte
-    // word, their zero points one 2-byte word
-    const uint32_t vs = uint32_t((row * G + r.g0) * 2), vz = uint32_t(row * G + r.g0);
-#pragma unroll
-    for (int i = 0; i < 2; i++) b.s[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs + (2 * i < r.gs ? 0u : kOob), 4 * i, 0);
-    if (kind == 1) {
-        const uint32_t z0 = __builtin_amdgcn_raw_buffer_load_b16(rz, vz, 0, 0);
-        const uint32_t z1 = __builtin_amdgcn_raw_buffer_load_b16(rz, vz + (2 < r.gs ? 0u : kOob), 2, 0);
-        b.z = z0 | (z1 << 16);
-    } else {
-        b.z = 0;
-    }
-}
-
-// Sum over the slice of codes x converted activations for the lane's row
-// (lanes 0..15 hold rows row0 + ln; other lanes' values are unused).
-__device__ __forceinline__ float slice_sum(const SliceRegs& b, const SliceRef& r, int kind, const int8_t* xs,
-                                           const int4* ms, int ln, int kg) {
-    float acc = 0.0f;
-    const bool alive = ln < 3;  // A rows 0..2 carry limbs 0..2
-#pragma unroll
-    for (int gl = 0; gl < 4; gl++) {
-        if (kind != 1 && gl >= 2) break;
-        if (gl >= r.gs) break;  // wave-uniform
-        const int g = r.g0 + gl;
-        int4v_t a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-        if (alive) {
-            const int8_t* pa = xs + g * kLimbRec + ln * kGroup + kg * 16;
-            a0 = *reinterpret_cast<const int4v_t*>(pa);
-            a1 = *reinterpret_cast<const int4v_t*>(pa + 64);
-        }
-        int4v_t b0, b1;
-        if (kind == 1) {
-            const int4v_t v = b.w[gl];
-            b0 = v & 0x0F0F0F0F;
-            b1 = (v >> 4) & 0x0F0F0F0F;
-        } else {
-            b0 = b.w[(2 * gl) & 3];
-            b1 = b.w[(2 * gl + 1) & 3];
-        }
-        int4v_t D = mfma_i8(a0, b0, int4v_t{0, 0, 0, 0});
-        D = mfma_i8(a1, b1, D);
-        const uint32_t sw = b.s[gl >> 1];
-        const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
-        const int z = kind == 1 ? int((b.z >> (8 * gl)) & 0xFF) : 0;
-        acc = combine(acc, D[0], D[1], D[2], z, ms[g], sc);
-    }
-    return acc;
-}
-
-// Columns [k0, k0 + 8) of the stage input, before normalisation.
+// Columns [k0, k0 + 8) of the stage input (IQ_IN_GQA: the value row of the
+// query head's key/value head).
 __device__ __forceinline__ void load_input8(const CStage& st, int k0, float (&v)[8]) {
     const float* src = st.x + k0;
-    if (st.in_op == IQ_IN_GQA) {
-        // query-head column k0 reads the value row of its key/value head
-        const int span = st.gqa_span, hd = st.gqa_hd;
-        src = st.x + (k0 / span) * hd + (k0 % hd);
-    }
+    if (st.in_op == IQ_IN_GQA) src = st.x + (k0 / st.gqa_span) * st.gqa_hd + (k0 % st.gqa_hd);
     const float4 a = *reinterpret_cast<const float4*>(src);
     const float4 c = *reinterpret_cast<const float4*>(src + 4);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
 }
 
-// Full-wave sum of a double, every lane gets the total (fixed order).
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 
-__global__ __launch_bounds__(64 * kWaves) void chain_kernel(const CParams P) {
+// Sum over the 16 lanes of a DPP row (every lane of the row active).
+__device__ __forceinline__ float row16_fsum(float v) {
+    v += __int_as_float(row_ror<8>(__float_as_int(v)));
+    v += __int_as_float(row_ror<4>(__float_as_int(v)));
+    v += __int_as_float(row_ror<2>(__float_as_int(v)));
+    v += __int_as_float(row_ror<1>(__float_as_int(v)));
+    return v;
+}
+
+// Workgroup = ks waves on one unit: TP = 1 one 16-row tile, TP = 2 the gate
+// and up tiles of the same rows (each wave holds both tiles' weights of its
+// slice and multiplies both by the same activation operand).  Wave w owns
+// the K slice [w gs, w gs + gs).  NG = slice capacity in groups (a multiple
+// of 4).  Dynamic LDS: limb records [G][384] | meta [G] int4 | (RMSNorm
+// without producer partials) the raw input [K] fp32.
+template <int KIND, int NG, int TP, int NORM>
+__global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void stage_kernel(const CStage st) {
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
-    __shared__ double ssq[kWaves];
+    __shared__ float red[kMaxWaves][TP][16];
+    __shared__ double ssq[kMaxWaves];
+    __shared__ int arrived;
+    constexpr int WPG = KIND == 1 ? 1 : 2;  // 16-byte weight loads per group
+    constexpr int XP = NG / 4;              // conversion passes (4 groups each)
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wg = blockIdx.x, W = gridDim.x;
-    // LDS: limb records [G][384] | meta [G] int4 | slice sums [slots][16]
-    int8_t* xs = lds;
+    const int nw = int(blockDim.x) >> 6;
+    const int G = st.G, K = st.K;
+    const int g0 = wave * st.gs < G ? wave * st.gs : G;
+    const int gs = (g0 + st.gs < G ? g0 + st.gs : G) - g0;
+    int4* ms = reinterpret_cast<int4*>(lds + G * kLimbRec);
+    float* xraw = reinterpret_cast<float*>(lds + G * (kLimbRec + 16));
 
-    SliceRegs B0, B1;
+    // the unit's tiles and their matrices
+    const int u = blockIdx.x;
+    int m0 = 0, tile = u;
+    if (TP == 1) {
+        if (st.nmat > 1 && u >= st.mat[1].tile0) m0 = 1;
+        if (st.nmat > 2 && u >= st.mat[2].tile0) m0 = 2;
+        m0 = __builtin_amdgcn_readfirstlane(m0);
+        tile = u - stage_mat(st, m0).tile0;
+    }
+    CMat Ms[TP];
+    Ms[0] = stage_mat(st, m0);
+    if (TP == 2) Ms[TP - 1] = st.mat[1];
+    const int64_t row0 = int64_t(tile) * 16, N = Ms[0].N;
+
+    // 1. Activations first (the vector L1 returns data in request order),
+    //    then bias / residual, scales, zero points and weights.  Every load
+    //    is a buffer load whose out-of-range offset reads zero, and no loaded
+    //    value is used before all loads are issued (a use waits for every
+    //    load issued before it).
+    // NORM: 0 no RMSNorm; 1 from the producer's per-tile sums of squares
+    // (<= 256 tiles: one 16-byte load per lane); 2 from the whole input
+    constexpr bool norm = NORM != 0;
+    constexpr bool full = NORM == 2;
+    constexpr int kMaxChunks = NORM == 2 ? 4 : 1;  // 16-byte chunks per thread
+    const int xlen = st.in_op == IQ_IN_GQA ? K / (st.gqa_span / st.gqa_hd) : K;
+    const rsrc_t rx = make_rsrc(st.x, int64_t(xlen) * 4);
+    u32x4_t xc[kMaxChunks], xw[XP][2], nwv[norm ? XP : 1];
+    if constexpr (full) {
+        const int nchunk = K / 4, nthr = nw * 64;
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; i++) {
+            const int c = tid + i * nthr;
+            xc[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, c < nchunk ? uint32_t(c) * 16 : kOob, 0, 0));
+        }
+    } else {
+        if constexpr (norm) {
+            // the producer's per-tile sums of squares, 4 per lane
+            const rsrc_t rp = make_rsrc(st.ssq_in, int64_t(st.ssq_n) * 4);
+            xc[0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(lane) * 16, 0, 0));
+        }
+#pragma unroll
+        for (int t = 0; t < XP; t++) {
+            const int g = g0 + 4 * t + kg;
+            int k0 = g * kGroup + ln * 8;
+            if (st.in_op == IQ_IN_GQA) k0 = (k0 / st.gqa_span) * st.gqa_hd + (k0 % st.gqa_hd);
+            const uint32_t off = 4 * t + kg < gs ? uint32_t(k0) * 4 : kOob;
+            xw[t][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+            xw[t][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 16, 0));
+        }
+    }
+    if constexpr (norm) {
+        const rsrc_t rn = make_rsrc(st.norm, int64_t(K) * 2);
+#pragma unroll
+        for (int t = 0; t < XP; t++) {
+            const int g = g0 + 4 * t + kg;
+            nwv[t] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rn, 4 * t + kg < gs ? uint32_t(g * kGroup + ln * 8) * 2 : kOob, 0, 0));
+        }
+    }
+    // bias (and residual) of the rows this lane may store (lanes 0..15 of
+    // every wave: the last wave to finish stores); rows past N read zero
+    uint32_t addb[TP], resb = 0;
     {
-        const CStage& st = P.st[0];
-        load_slice(B0, st, slice_ref(st, wg, W, wave), ln, kg);
+        const uint32_t ro = lane < 16 ? uint32_t(row0 + ln) : 0x20000000u;
+#pragma unroll
+        for (int t = 0; t < TP; t++) {
+            const rsrc_t rb = make_rsrc(Ms[t].bias, Ms[t].bias ? N * 2 : 0);
+            addb[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, ro * 2, 0, 0);
+        }
+        if (TP == 1 && st.out_op == IQ_OUT_RESIDUAL) {
+            const rsrc_t rr = make_rsrc(st.res, N * 4);
+            resb = __builtin_amdgcn_raw_buffer_load_b32(rr, ro * 4, 0, 0);
+        }
     }
-    for (int s = 0; s < P.nst; s++) {
-        const CStage& st = P.st[s];
-        const int G = st.G;
-        int4* ms = reinterpret_cast<int4*>(lds + G * kLimbRec);
-        float* red = reinterpret_cast<float*>(lds + G * (kLimbRec + 16));
-        if (s > 0) {
-            // every workgroup has stored its outputs of stages < s
-            if (tid == 0) {
-                const int target = W * s;
-                int n = 0;
-                while (__hip_atomic_load(P.bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-                    if (++n > P.spin_limit) {
-                        __hip_atomic_store(P.bar + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
-                }
-            }
-            __syncthreads();
-        }
+    if (tid == 0) arrived = 0;
+    // Every wave's activation requests go out before any wave's weight
+    // requests (the barrier waits for no load); this also publishes the
+    // cleared arrival counter before any wave can arrive.
+    __syncthreads();
 
-        // 1. The stage input into limb records: pass t, wave w, lane row kg
-        //    converts group 64 t + 4 w + kg (16 lanes x 8 columns).
-        {
-            const bool perm = st.kind == 1;
-            float v[kMaxPasses][8];
-            double part = 0.0;
+    const int64_t rb = KIND == 1 ? K / 2 : K;
+    const int64_t rows = N - row0 < 16 ? N - row0 : 16;
+    uint32_t sw[TP][NG / 2], zw[TP][NG / 2];
+    int4v_t w[TP][NG][WPG];
 #pragma unroll
-            for (int t = 0; t < kMaxPasses; t++) {
-                const int g = 64 * t + 4 * wave + kg;
+    for (int t = 0; t < TP; t++) {
+        const rsrc_t rs = make_rsrc(Ms[t].scales + row0 * G, rows * G * 2);
+        const rsrc_t rz = make_rsrc(KIND == 1 ? Ms[t].zeros + row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+        const uint32_t vs = uint32_t((ln * G + g0) * 2), vz = uint32_t(ln * G + g0);
+        if (G % 4 == 0) {
+            // slices start on 4-group boundaries: one 8-byte scale load and
+            // one 4-byte zero-point load per 4 groups
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[t][i] = 0.0f;
-                if (64 * t + 4 * wave < G) {  // wave-uniform
-                    if (g < G) load_input8(st, g * kGroup + ln * 8, v[t]);
-#pragma unroll
-                    for (int i = 0; i < 8; i++) part += double(v[t][i]) * double(v[t][i]);
-                }
+            for (int i = 0; i < NG / 4; i++) {
+                const uint32_t ok = 4 * i < gs ? 0u : kOob;
+                const auto sv = __builtin_amdgcn_raw_buffer_load_b64(rs, vs + ok, 8 * i, 0);
+                sw[t][2 * i] = sv[0];
+                sw[t][2 * i + 1] = sv[1];
+                zw[t][2 * i] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b32(rz, vz + ok, 4 * i, 0) : 0u;
             }
-            if (st.in_op == IQ_IN_RMSNORM) {
-                // x / sqrt(mean(x^2) + eps) * w   (src/forward.cpp:21-31)
-                part = wave_sum(part);
-                if (lane == 0) ssq[wave] = part;
-                __syncthreads();
-                double ss = 0.0;
+        } else {
 #pragma unroll
-                for (int w = 0; w < kWaves; w++) ss += ssq[w];
-                const float scale = 1.0f / __builtin_sqrtf(float(ss / double(st.K)) + st.eps);
-#pragma unroll
-                for (int t = 0; t < kMaxPasses; t++) {
-                    const int g = 64 * t + 4 * wave + kg;
-                    if (64 * t + 4 * wave < G && g < G) {
-                        const uint4 nb = *reinterpret_cast<const uint4*>(st.norm + g * kGroup + ln * 8);
-                        const uint32_t nw[4] = {nb.x, nb.y, nb.z, nb.w};
-#pragma unroll
-                        for (int i = 0; i < 8; i++) {
-                            const float w = __uint_as_float((i & 1) ? (nw[i >> 1] & 0xFFFF0000u) : (nw[i >> 1] << 16));
-                            v[t][i] = (v[t][i] * scale) * w;
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < kMaxPasses; t++) {
-                const int g = 64 * t + 4 * wave + kg;
-                if (64 * t + 4 * wave >= G) break;  // wave-uniform
-                const bool ok = g < G;
-                int4 md;
-                if (perm) md = convert_group<true>(v[t], ln, ok, xs + (ok ? g : 0) * kLimbRec);
-                else md = convert_group<false>(v[t], ln, ok, xs + (ok ? g : 0) * kLimbRec);
-                if (ok && ln == 0) ms[g] = md;
+            for (int i = 0; i < NG / 2; i++) {
+                const uint32_t ok = 2 * i < gs ? 0u : kOob;
+                sw[t][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs + ok, 4 * i, 0);
+                zw[t][i] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b16(rz, vz + ok, 2 * i, 0) : 0u;
             }
         }
+    }
+#pragma unroll
+    for (int t = 0; t < TP; t++) {
+        const rsrc_t rq = make_rsrc(Ms[t].q + row0 * rb, rows * rb);
+        const uint32_t vq = uint32_t(ln * rb) + uint32_t(g0 * (KIND == 1 ? 64 : 128) + kg * 16);
+#pragma unroll
+        for (int gl = 0; gl < NG; gl++)
+#pragma unroll
+            for (int h = 0; h < WPG; h++)
+                w[t][gl][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                              rq, vq + (gl < gs ? 0u : kOob), KIND == 1 ? gl * 64 : gl * 128 + h * 64, 0));
+    }
+
+    // 2. The slice's activations.  RMSNorm (src/forward.cpp:21-31):
+    //    x / sqrt(mean(x^2) + eps) * w, the sum of squares in double in a
+    //    fixed order: from the producer's per-tile sums (every wave adds
+    //    them itself), or from the whole input (reduced through LDS, the raw
+    //    input kept in LDS for the slices).
+    float xv[XP][8];
+    float scale = 1.0f;
+    if constexpr (full) {
+        double part = 0.0;
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const double v = double(__uint_as_float(xc[i][j]));
+                part += v * v;
+            }
+        const int nchunk = K / 4, nthr = nw * 64;
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; i++) {
+            const int c = tid + i * nthr;
+            if (c < nchunk) reinterpret_cast<u32x4_t*>(xraw)[c] = xc[i];
+        }
+        part = wave_sum(part);
+        if (lane == 0) ssq[wave] = part;
         __syncthreads();
-
-        // 2. This workgroup's slices, 16 at a time, the next one's weights
-        //    in flight while the current one is multiplied.
-        const int nsl = units_of(st, wg, W) * st.tpu * st.chunks;
-        const int nit = (nsl + kWaves - 1) / kWaves;
-        for (int it = 0; it < nit; it += 2) {
-            const SliceRef r0 = slice_ref(st, wg, W, it * kWaves + wave);
-            const SliceRef r1 = slice_ref(st, wg, W, (it + 1) * kWaves + wave);
-            if (it + 1 < nit) load_slice(B1, st, r1, ln, kg);
-            if (r0.valid) {
-                const float a = slice_sum(B0, r0, st.kind, xs, ms, ln, kg);
-                if (lane < 16) red[r0.slot * 16 + ln] = a;
-            }
-            if (it + 1 >= nit) break;
-            if (it + 2 < nit) load_slice(B0, st, slice_ref(st, wg, W, (it + 2) * kWaves + wave), ln, kg);
-            if (r1.valid) {
-                const float a = slice_sum(B1, r1, st.kind, xs, ms, ln, kg);
-                if (lane < 16) red[r1.slot * 16 + ln] = a;
-            }
-        }
-        __syncthreads();
-
-        // 3. Per unit: slice sums in slice order, the epilogue, write-through
-        //    stores (wave j % 16 finalises unit j, lanes 0..15 its rows).
-        const int nu = units_of(st, wg, W);
-        for (int j = wave; j < nu; j += kWaves) {
-            if (lane >= 16) continue;
-            const int u = wg + j * W;
-            float acc[2] = {0.0f, 0.0f};
+        double ss = 0.0;
+        for (int i = 0; i < nw; i++) ss += ssq[i];
+        scale = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
 #pragma unroll
-            for (int p = 0; p < 2; p++) {
-                if (p >= st.tpu) break;
-                const float* rp = red + ((j * st.tpu + p) * st.chunks) * 16 + ln;
-                float sum = 0.0f;
-                for (int c = 0; c < st.chunks; c++) sum += rp[c * 16];
-                acc[p] = sum;
-            }
-            int m = 0, tile = u;
-            if (st.tpu == 1) {
-                for (int i = 1; i < kMaxStageMats; i++)
-                    if (i < st.nmat && u >= st.mat[i].tile0) m = i;
-                tile = u - st.mat[m].tile0;
-            }
-            const CMat& M = st.mat[m];
-            const int64_t row = int64_t(tile) * 16 + ln;
-            if (row >= M.N) continue;
-            float out;
-            if (st.out_op == IQ_OUT_SWIGLU) {
-                // silu(g) * u  (kernels/ops/elementwise.cu:6-11)
-                const float g = acc[0] + (st.mat[0].bias ? bf16_to_f32(st.mat[0].bias[row]) : 0.0f);
-                const float up = acc[1] + (st.mat[1].bias ? bf16_to_f32(st.mat[1].bias[row]) : 0.0f);
-                out = g / (1.0f + expf(-g)) * up;
+        for (int t = 0; t < XP; t++) {
+            if (4 * t >= gs) continue;
+            const int g = 4 * t + kg < gs ? g0 + 4 * t + kg : g0;
+            const u32x4_t a = reinterpret_cast<const u32x4_t*>(xraw + g * kGroup + ln * 8)[0];
+            const u32x4_t c = reinterpret_cast<const u32x4_t*>(xraw + g * kGroup + ln * 8)[1];
+            xw[t][0] = a;
+            xw[t][1] = c;
+        }
+    } else if constexpr (norm) {
+        double part = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) part += double(__uint_as_float(xc[0][j]));
+        const double ss = wave_sum(part);
+        scale = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
+    }
+#pragma unroll
+    for (int t = 0; t < XP; t++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float r = __uint_as_float(xw[t][i >> 2][i & 3]);
+            if constexpr (norm) {
+                const uint32_t nv = nwv[t][i >> 1];
+                const float wn = __uint_as_float((i & 1) ? (nv & 0xFFFF0000u) : (nv << 16));
+                xv[t][i] = (r * scale) * wn;
             } else {
-                out = acc[0] + (M.bias ? bf16_to_f32(M.bias[row]) : 0.0f);
-                if (st.out_op == IQ_OUT_RESIDUAL) out = st.res[row] + out;
+                xv[t][i] = r;
             }
-            __hip_atomic_store(M.y + row, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        // stores complete (written through) before this workgroup arrives;
-        // only then the next stage's first weights are requested
-        __builtin_amdgcn_s_waitcnt(0);
-        if (s + 1 < P.nst) {
-            const CStage& nx = P.st[s + 1];
-            load_slice(B0, nx, slice_ref(nx, wg, W, wave), ln, kg);
+
+    // 3. This wave's slice into limb records.
+#pragma unroll
+    for (int t = 0; t < XP; t++) {
+        if (4 * t >= gs) continue;  // wave-uniform
+        const int g = g0 + 4 * t + kg;
+        const bool ok = 4 * t + kg < gs;
+        const int4 md = convert_group<KIND == 1>(xv[t], ln, ok, lds + (ok ? g : g0) * kLimbRec);
+        if (ok && ln == 0) ms[g] = md;
+    }
+
+    // 4. Codes x limbs: A rows 0..2 = limbs 0..2 (lanes 0..15 hold the three
+    //    sums of row ln in D[0..2]); the wave reads only its own records.
+    //    (Fully unrolled with a wave-uniform guard: a loop the compiler does
+    //    not unroll indexes the weight registers dynamically, which moves
+    //    them to scratch memory.)
+    float acc[TP];
+#pragma unroll
+    for (int t = 0; t < TP; t++) acc[t] = 0.0f;
+    const bool alive = ln < 3;
+#pragma unroll
+    for (int gl = 0; gl < NG; gl++) {
+        if (gl >= gs) continue;  // wave-uniform
+        const int g = g0 + gl;
+        int4v_t a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+        if (alive) {
+            const int8_t* pa = lds + g * kLimbRec + ln * kGroup + kg * 16;
+            a0 = *reinterpret_cast<const int4v_t*>(pa);
+            a1 = *reinterpret_cast<const int4v_t*>(pa + 64);
         }
-        __syncthreads();
-        if (tid == 0 && s + 1 < P.nst) __hip_atomic_fetch_add(P.bar, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int4 md = ms[g];
+#pragma unroll
+        for (int t = 0; t < TP; t++) {
+            int4v_t b0, b1;
+            if (KIND == 1) {
+                b0 = w[t][gl][0] & 0x0F0F0F0F;
+                b1 = (w[t][gl][0] >> 4) & 0x0F0F0F0F;
+            } else {
+                b0 = w[t][gl][0];
+                b1 = w[t][gl][WPG - 1];
+            }
+            int4v_t D = mfma_i8(a0, b0, int4v_t{0, 0, 0, 0});
+            D = mfma_i8(a1, b1, D);
+            const uint32_t s2 = sw[t][gl >> 1];
+            const float sc = __uint_as_float((gl & 1) ? (s2 & 0xFFFF0000u) : (s2 << 16));
+            const int z = KIND != 1 ? 0
+                          : (G % 4 == 0 ? int((zw[t][(gl >> 2) * 2] >> (8 * (gl & 3))) & 0xFF)
+                                        : int((zw[t][gl >> 1] >> (8 * (gl & 1))) & 0xFF));
+            acc[t] = combine(acc[t], D[0], D[1], D[2], z, md, sc);
+        }
+    }
+
+    // 5. Partials through LDS; the last wave adds them in wave order and
+    //    applies the epilogue (and the per-tile sum of squares of the output
+    //    for a consumer's RMSNorm).
+    if (lane < 16) {
+#pragma unroll
+        for (int t = 0; t < TP; t++) red[wave][t][ln] = acc[t];
+    }
+    int prior = 0;
+    if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    prior = __builtin_amdgcn_readfirstlane(prior);
+    if (prior != nw - 1 || lane >= 16) return;
+    float sum[TP];
+#pragma unroll
+    for (int t = 0; t < TP; t++) {
+        sum[t] = 0.0f;
+        for (int i = 0; i < nw; i++) sum[t] += red[i][t][ln];
+    }
+    const int64_t row = row0 + ln;
+    float v = sum[0] + __uint_as_float(addb[0] << 16);
+    if (TP == 2) {
+        // silu(g) * u  (kernels/ops/elementwise.cu:6-11)
+        const float up = sum[TP - 1] + __uint_as_float(addb[TP - 1] << 16);
+        v = v / (1.0f + expf(-v)) * up;
+    } else if (st.out_op == IQ_OUT_RESIDUAL) {
+        v = __uint_as_float(resb) + v;
+    }
+    if (row < N) Ms[0].y[row] = v;
+    if (st.ssq_out) {
+        const float sq = row16_fsum(row < N ? v * v : 0.0f);
+        if (ln == 0) st.ssq_out[tile] = sq;
     }
 }
 
-__global__ void chain_reset_kernel(int* bar) {
-    if (threadIdx.x < 2) bar[threadIdx.x] = 0;
+template <int KIND>
+hipError_t launch_stage_k(const HostStage& h, hipStream_t stream) {
+    const dim3 grid(unsigned(h.st.units)), block(unsigned(64 * h.st.ks));
+    const int norm = h.st.in_op != IQ_IN_RMSNORM ? 0 : (h.st.ssq_in ? 1 : 2);
+#define IQ_STAGE(NG_, TP_)                                                                  \
+    do {                                                                                    \
+        if (norm == 1) stage_kernel<KIND, NG_, TP_, 1><<<grid, block, h.lds, stream>>>(h.st); \
+        else if (norm == 2) stage_kernel<KIND, NG_, TP_, 2><<<grid, block, h.lds, stream>>>(h.st); \
+        else stage_kernel<KIND, NG_, TP_, 0><<<grid, block, h.lds, stream>>>(h.st);         \
+    } while (0)
+    if (h.st.tpu == 2) {
+        if (h.ng == 4) IQ_STAGE(4, 2);
+        else IQ_STAGE(8, 2);
+    } else {
+        switch (h.ng) {
+            case 4: IQ_STAGE(4, 1); break;
+            case 8: IQ_STAGE(8, 1); break;
+            case 12: IQ_STAGE(12, 1); break;
+            default:
+                if constexpr (KIND == 0) IQ_STAGE(20, 1);
+                break;
+        }
+    }
+#undef IQ_STAGE
+    return hipGetLastError();
 }
-
-}  // namespace
-
-// Host side of a chain: the validated program on the device.
-struct Chain {
-    int device = 0;
-    int nst = 0;
-    int W = 0;
-    size_t lds = 0;
-    CStage* d_st = nullptr;
-    int* d_bar = nullptr;
-};
-
-namespace {
 
 struct Range {
     uintptr_t lo, hi;
@@ -418,17 +440,22 @@ bool overlaps(const Range& a, const Range& b) { return a.lo < b.hi && b.lo < a.h
 
 }  // namespace
 
+// Host side of a chain: the validated stages and their launch shapes.
+struct Chain {
+    int device = 0;
+    std::vector<HostStage> stages;
+    float* partials = nullptr;  // per-tile sums of squares passed between stages
+};
+
 int chain_create(const iq_stage* stages, int n, Chain** out) {
     if (!stages || !out) return IQ_ENULL;
     *out = nullptr;
     if (n < 1) return IQ_ESHAPE;
-    std::vector<CStage> prog(static_cast<size_t>(n));
-    std::vector<std::vector<Range>> reads(static_cast<size_t>(n)), writes(static_cast<size_t>(n));
-    size_t lds_max = 0;
-    const int cus = device_cu_count();
+    std::vector<HostStage> prog(static_cast<size_t>(n));
     for (int s = 0; s < n; s++) {
         const iq_stage& a = stages[s];
-        CStage& c = prog[size_t(s)];
+        HostStage& hs = prog[size_t(s)];
+        CStage& c = hs.st;
         std::memset(&c, 0, sizeof(c));
         if (a.n < 1 || a.n > kMaxStageMats) return IQ_ESHAPE;
         if (a.in_op < IQ_IN_PLAIN || a.in_op > IQ_IN_GQA) return IQ_ESHAPE;
@@ -436,9 +463,8 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         const iq_view& W0 = a.W[0];
         if (W0.kind != IQ_INT8 && W0.kind != IQ_INT4) return IQ_EKIND;
         const int64_t K = W0.cols, G = (K + kGroup - 1) / kGroup;
-        // whole groups, an even group count (paired scale loads), at most
-        // three conversion passes
-        if (K <= 0 || K % (2 * kGroup) || G > 64 * kMaxPasses) return IQ_ESHAPE;
+        // whole groups and an even group count (paired scale loads)
+        if (K <= 0 || K % (2 * kGroup)) return IQ_ESHAPE;
         int tiles = 0;
         for (int i = 0; i < a.n; i++) {
             const iq_view& Wi = a.W[i];
@@ -446,19 +472,19 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
             if (Wi.cols != K || Wi.groups != G || Wi.rows <= 0 || Wi.rows > (int64_t(1) << 30)) return IQ_ESHAPE;
             if (!Wi.q || !Wi.scales || (Wi.kind == IQ_INT4 && !Wi.zeros)) return IQ_ENULL;
             const int64_t rb = Wi.kind == IQ_INT4 ? K / 2 : K;
-            if (Wi.rows * rb >= (int64_t(1) << 31)) return IQ_ETOOLARGE;
+            if (16 * rb >= (int64_t(1) << 31)) return IQ_ETOOLARGE;
             c.mat[i] = CMat{Wi.q, Wi.scales, Wi.kind == IQ_INT4 ? Wi.zeros : nullptr, a.bias[i], a.y[i],
                             int32_t(Wi.rows), tiles};
             tiles += int((Wi.rows + 15) / 16);
         }
         const bool pair = a.out_op == IQ_OUT_SWIGLU;
         if (pair && (a.n != 2 || a.W[1].rows != W0.rows)) return IQ_ESHAPE;
+        if (a.out_op == IQ_OUT_RESIDUAL && a.n != 1) return IQ_ESHAPE;
+        std::vector<Range> reads, writes;
         const int nout = pair ? 1 : a.n;
         for (int i = 0; i < nout; i++) {
             if (!a.y[i]) return IQ_ENULL;
-            if (reinterpret_cast<uintptr_t>(a.y[i]) % 4) return IQ_ESHAPE;
-            writes[size_t(s)].push_back({reinterpret_cast<uintptr_t>(a.y[i]),
-                                         reinterpret_cast<uintptr_t>(a.y[i] + a.W[i].rows)});
+            writes.push_back({reinterpret_cast<uintptr_t>(a.y[i]), reinterpret_cast<uintptr_t>(a.y[i] + a.W[i].rows)});
         }
         if (!a.x) return IQ_ENULL;
         if (reinterpret_cast<uintptr_t>(a.x) % 16) return IQ_ESHAPE;
@@ -470,23 +496,30 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
             c.gqa_span = int32_t(hd * grp);
             xlen = K / grp;
         }
-        reads[size_t(s)].push_back({reinterpret_cast<uintptr_t>(a.x), reinterpret_cast<uintptr_t>(a.x + xlen)});
+        reads.push_back({reinterpret_cast<uintptr_t>(a.x), reinterpret_cast<uintptr_t>(a.x + xlen)});
         if (a.in_op == IQ_IN_RMSNORM) {
             if (!a.norm) return IQ_ENULL;
             if (reinterpret_cast<uintptr_t>(a.norm) % 16) return IQ_ESHAPE;
             if (!(a.eps >= 0.0f)) return IQ_ESHAPE;
+            if (K > 16384) return IQ_ETOOLARGE;  // the raw input is kept in LDS
         }
         if (a.out_op == IQ_OUT_RESIDUAL) {
             if (!a.residual) return IQ_ENULL;
-            reads[size_t(s)].push_back({reinterpret_cast<uintptr_t>(a.residual),
-                                        reinterpret_cast<uintptr_t>(a.residual + W0.rows)});
-            if (a.n != 1) return IQ_ESHAPE;
+            reads.push_back({reinterpret_cast<uintptr_t>(a.residual),
+                             reinterpret_cast<uintptr_t>(a.residual + W0.rows)});
+        }
+        // a stage's workgroups read its inputs while others store: no output
+        // may overlap an input or another output of the same stage
+        for (size_t i = 0; i < writes.size(); i++) {
+            for (const Range& r : reads)
+                if (overlaps(writes[i], r)) return IQ_EALIAS;
+            for (size_t j = 0; j < i; j++)
+                if (overlaps(writes[i], writes[j])) return IQ_EALIAS;
         }
         c.x = a.x;
         c.norm = a.norm;
         c.res = a.residual;
         c.eps = a.eps;
-        c.kind = W0.kind;
         c.in_op = a.in_op;
         c.out_op = a.out_op;
         c.nmat = a.n;
@@ -494,75 +527,89 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         c.G = int32_t(G);
         c.tpu = pair ? 2 : 1;
         c.units = pair ? int((W0.rows + 15) / 16) : tiles;
-        c.gsl = W0.kind == IQ_INT4 ? 4 : 2;
-        c.chunks = int((G + c.gsl - 1) / c.gsl);
-        const int64_t per_wg = (c.units + cus - 1) / cus;
-        const size_t lds = size_t(G) * (kLimbRec + 16) + size_t(per_wg) * c.tpu * c.chunks * 16 * sizeof(float);
-        lds_max = std::max(lds_max, lds);
+        // slices of whole 4-group blocks (measured: fewer, fatter waves beat
+        // more waves with 2 groups each), at most 16 waves of <= 12 groups
+        // (int4) or 8 waves of <= 20 groups (int8: twice the weight
+        // registers per group); a SwiGLU pair holds two tiles per wave
+        const bool i4 = W0.kind == IQ_INT4;
+        const int maxw = i4 ? kMaxWaves : kMaxWaves / 2;
+        int gs = int((G + maxw - 1) / maxw);
+        gs = (gs + 3) & ~3;
+        if (gs > (pair ? 8 : (i4 ? 12 : 20))) return IQ_ETOOLARGE;
+        c.gs = gs;
+        c.ks = int((G + gs - 1) / gs);
+        hs.kind = W0.kind;
+        hs.ng = gs;
+        // RMSNorm from the whole input: at most four 16-byte chunks per thread
+        if (a.in_op == IQ_IN_RMSNORM && K > 16 * 64 * int64_t(c.ks)) return IQ_ETOOLARGE;
+        hs.lds = size_t(G) * (kLimbRec + 16) + (a.in_op == IQ_IN_RMSNORM ? size_t(K) * 4 : 0);
+        if (hs.lds > 160 * 1024) return IQ_ETOOLARGE;
     }
-    // Single assignment: a stage writes nothing that it or an earlier stage
-    // reads or writes (a rewritten line could be stale in another XCD's L2).
-    for (int s = 0; s < n; s++)
-        for (const Range& w : writes[size_t(s)])
-            for (int e = 0; e <= s; e++) {
-                for (const Range& r : reads[size_t(e)])
-                    if (overlaps(w, r)) return IQ_EALIAS;
-                for (const Range& o : writes[size_t(e)])
-                    if ((e < s || &o != &w) && overlaps(w, o)) return IQ_EALIAS;
+    // (a consumer takes the producer's partial sums only when they fit one
+    // 16-byte load per lane: <= 256 tiles, K <= 4096)
+    // RMSNorm inputs produced by an earlier stage of the chain: that stage
+    // also writes per-tile sums of squares, so the consumer's workgroups
+    // need not read the whole vector (unless a stage in between rewrites it)
+    std::vector<std::pair<int, int>> links;  // (producer, consumer)
+    for (int s = 0; s < n; s++) {
+        if (stages[s].in_op != IQ_IN_RMSNORM) continue;
+        const float* x = stages[s].x;
+        const int64_t K = stages[s].W[0].cols;
+        for (int e = s - 1; e >= 0; e--) {
+            const iq_stage& a = stages[e];
+            const int nout = a.out_op == IQ_OUT_SWIGLU ? 1 : a.n;
+            bool hit = false, clash = false;
+            for (int i = 0; i < nout; i++) {
+                const Range w{reinterpret_cast<uintptr_t>(a.y[i]), reinterpret_cast<uintptr_t>(a.y[i] + a.W[i].rows)};
+                if (a.y[i] == x && a.W[i].rows == K && nout == 1 && K <= 4096) hit = true;
+                else if (overlaps(w, Range{reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(x + K)})) clash = true;
             }
-    if (lds_max > 160 * 1024) return IQ_ETOOLARGE;
-
-    Chain* ch = new Chain();
-    hipError_t e = hipGetDevice(&ch->device);
-    int occ = 0;
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(chain_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_max));
-    if (e == hipSuccess)
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(chain_kernel), 64 * kWaves,
-                                                          lds_max);
-    if (e == hipSuccess && occ < 1) e = hipErrorCooperativeLaunchTooLarge;
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ch->d_st), sizeof(CStage) * size_t(n));
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ch->d_bar), 256);
-    if (e == hipSuccess) e = hipMemcpy(ch->d_st, prog.data(), sizeof(CStage) * size_t(n), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(ch->d_bar, 0, 256);
-    if (e != hipSuccess) {
-        chain_destroy(ch);
-        return e == hipErrorOutOfMemory ? IQ_ENOMEM : int(e);
+            if (hit) links.emplace_back(e, s);
+            if (hit || clash) break;
+        }
     }
-    ch->nst = n;
-    ch->W = cus;
-    ch->lds = lds_max;
+    Chain* ch = new Chain();
+    if (hipGetDevice(&ch->device) != hipSuccess) {
+        delete ch;
+        return IQ_EDEVICE;
+    }
+    if (!links.empty()) {
+        // one partial-sum array per producer
+        std::vector<size_t> off(static_cast<size_t>(n), size_t(-1));
+        size_t total = 0;
+        for (const auto& l : links)
+            if (off[size_t(l.first)] == size_t(-1)) {
+                off[size_t(l.first)] = total;
+                total += size_t((prog[size_t(l.first)].st.mat[0].N + 15) / 16 + 63) / 64 * 64;
+            }
+        const hipError_t e = hipMalloc(reinterpret_cast<void**>(&ch->partials), total * sizeof(float));
+        if (e != hipSuccess) {
+            delete ch;
+            return e == hipErrorOutOfMemory ? IQ_ENOMEM : int(e);
+        }
+        for (const auto& l : links) {
+            float* p = ch->partials + off[size_t(l.first)];
+            prog[size_t(l.first)].st.ssq_out = p;
+            prog[size_t(l.second)].st.ssq_in = p;
+            prog[size_t(l.second)].st.ssq_n = (prog[size_t(l.first)].st.mat[0].N + 15) / 16;
+        }
+    }
+    ch->stages = std::move(prog);
     *out = ch;
     return IQ_OK;
 }
 
 hipError_t chain_run(const Chain* ch, hipStream_t stream) {
-    chain_reset_kernel<<<1, 64, 0, stream>>>(ch->d_bar);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    CParams p;
-    p.st = ch->d_st;
-    p.nst = ch->nst;
-    p.bar = ch->d_bar;
-    p.spin_limit = 1 << 22;  // ~0.1-0.5 s of sleeps per barrier
-    void* args[] = {&p};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(chain_kernel), dim3(unsigned(ch->W)),
-                                      dim3(64 * kWaves), args, ch->lds, stream);
-}
-
-int chain_timed_out(const Chain* ch, int* flag) {
-    int v[2] = {0, 0};
-    const hipError_t e = hipMemcpy(v, ch->d_bar, sizeof(v), hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return int(e);
-    *flag = v[1];
-    return IQ_OK;
+    for (const HostStage& h : ch->stages) {
+        const hipError_t e = h.kind == IQ_INT4 ? launch_stage_k<1>(h, stream) : launch_stage_k<0>(h, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 void chain_destroy(Chain* ch) {
     if (!ch) return;
-    if (ch->d_st) (void)hipFree(ch->d_st);
-    if (ch->d_bar) (void)hipFree(ch->d_bar);
+    if (ch->partials) (void)hipFree(ch->partials);
     delete ch;
 }
 
@@ -588,16 +635,6 @@ int iq_chain_run(const iq_chain* chain, void* stream) {
     if (dev != chain->device) return IQ_EDEVICE;
     const hipError_t r = iq::chain_run(chain, static_cast<hipStream_t>(stream));
     return r == hipSuccess ? IQ_OK : int(r);
-}
-
-int iq_chain_status(const iq_chain* chain) {
-    if (!chain) return IQ_ENULL;
-    const hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return int(e);
-    int flag = 0;
-    const int rc = iq::chain_timed_out(chain, &flag);
-    if (rc) return rc;
-    return flag ? IQ_ETIMEOUT : IQ_OK;
 }
 
 void iq_chain_destroy(iq_chain* chain) { iq::chain_destroy(chain); }

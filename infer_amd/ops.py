@@ -78,7 +78,6 @@ SIGNATURES = {
     "iq_quantize": ([_P, _I64, _I64, ctypes.c_int, _P, _P, _P, _P], ctypes.c_int),
     "iq_chain_create": ([ctypes.POINTER(IqStage), ctypes.c_int, ctypes.POINTER(_P)], ctypes.c_int),
     "iq_chain_run": ([_P, _P], ctypes.c_int),
-    "iq_chain_status": ([_P], ctypes.c_int),
     "iq_chain_destroy": ([_P], None),
     "iq_init": ([ctypes.c_int], ctypes.c_int),
     "iq_init_stream": ([ctypes.c_int, _P], ctypes.c_int),
