@@ -25,8 +25,11 @@ Also reported (measured after the timed region, outside it):
              from profiles/gemv_int4_7b_m1_traffic.json (rocprofv3 counters);
   cpu_baseline  the reference CPU path (src/forward.cpp linear over dequant(),
              restated in oracle/iq_oracle.c) on a bounded sample, 1 thread;
-  detail     int4 at 16 rows, the int8 set at 1 and 16 rows, the prefill GEMM
-             (config 5), on-device quantize, configs 1-3.
+  detail     per-shape GB/s of the 1-row launches, int4 at 16 rows, the decode
+             step chained as the engine runs it (norms, attention at position
+             0, SwiGLU, residuals fused into the GEMV stages), the int8 set
+             at 1 and 16 rows, the prefill GEMM (config 5), on-device
+             quantize, configs 1-3.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -189,11 +192,17 @@ def kernel_roofline(torch, step, only_kind=None):
         timing.append((nb, len(gops), e0, e1))
     torch.cuda.synchronize()
     tot_b, tot_ms, n = 0, 0.0, 0
-    for nb, cnt, e0, e1 in timing:
+    per_shape = {}
+    for (nb, cnt, e0, e1), key in zip(timing, [k for k in groups if only_kind is None or k[-1] == only_kind]):
+        ms = e0.elapsed_time(e1)
         tot_b += nb
-        tot_ms += e0.elapsed_time(e1)
+        tot_ms += ms
         n += cnt
-    return tot_b, tot_ms, n
+        name = "|".join(str(r) for r in key[:-2]) + f"x{key[-2]}"
+        per_shape[name] = {"launches": cnt, "avg_us": round(ms * 1e3 / cnt, 2),
+                           "bytes_per_launch": int(nb / cnt), "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+                           "frac_hbm_peak": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return tot_b, tot_ms, n, per_shape
 
 
 def cpu_baseline(torch, model, seconds=10.0, threads=1):
@@ -328,6 +337,44 @@ def bench_gemv_single(torch, ops, kind, N, K, M, copies, reps=200, seed=11):
     return per_ms * 1e3, nb / (per_ms * 1e-3) / 1e9
 
 
+def bench_decode_chain(torch, ops, model, steps, warmup):
+    """The quantised decode step as the reference's engine chains it
+    (kernels/batch_gpu.cu:186-215), one token at position 0: embedding
+    gather, then per layer RMSNorm -> q|k|v, single-key attention -> o +
+    residual, RMSNorm -> gate|up with the SwiGLU epilogue, down + residual,
+    and the final RMSNorm -> lm_head, every stage reading the previous
+    stage's output (infer_amd/chain.py; one launch per stage, captured in a
+    HIP graph).  Same weights as the headline step; random bf16 norm
+    weights and q/k/v biases; the int8 lm_head doubles as the embedding
+    table.  GB/s counts the packed weights read per step."""
+    from infer_amd import chain as C
+    g = torch.Generator(device="cuda").manual_seed(21)
+    nb = lambda n: (torch.rand(n, generator=g, device="cuda") * 0.8 + 0.6).to(torch.bfloat16).view(torch.int16)
+    cfg = dict(hidden=H7, inter=I7, heads=NH7, kv_heads=KV7, head_dim=128, vocab=V7, layers=len(model.layers),
+               eps=1e-6)
+    layers = []
+    for L in model.layers:
+        d = dict(L)
+        d["input_ln"], d["post_ln"] = nb(H7), nb(H7)
+        d["q_b"], d["k_b"], d["v_b"] = nb(NH7 * 128), nb(KV7 * 128), nb(KV7 * 128)
+        layers.append(d)
+    spec = dict(cfg=cfg, layers=layers, embed=model.head, head=model.head, final_norm=nb(H7))
+    step = C.DecodeStep(spec)
+    step.step(1234)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        step.step()
+    ms, _ = time_graph(torch, gr, steps, warmup)
+    wb = step.weight_bytes()
+    out = {"us_per_step": round(ms * 1e3, 1), "GBps": round(wb / (ms * 1e-3) / 1e9, 1),
+           "frac_hbm_peak": round(wb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "launches": len(step.chain.stages) + 1, "weight_bytes": int(wb),
+           "logits_finite": bool(torch.isfinite(step.logits).all().item())}
+    del gr, step
+    return out
+
+
 def profile_workload(torch, ops):
     """Fixed short workload for `rocprofv3 --pmc` runs: 4 layers of the 7B
     int4 set at 1 row (q|k|v, o, gate|up, down launches as in the step), then
@@ -356,6 +403,18 @@ def profile_gemm_workload(torch, ops):
     torch.cuda.synchronize()
 
 
+def profile_quantize_workload(torch, ops):
+    """Fixed short workload for `rocprofv3 --pmc` runs of the on-device
+    quantiser: 18944 x 3584 bf16 -> int8 and int4, 3 launches each."""
+    gq = torch.Generator(device="cuda").manual_seed(3)
+    w = (torch.randn(I7, H7, generator=gq, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+    for kind in (0, 1):
+        out = ops.alloc_quant(kind, I7, H7)
+        for _ in range(3):
+            ops.quantize(w, kind, out=out)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -367,6 +426,8 @@ def main():
                     help="short fixed workload for rocprofv3 counter runs (prints nothing)")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="short fixed prefill-GEMM workload for rocprofv3 counter runs (prints nothing)")
+    ap.add_argument("--profile-quantize", action="store_true",
+                    help="short fixed quantize workload for rocprofv3 counter runs (prints nothing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -382,6 +443,9 @@ def main():
         return
     if args.profile_gemm:
         profile_gemm_workload(torch, ops)
+        return
+    if args.profile_quantize:
+        profile_quantize_workload(torch, ops)
         return
     t_setup = time.perf_counter()
 
@@ -408,7 +472,7 @@ def main():
                   "max_us": round(per[-1], 1)}
 
     # roofline of the dominant kernel (int4 GEMV, 1 row)
-    rb, rms, rn = kernel_roofline(torch, st, only_kind=1)
+    rb, rms, rn, per_shape = kernel_roofline(torch, st, only_kind=1)
     achieved = rb / (rms * 1e-3) / 1e9
     traffic = None
     prof = os.path.join(ROOT, "profiles", "gemv_int4_7b_m1_traffic.json")
@@ -424,7 +488,7 @@ def main():
                 "algorithmic_bytes_per_launch": int(rb / max(rn, 1))}
     del g
 
-    detail = {"7b_int4_m1_step_spread": step_stats}
+    detail = {"7b_int4_m1_step_spread": step_stats, "7b_int4_m1_gemv_per_shape": per_shape}
     cpu = None
     if not args.quick:
         st16 = Step(torch, ops, m4, 16)
@@ -434,6 +498,7 @@ def main():
                                  "GBps": round(st16.bytes / (ms16 * 1e-3) / 1e9, 1),
                                  "ratio_vs_m1": round(ms16 / ms_wall, 3)}
         del g16, st16
+        detail["7b_int4_decode_chain_m1"] = bench_decode_chain(torch, ops, m4, args.steps, args.warmup)
         cpu_gbs, cpu_sample = cpu_baseline(torch, m4, args.cpu_seconds)
         cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": "oracle iqo_linear_q_f32 (src/forward.cpp:35-47 over dequant(), scalar fp32, "
@@ -538,7 +603,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "int4 (int8 lm_head) weights x fp32 activations: exact int32 MFMA sums, fp32 accumulation",
         "data": "synthetic",
         "config": {
             "workload": "Qwen2.5-7B decode linear set, int4 group-128 (bf16 scale, u8 zero) x 28 layers "

@@ -23,7 +23,10 @@
  * this boundary.  The library keeps one workspace (activation operands,
  * split-K partial sums; about 35 MB) per (device, stream) pair, allocated on
  * the first call that needs it: calls on different streams may overlap, and
- * calls on one stream are ordered by the stream.
+ * calls on one stream are ordered by the stream.  A stream under graph
+ * capture cannot allocate: without its own workspace (iq_init_stream before
+ * the capture) it uses the device's null-stream workspace (iq_init), which
+ * it then shares with the null stream.
  */
 #ifndef IQ_H
 #define IQ_H

@@ -105,7 +105,20 @@ hipError_t get_workspace(hipStream_t stream, Workspace** out) {
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_mu);
-    Workspace*& ws = g_ws[std::make_pair(dev, stream)];
+    const auto key = std::make_pair(dev, stream);
+    if (!g_ws.count(key) && stream) {
+        // A stream under graph capture cannot allocate: it uses the device's
+        // null-stream workspace (made by iq_init) unless iq_init_stream gave
+        // it its own before the capture.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+            auto it = g_ws.find(std::make_pair(dev, hipStream_t(nullptr)));
+            if (it == g_ws.end() || !it->second) return hipErrorStreamCaptureUnsupported;
+            *out = it->second;
+            return hipSuccess;
+        }
+    }
+    Workspace*& ws = g_ws[key];
     if (!ws) {
         Workspace* w = new Workspace();
         e = create_workspace(w);

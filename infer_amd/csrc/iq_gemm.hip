@@ -58,10 +58,15 @@ __device__ __forceinline__ uint32_t bf16_pair_int(int a, int b) {
 // NJ: 32-column MFMA tiles per wave along the output features (tile width
 // BN = 64 NJ): 2 for wide matrices, 1 when 128-wide tiles would leave CUs idle.
 // BM: activation rows per tile, 128, or 64 for short T (each wave 32 rows).
+// BM = 256 (bf16 activations): 8 waves (4 x 2), each dequantised weight
+// tile in LDS then feeds twice the MFMAs of a 128-row tile.
 template <int KIND, bool XF32, bool FASTW, bool FASTX, int NJ, int BM>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
+__global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 : 2) void gemm_kernel(const GemmParams p) {
     constexpr int BN = 64 * NJ;
-    constexpr int NI = BM / 64;  // 32-row MFMA tiles per wave along the rows
+    constexpr int NT = BM == 256 ? 2 * kThreads : kThreads;  // threads
+    constexpr int WR = NT / 128;                           // waves along the rows
+    constexpr int WROWS = BM / WR;                         // rows per wave
+    constexpr int NI = WROWS / 32;  // 32-row MFMA tiles per wave along the rows
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t Al[XF32 ? 2 : 1][XF32 ? BM : 1][LDSW];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][LDSW];
@@ -89,8 +94,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     const int64_t range_bytes = KIND == 1 ? (klen + 1) / 2 : klen;
 
     // ---- register staging of one K step
-    constexpr int XCH = XF32 ? BM / 16 : BM / 32;  // 16-byte activation chunks per thread
-    constexpr int WCH = KIND == 1 ? 1 : NJ;     // 16-byte weight chunks per thread
+    constexpr int XCH = BM * (XF32 ? BK / 4 : BK / 8) / NT;  // 16-byte activation chunks per thread
+    constexpr int WCH0 = BN * (KIND == 1 ? 2 : 4) / NT;       // 16-byte weight chunks per thread
+    constexpr int WCH = WCH0 > 0 ? WCH0 : 1;
     struct Regs {
         uint4 xr[XCH];
         uint4 wr[WCH];
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     int wcol[WCH];
 #pragma unroll
     for (int i = 0; i < WCH; i++) {
-        const int c = tid + kThreads * i;
+        const int c = tid + NT * i;
         const int row = KIND == 1 ? c >> 1 : c >> 2;
         const int64_t n = n0 + row;
         wok[i] = row < BN && n < p.N;
@@ -119,7 +125,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
     int xcol[XCH];
 #pragma unroll
     for (int i = 0; i < XCH; i++) {
-        const int c = tid + kThreads * i;
+        const int c = tid + NT * i;
         const int row = XF32 ? c >> 4 : c >> 3;
         const int64_t m = m0 + row;
         xok[i] = m < p.T;
@@ -179,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         const uint32_t zr = rg.zr;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
-            const int c = tid + kThreads * i;
+            const int c = tid + NT * i;
             if (XF32) {
                 const int row = c >> 4, kc = c & 15;
                 const float f[4] = {__uint_as_float(xr[i].x), __uint_as_float(xr[i].y),
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         }
 #pragma unroll
         for (int i = 0; i < WCH; i++) {
-            const int c = tid + kThreads * i;
+            const int c = tid + NT * i;
             const uint32_t d[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
             if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;  // int4 at BN = 64: half the threads
             if (KIND == 1) {
@@ -288,8 +294,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
             bf16x8_t a[NI], al[NI], bw[NJ];
 #pragma unroll
             for (int i = 0; i < NI; i++) {
-                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * (BM / 2) + i * 32 + (lane & 31)][kof]);
-                if (XF32) al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[XF32 ? buf : 0][XF32 ? wm * (BM / 2) + i * 32 + (lane & 31) : 0][kof]);
+                a[i] = *reinterpret_cast<const bf16x8_t*>(&As[buf][wm * WROWS + i * 32 + (lane & 31)][kof]);
+                if (XF32) al[i] = *reinterpret_cast<const bf16x8_t*>(&Al[XF32 ? buf : 0][XF32 ? wm * WROWS + i * 32 + (lane & 31) : 0][kof]);
             }
 #pragma unroll
             for (int j = 0; j < NJ; j++)
@@ -336,7 +342,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmParams p) {
         for (int i = 0; i < NI; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+                const int64_t m = m0 + wm * WROWS + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
                 if (m < p.T) dst[m * p.N + ncol[j]] = acc[i][j][r] + bv;
             }
     }
@@ -356,6 +362,12 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
 template <int KIND, bool XF32, int NJ>
 void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t stream) {
     const unsigned grid = unsigned(p.tiles_m * p.tiles_n * p.splits);
+    if constexpr (!XF32) {
+        if (bm == 256) {  // (fast paths only)
+            gemm_kernel<KIND, XF32, true, true, NJ, 256><<<grid, 2 * kThreads, 0, stream>>>(p);
+            return;
+        }
+    }
     if (bm == 64) gemm_kernel<KIND, XF32, true, true, NJ, 64><<<grid, kThreads, 0, stream>>>(p);  // (fast paths only)
     else if (fastw && fastx) gemm_kernel<KIND, XF32, true, true, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
     else if (fastw) gemm_kernel<KIND, XF32, true, false, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
@@ -422,7 +434,14 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
     // 18944 at T = 64 / 256: 115 / 186 -> 58 / 170 us, but at T = 128 (a
     // narrow matrix, already split over K) 93 -> 103: kept at 128 rows there
     const bool short_t = T <= 64 || (T > 128 && T <= 256) || (T <= 128 && W.rows >= 8192);
-    const int bm = (short_t && fastw && fastx) ? 64 : 128;
+    // 256-row tiles (8 waves) for long bf16 prefills of int4 weights: each
+    // dequantised weight tile (nibble unpack + zero point, the costlier
+    // conversion) feeds twice the MFMAs.  7B at T = 1024: int4 gate|up 255 ->
+    // 221 us, down 327 -> 264 us; int8 gate|up 231 -> 260 us (slower: one
+    // 8-wave workgroup per CU leaves the step barriers uncovered), so int8
+    // keeps 128-row tiles.
+    const bool big = !x_f32 && fastw && fastx && T >= 512 && W.kind == 1;
+    const int bm = (short_t && fastw && fastx) ? 64 : (big ? 256 : 128);
     p.tiles_m = int((T + bm - 1) / bm);
     if (x_f32) {
         if (W.kind == 1) launch_gemm_nj<1, true>(p, fastw, fastx, bm, stream);
