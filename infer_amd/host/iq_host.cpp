@@ -9,6 +9,8 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -276,6 +278,138 @@ QMatrix quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, QKind kind)
     }
     cleanup();
     return m;
+}
+
+// ------------------------------------------------------------------ model quantiser
+namespace {
+
+// Device buffers for one matrix at a time, grown to the largest seen.
+class Staging {
+public:
+    ~Staging() {
+        if (d_) (void)hipFree(d_);
+    }
+    // bf16 input, codes, scales, zero points for a rows x cols matrix
+    void fit(int64_t rows, int64_t cols) {
+        const size_t G = size_t((cols + kGroup - 1) / kGroup);
+        in_ = size_t(rows) * cols * 2;
+        q_ = size_t(rows) * cols;  // int8 upper bound
+        s_ = size_t(rows) * G * 2;
+        z_ = size_t(rows) * G;
+        const size_t need = align(in_) + align(q_) + align(s_) + align(z_);
+        if (need > cap_) {
+            if (d_) (void)hipFree(d_);
+            d_ = nullptr;
+            cap_ = 0;
+            hip_check(hipMalloc(&d_, need), "quantize_model: hipMalloc");
+            cap_ = need;
+        }
+    }
+    uint16_t* in() { return reinterpret_cast<uint16_t*>(base(0)); }
+    uint8_t* q() { return reinterpret_cast<uint8_t*>(base(align(in_))); }
+    uint16_t* s() { return reinterpret_cast<uint16_t*>(base(align(in_) + align(q_))); }
+    uint8_t* z() { return reinterpret_cast<uint8_t*>(base(align(in_) + align(q_) + align(s_))); }
+
+private:
+    static size_t align(size_t v) { return (v + 255) & ~size_t(255); }
+    char* base(size_t off) { return static_cast<char*>(d_) + off; }
+    void* d_ = nullptr;
+    size_t cap_ = 0, in_ = 0, q_ = 0, s_ = 0, z_ = 0;
+};
+
+// Worst |w - dequant(w)| / absmax over the groups of every rows/64-th row
+// (zero-absmax groups skipped): the reference's report of
+// tools/quantize.cpp:35-45, evaluated the same way on the host.
+double sampled_group_error(const uint16_t* w, const QTensor& t) {
+    double worst = 0.0;
+    const int64_t step = std::max<int64_t>(1, t.rows / 64);
+    for (int64_t r = 0; r < t.rows; r += step)
+        for (int64_t g = 0; g < t.groups(); g++) {
+            float amax = 0.0f, err = 0.0f;
+            const int64_t c1 = std::min(t.cols, (g + 1) * kGroup);
+            for (int64_t c = g * kGroup; c < c1; c++) {
+                const float x = bf16_bits_to_f32(w[r * t.cols + c]);
+                amax = std::max(amax, std::fabs(x));
+                err = std::max(err, std::fabs(x - dequant(t, r, c)));
+            }
+            if (amax > 0.0f) worst = std::max(worst, double(err / amax));
+        }
+    return worst;
+}
+
+}  // namespace
+
+QuantizeReport quantize_model(const std::map<std::string, BF16Tensor>& src, const ModelConfig& cfg, QKind kind,
+                              QuantWriter& w) {
+    if (kind != QKind::kInt8 && kind != QKind::kInt4) throw std::runtime_error("quantize_model: kind must be int8 or int4");
+    QuantizeReport rep;
+    const auto t0 = std::chrono::steady_clock::now();
+    Staging dev;
+    auto find = [&](const std::string& name) -> const BF16Tensor* {
+        auto it = src.find(name);
+        return it == src.end() ? nullptr : &it->second;
+    };
+    auto need = [&](const std::string& name) -> const BF16Tensor& {
+        const BF16Tensor* t = find(name);
+        if (!t || !t->data) throw std::runtime_error("quantize_model: missing tensor " + name);
+        return *t;
+    };
+    auto matrix = [&](const std::string& name) {
+        const BF16Tensor& t = need(name);
+        if (t.shape.size() != 2 || t.shape[0] <= 0 || t.shape[1] <= 0)
+            throw std::runtime_error("quantize_model: " + name + " is not a matrix");
+        const int64_t rows = t.shape[0], cols = t.shape[1];
+        if (kind == QKind::kInt4 && (cols & 1)) throw std::runtime_error("quantize_model: " + name + " has an odd width");
+        QMatrix m;
+        m.kind = kind;
+        m.rows = rows;
+        m.cols = cols;
+        const int64_t G = (cols + kGroup - 1) / kGroup;
+        m.q.resize(kind == QKind::kInt4 ? size_t(rows) * cols / 2 : size_t(rows) * cols);
+        m.scales.resize(size_t(rows) * G);
+        if (kind == QKind::kInt4) m.zeros.resize(size_t(rows) * G);
+        dev.fit(rows, cols);
+        hip_check(hipMemcpy(dev.in(), t.data, size_t(rows) * cols * 2, hipMemcpyHostToDevice), "quantize_model: upload");
+        iq_check(iq_quantize(dev.in(), rows, cols, kind == QKind::kInt4 ? IQ_INT4 : IQ_INT8, dev.q(), dev.s(),
+                             kind == QKind::kInt4 ? dev.z() : nullptr, nullptr),
+                 "quantize_model");
+        hip_check(hipMemcpy(m.q.data(), dev.q(), m.q.size(), hipMemcpyDeviceToHost), "quantize_model: download");
+        hip_check(hipMemcpy(m.scales.data(), dev.s(), m.scales.size() * 2, hipMemcpyDeviceToHost),
+                  "quantize_model: download");
+        if (!m.zeros.empty())
+            hip_check(hipMemcpy(m.zeros.data(), dev.z(), m.zeros.size(), hipMemcpyDeviceToHost), "quantize_model: download");
+        rep.worst = std::max(rep.worst, sampled_group_error(t.data, m.view()));
+        rep.bytes_in += size_t(rows) * cols * 2;
+        rep.bytes_out += m.q.size() + m.scales.size() * 2 + m.zeros.size();
+        rep.matrices++;
+        w.add(name, m);
+    };
+    auto copy_vec = [&](const std::string& name, bool required) {
+        const BF16Tensor* t = required ? &need(name) : find(name);
+        if (!t || !t->data) return;
+        int64_t n = 1;
+        for (int64_t d : t->shape) n *= d;
+        w.add_bf16(name, t->data, t->shape);
+        rep.bytes_in += size_t(n) * 2;
+        rep.bytes_out += size_t(n) * 2;
+        rep.vectors++;
+    };
+    matrix("model.embed_tokens.weight");
+    if (find("lm_head.weight")) matrix("lm_head.weight");
+    copy_vec("model.norm.weight", true);
+    for (int64_t i = 0; i < cfg.num_hidden_layers; i++) {
+        const std::string p = "model.layers." + std::to_string(i) + ".";
+        for (const char* m : {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                              "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+                              "mlp.down_proj.weight"})
+            matrix(p + m);
+        copy_vec(p + "input_layernorm.weight", true);
+        copy_vec(p + "post_attention_layernorm.weight", true);
+        for (const char* b : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"})
+            copy_vec(p + b, false);
+    }
+    rep.seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    return rep;
 }
 
 // ------------------------------------------------------------------ writer

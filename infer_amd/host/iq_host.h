@@ -152,6 +152,35 @@ private:
     QuantFile file_;
 };
 
+// A bf16 tensor of a model held in host memory (a source for quantize_model).
+struct BF16Tensor {
+    const uint16_t* data = nullptr;
+    std::vector<int64_t> shape;
+};
+
+// What quantize_model reports (tools/quantize.cpp:76-81): bytes before and
+// after, the worst per-group error |w - dequant(w)| as a fraction of the
+// group's absmax over sampled rows (every rows / 64-th row, every group),
+// and the wall time.
+struct QuantizeReport {
+    size_t bytes_in = 0, bytes_out = 0;
+    double worst = 0.0;
+    double seconds = 0.0;
+    int matrices = 0, vectors = 0;
+};
+
+// The offline quantiser's loop (tools/quantize.cpp:30-73) with the packing on
+// the GPU: every linear matrix and the embedding table of the model `src`
+// holds (names as in the reference's files; `cfg` gives the layer count) is
+// quantised to `kind` by iq_quantize, bit-exact to the reference's CPU
+// quantiser, and added to `w` with the norms and biases copied as bf16, in
+// the reference's order (embedding, lm_head when present, final norm, then
+// per layer q, k, v, o, gate, up, down, the two norms, the q/k/v biases when
+// present), so w.write() produces the reference's .llmq file byte for byte.
+// Missing required tensors throw.  One device staging buffer, reused.
+QuantizeReport quantize_model(const std::map<std::string, BF16Tensor>& src, const ModelConfig& cfg, QKind kind,
+                              QuantWriter& w);
+
 namespace gpu {
 
 // kernels/ops/ops.cuh:165-172; byte-compatible with iq_view.

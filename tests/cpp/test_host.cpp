@@ -13,6 +13,11 @@
 //       re-writes every tensor of <in> with QuantWriter, in file order
 //   test_host errors <dir>
 //       malformed containers must throw std::runtime_error
+//   test_host qmodel <tensors.bin> <model_dir> int8|int4 <out.llmq>
+//       quantize_model (the offline quantiser's loop, packing on the GPU) over
+//       the bf16 tensors of <tensors.bin> (u32 count; per tensor u32 name
+//       length, name, u32 ndim, i64 dims, bf16 data), config from
+//       <model_dir>/config.json; writes <out.llmq> and prints the report
 //   test_host gpu <model_dir>
 //       on-device quantize (bit-exact), linear_q / embedding on every matrix
 //       of the tiny model (int8 and int4) against the oracle
@@ -26,6 +31,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <random>
 #include <stdexcept>
 #include <string>
@@ -309,6 +315,40 @@ void on_fault(int sig) {
     _exit(128 + sig);
 }
 
+int cmd_qmodel(const std::string& bin, const std::string& dir, const std::string& kind, const std::string& out) {
+    std::ifstream f(bin, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + bin);
+    auto rd = [&](void* p, size_t n) {
+        f.read(static_cast<char*>(p), std::streamsize(n));
+        if (!f) throw std::runtime_error("truncated " + bin);
+    };
+    uint32_t count = 0;
+    rd(&count, 4);
+    std::vector<std::vector<uint16_t>> store(count);
+    std::map<std::string, llm::BF16Tensor> src;
+    for (uint32_t i = 0; i < count; i++) {
+        uint32_t nl = 0, nd = 0;
+        rd(&nl, 4);
+        std::string name(nl, '\0');
+        rd(&name[0], nl);
+        rd(&nd, 4);
+        std::vector<int64_t> shape(nd);
+        rd(shape.data(), 8 * nd);
+        int64_t n = 1;
+        for (int64_t d : shape) n *= d;
+        store[i].resize(size_t(n));
+        rd(store[i].data(), size_t(n) * 2);
+        src[name] = llm::BF16Tensor{store[i].data(), shape};
+    }
+    const llm::ModelConfig cfg = llm::ModelConfig::from_file(dir + "/config.json");
+    llm::QuantWriter w;
+    const llm::QuantizeReport r = llm::quantize_model(src, cfg, kind_of(kind), w);
+    w.write(out);
+    std::printf("quantized %d matrices, %d vectors: %zu -> %zu bytes, worst group error %.6f of absmax\n", r.matrices,
+                r.vectors, r.bytes_in, r.bytes_out, r.worst);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     std::setvbuf(stdout, nullptr, _IOLBF, 0);
     std::signal(SIGSEGV, on_fault);
@@ -324,6 +364,7 @@ int main(int argc, char** argv) {
         else if (cmd == "roundtrip" && argc == 4) rc = cmd_roundtrip(argv[2], argv[3]);
         else if (cmd == "errors") rc = cmd_errors(argv[2]);
         else if (cmd == "gpu") rc = cmd_gpu(argv[2]);
+        else if (cmd == "qmodel" && argc == 6) rc = cmd_qmodel(argv[2], argv[3], argv[4], argv[5]);
         if (rc == 0) std::fprintf(stderr, "test_host %s: all checks passed\n", cmd.c_str());
         return rc;
     } catch (const std::exception& e) {

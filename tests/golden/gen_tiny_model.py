@@ -51,27 +51,13 @@ def fnv1a64(b):
     return "%016x" % h
 
 
-def main():
-    L = ref_lib()
-    P = ctypes.c_void_p
-    L.ref_writer_new.restype = P
-    L.ref_writer_free.argtypes = [P]
-    L.ref_writer_add.argtypes = [P, ctypes.c_char_p, P, P, P, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
-    L.ref_writer_add.restype = ctypes.c_int
-    L.ref_writer_add_bf16.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int64]
-    L.ref_writer_add_bf16.restype = ctypes.c_int
-    L.ref_writer_write.argtypes = [P, ctypes.c_char_p]
-    L.ref_writer_write.restype = ctypes.c_int
-    L.ref_quantmodel_layers.argtypes = [ctypes.c_char_p, ctypes.c_int]
-    L.ref_quantmodel_layers.restype = ctypes.c_int
-
-    os.makedirs(OUT, exist_ok=True)
-    with open(os.path.join(OUT, "config.json"), "w") as f:
-        json.dump(CONFIG, f, indent=2)
+def tiny_entries():
+    """The tiny model's bf16 tensors, in tools/quantize.cpp:56-73 order:
+    [("m" matrix | "v" vector, name, bf16 bits array)] (seeded; the same
+    arrays every call)."""
     H, I, V = CONFIG["hidden_size"], CONFIG["intermediate_size"], CONFIG["vocab_size"]
     hd = H // CONFIG["num_attention_heads"]
     q_out, kv_out = CONFIG["num_attention_heads"] * hd, CONFIG["num_key_value_heads"] * hd
-
     rng = np.random.default_rng(2024)
 
     def mat(r, c):
@@ -98,6 +84,32 @@ def main():
                     ("v", pre + "self_attn.q_proj.bias", vec(q_out)),
                     ("v", pre + "self_attn.k_proj.bias", vec(kv_out)),
                     ("v", pre + "self_attn.v_proj.bias", vec(kv_out))]
+
+    return entries
+
+
+def main():
+    L = ref_lib()
+    P = ctypes.c_void_p
+    L.ref_writer_new.restype = P
+    L.ref_writer_free.argtypes = [P]
+    L.ref_writer_add.argtypes = [P, ctypes.c_char_p, P, P, P, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    L.ref_writer_add.restype = ctypes.c_int
+    L.ref_writer_add_bf16.argtypes = [P, ctypes.c_char_p, P, ctypes.c_int64]
+    L.ref_writer_add_bf16.restype = ctypes.c_int
+    L.ref_writer_write.argtypes = [P, ctypes.c_char_p]
+    L.ref_writer_write.restype = ctypes.c_int
+    L.ref_quantmodel_layers.argtypes = [ctypes.c_char_p, ctypes.c_int]
+    L.ref_quantmodel_layers.restype = ctypes.c_int
+
+    os.makedirs(OUT, exist_ok=True)
+    with open(os.path.join(OUT, "config.json"), "w") as f:
+        json.dump(CONFIG, f, indent=2)
+    H, I, V = CONFIG["hidden_size"], CONFIG["intermediate_size"], CONFIG["vocab_size"]
+    hd = H // CONFIG["num_attention_heads"]
+    q_out, kv_out = CONFIG["num_attention_heads"] * hd, CONFIG["num_key_value_heads"] * hd
+
+    entries = tiny_entries()
 
     manifest = {}
     for kind, fname in ((0, "model.q8.llmq"), (1, "model.q4.llmq")):

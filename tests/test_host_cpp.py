@@ -69,3 +69,63 @@ def test_host_launchers_on_gpu():
     print("test_host gpu", TINY, flush=True)
     rc, out, err = run("gpu", TINY, timeout=110)
     assert rc == 0, out + err
+
+
+def _tiny_entries():
+    import sys
+    sys.path.insert(0, os.path.join(HERE, "golden"))
+    from gen_tiny_model import fnv1a64, tiny_entries
+    return tiny_entries(), fnv1a64
+
+
+def test_tiny_model_sources_reproduce_the_fixture():
+    """The seeded bf16 tensors of tests/golden/gen_tiny_model.py, packed by
+    the oracle's quantiser (src/quant.cpp restated, pinned to the
+    reference's vectors), hash to the manifest the reference's own writer
+    recorded: they are the inputs the fixture files were made from."""
+    import numpy as np
+    from oracle import oracle as O
+    entries, fnv = _tiny_entries()
+    manifest = json.load(open(os.path.join(TINY, "manifest.json")))
+    for kind, fname in ((0, "model.q8.llmq"), (1, "model.q4.llmq")):
+        assert [e[1] for e in entries] == [m["name"] for m in manifest[fname]]
+        for (typ, name, arr), ref in zip(entries, manifest[fname]):
+            if typ == "v":
+                assert fnv(arr.tobytes()) == ref["data"], name
+            else:
+                q, s, z = O.quantize(arr, kind)
+                assert fnv(q.tobytes()) == ref["q"] and fnv(s.tobytes()) == ref["scales"], name
+                if kind == 1:
+                    assert fnv(z.tobytes()) == ref["zeros"], name
+
+
+def _write_tensors(path, entries):
+    import struct
+    with open(path, "wb") as f:
+        f.write(struct.pack("<I", len(entries)))
+        for _, name, arr in entries:
+            nb = name.encode()
+            f.write(struct.pack("<I", len(nb)) + nb + struct.pack("<I", arr.ndim))
+            f.write(struct.pack(f"<{arr.ndim}q", *arr.shape))
+            f.write(arr.astype("<u2").tobytes())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,fname", [("int8", "model.q8.llmq"), ("int4", "model.q4.llmq")])
+def test_quantize_model_on_gpu_writes_the_reference_file(kind, fname, tmp_path):
+    """llm::quantize_model (tools/quantize.cpp:30-83's loop, packing on the
+    GPU) over the tiny model's bf16 tensors writes the reference's own
+    .llmq file byte for byte, and reports a worst group error within the
+    quantiser's bounds: half a step for int8 (step = absmax / 127, its bf16
+    rounding included: < 1/200 of absmax); for int4 a step of (hi - lo) / 15
+    <= 2 absmax / 15 (half a step of rounding plus the zero point's)."""
+    entries, _ = _tiny_entries()
+    src = str(tmp_path / "tensors.bin")
+    _write_tensors(src, entries)
+    out = str(tmp_path / fname)
+    print("qmodel", kind, flush=True)
+    rc, o, e = run("qmodel", src, TINY, kind, out, timeout=110)
+    assert rc == 0, o + e
+    assert open(out, "rb").read() == open(os.path.join(TINY, fname), "rb").read()
+    worst = float(o.split("worst group error")[1].split()[0])
+    assert 0 < worst <= (1 / 200 if kind == "int8" else 2 / 15), worst
