@@ -860,5 +860,135 @@ DevQuantModel::DevQuantModel(const QuantModel& m)
     }
 }
 
+namespace {
+iq_view to_iq(const QuantView& v) {
+    iq_view r;
+    std::memcpy(&r, &v, sizeof(r));
+    return r;
+}
+}  // namespace
+
+DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
+    const int64_t H = cfg.hidden_size, I = cfg.intermediate_size, V = cfg.vocab_size;
+    const int64_t hd = cfg.head_dim, nh = cfg.num_attention_heads, nkv = cfg.num_key_value_heads;
+    const int64_t qo = nh * hd, kvo = nkv * hd, L = cfg.num_hidden_layers;
+    H_ = H;
+    V_ = V;
+    if (int64_t(m.layers.size()) != L) throw std::runtime_error("DecodeStep: model and config disagree on layers");
+    // arena: h0, per layer q, k, v, h1, act, h2, then logits; each vector on
+    // its own 1 KiB boundary
+    auto pad = [](int64_t n) { return (n + 255) / 256 * 256; };
+    int64_t total = pad(H) + L * (pad(qo) + 2 * pad(kvo) + 2 * pad(H) + pad(I)) + pad(V);
+    hip_check(hipMalloc(reinterpret_cast<void**>(&arena_), size_t(total) * 4), "DecodeStep: hipMalloc");
+    if (hipMalloc(reinterpret_cast<void**>(&ids_), 8) != hipSuccess) {
+        (void)hipFree(arena_);
+        throw std::runtime_error("DecodeStep: hipMalloc");
+    }
+    float* cur = arena_;
+    auto take = [&](int64_t n) {
+        float* p = cur;
+        cur += pad(n);
+        return p;
+    };
+    std::vector<iq_stage> st;
+    float* h = take(H);
+    h_.push_back(h);
+    const float eps = float(cfg.rms_norm_eps);
+    for (int64_t l = 0; l < L; l++) {
+        const DevLayer& D = m.layers[size_t(l)];
+        float *q = take(qo), *k = take(kvo), *v = take(kvo), *h1 = take(H), *act = take(I), *h2 = take(H);
+        iq_stage a{};
+        a.in_op = IQ_IN_RMSNORM;
+        a.out_op = IQ_OUT_STORE;
+        a.n = 3;
+        a.eps = eps;
+        a.x = h;
+        a.norm = D.input_ln.bf16();
+        a.W[0] = to_iq(D.q_w.view());
+        a.W[1] = to_iq(D.k_w.view());
+        a.W[2] = to_iq(D.v_w.view());
+        a.bias[0] = D.q_b.empty() ? nullptr : D.q_b.bf16();
+        a.bias[1] = D.k_b.empty() ? nullptr : D.k_b.bf16();
+        a.bias[2] = D.v_b.empty() ? nullptr : D.v_b.bf16();
+        a.y[0] = q;
+        a.y[1] = k;
+        a.y[2] = v;
+        st.push_back(a);
+        iq_stage o{};
+        o.in_op = IQ_IN_GQA;
+        o.out_op = IQ_OUT_RESIDUAL;
+        o.n = 1;
+        o.gqa_head_dim = int32_t(hd);
+        o.gqa_group = int32_t(nh / nkv);
+        o.x = v;
+        o.residual = h;
+        o.W[0] = to_iq(D.o_w.view());
+        o.y[0] = h1;
+        st.push_back(o);
+        iq_stage g{};
+        g.in_op = IQ_IN_RMSNORM;
+        g.out_op = IQ_OUT_SWIGLU;
+        g.n = 2;
+        g.eps = eps;
+        g.x = h1;
+        g.norm = D.post_attn_ln.bf16();
+        g.W[0] = to_iq(D.gate_w.view());
+        g.W[1] = to_iq(D.up_w.view());
+        g.y[0] = act;
+        st.push_back(g);
+        iq_stage d{};
+        d.in_op = IQ_IN_PLAIN;
+        d.out_op = IQ_OUT_RESIDUAL;
+        d.n = 1;
+        d.x = act;
+        d.residual = h1;
+        d.W[0] = to_iq(D.down_w.view());
+        d.y[0] = h2;
+        st.push_back(d);
+        h = h2;
+        h_.push_back(h);
+    }
+    logits_ = take(V);
+    iq_stage f{};
+    f.in_op = IQ_IN_RMSNORM;
+    f.out_op = IQ_OUT_STORE;
+    f.n = 1;
+    f.eps = eps;
+    f.x = h;
+    f.norm = m.final_norm.bf16();
+    f.W[0] = to_iq(m.head());
+    f.y[0] = logits_;
+    st.push_back(f);
+    const int rc = iq_chain_create(st.data(), int(st.size()), &chain_);
+    if (rc != IQ_OK) {
+        (void)hipFree(arena_);
+        (void)hipFree(ids_);
+        throw std::runtime_error(std::string("DecodeStep: ") + iq_error_string(rc));
+    }
+}
+
+DecodeStep::~DecodeStep() {
+    if (chain_) iq_chain_destroy(chain_);
+    if (arena_) (void)hipFree(arena_);
+    if (ids_) (void)hipFree(ids_);
+}
+
+void DecodeStep::step(int64_t token, hipStream_t stream) {
+    if (token < 0 || token >= V_) throw std::runtime_error("DecodeStep: token id out of range");
+    hip_check(hipMemcpyAsync(ids_, &token, 8, hipMemcpyHostToDevice, stream), "DecodeStep: id upload");
+    run(stream);
+}
+
+void DecodeStep::run(hipStream_t stream) {
+    iq_check(iq_embedding(reinterpret_cast<const iq_view*>(&m_.embed_tokens.view()), ids_, 1, H_, h_[0], stream),
+             "DecodeStep: embedding");
+    iq_check(iq_chain_run(chain_, stream), "DecodeStep: chain");
+}
+
+const float* DecodeStep::hidden(int layer) const {
+    if (layer < 0 || size_t(layer) >= h_.size()) throw std::runtime_error("DecodeStep: no such layer");
+    return h_[size_t(layer)];
+}
+
 }  // namespace gpu
 }  // namespace llm

@@ -240,5 +240,39 @@ struct DevQuantModel {
     const QuantView& head() const { return lm_head.empty() ? embed_tokens.view() : lm_head.view(); }
 };
 
+// The quantised part of the reference's decode step
+// (GpuBatch::Impl::launch_sequence, kernels/batch_gpu.cu:186-215) for one
+// sequence of one token at position 0, as one chain (include/iq.h
+// iq_chain_*): the quantised embedding gather, then per layer RMSNorm ->
+// q|k|v (+ biases), single-key attention (each query head takes its kv
+// head's value row: the softmax over one key is 1) -> o + residual,
+// RMSNorm -> gate|up with the SwiGLU epilogue, down + residual, and the
+// final RMSNorm -> LM head.  Every intermediate vector has its own device
+// buffer.  The model's widths must be multiples of 256 (the chain's stage
+// rule).  Runs are asynchronous on `stream`; run(stream) issues only device
+// work (capturable into a HIP graph) after the token id is in ids().
+class DecodeStep {
+public:
+    DecodeStep(const DevQuantModel& m, const ModelConfig& cfg);
+    ~DecodeStep();
+    DecodeStep(const DecodeStep&) = delete;
+    DecodeStep& operator=(const DecodeStep&) = delete;
+    // copies `token` to ids() (host to device, on `stream`), then run()
+    void step(int64_t token, hipStream_t stream = nullptr);
+    void run(hipStream_t stream = nullptr);
+    int64_t* ids() const { return ids_; }            // device, 1 id
+    const float* logits() const { return logits_; }  // device, vocab_size
+    const float* hidden(int layer) const;            // residual stream entering `layer` (layers: the last)
+
+private:
+    const DevQuantModel& m_;
+    int64_t H_ = 0, V_ = 0;
+    float* arena_ = nullptr;
+    int64_t* ids_ = nullptr;
+    float* logits_ = nullptr;
+    std::vector<float*> h_;  // h_[l]: hidden state entering layer l; h_[L]: final
+    iq_chain* chain_ = nullptr;
+};
+
 }  // namespace gpu
 }  // namespace llm

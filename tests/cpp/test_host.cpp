@@ -18,6 +18,10 @@
 //       the bf16 tensors of <tensors.bin> (u32 count; per tensor u32 name
 //       length, name, u32 ndim, i64 dims, bf16 data), config from
 //       <model_dir>/config.json; writes <out.llmq> and prints the report
+//   test_host chain <tensors.bin> <dir> int8|int4 <token> <out.bin>
+//       the whole host path: quantize_model -> <dir>/model.q8|q4.llmq (config
+//       from <dir>/config.json) -> QuantModel::load -> DevQuantModel ->
+//       gpu::DecodeStep::step(token); writes the logits (fp32) to <out.bin>
 //   test_host gpu <model_dir>
 //       on-device quantize (bit-exact), linear_q / embedding on every matrix
 //       of the tiny model (int8 and int4) against the oracle
@@ -29,6 +33,7 @@
 #include <cmath>
 #include <csignal>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <map>
@@ -349,6 +354,55 @@ int cmd_qmodel(const std::string& bin, const std::string& dir, const std::string
     return 0;
 }
 
+std::map<std::string, llm::BF16Tensor> read_tensors(const std::string& bin, std::vector<std::vector<uint16_t>>& store) {
+    std::ifstream f(bin, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + bin);
+    auto rd = [&](void* p, size_t n) {
+        f.read(static_cast<char*>(p), std::streamsize(n));
+        if (!f) throw std::runtime_error("truncated " + bin);
+    };
+    uint32_t count = 0;
+    rd(&count, 4);
+    store.assign(count, {});
+    std::map<std::string, llm::BF16Tensor> src;
+    for (uint32_t i = 0; i < count; i++) {
+        uint32_t nl = 0, nd = 0;
+        rd(&nl, 4);
+        std::string name(nl, '\0');
+        rd(&name[0], nl);
+        rd(&nd, 4);
+        std::vector<int64_t> shape(nd);
+        rd(shape.data(), 8 * nd);
+        int64_t n = 1;
+        for (int64_t d : shape) n *= d;
+        store[i].resize(size_t(n));
+        rd(store[i].data(), size_t(n) * 2);
+        src[name] = llm::BF16Tensor{store[i].data(), shape};
+    }
+    return src;
+}
+
+int cmd_chain(const std::string& bin, const std::string& dir, const std::string& kind, int64_t token,
+              const std::string& out) {
+    std::vector<std::vector<uint16_t>> store;
+    const auto src = read_tensors(bin, store);
+    const llm::ModelConfig cfg = llm::ModelConfig::from_file(dir + "/config.json");
+    llm::QuantWriter w;
+    llm::quantize_model(src, cfg, kind_of(kind), w);
+    w.write(llm::QuantModel::file_for(dir, kind_of(kind)));
+    llm::QuantModel qm;
+    qm.load(dir, kind_of(kind));
+    llm::gpu::DevQuantModel dm(qm);
+    llm::gpu::DecodeStep step(dm, qm.cfg);
+    step.step(token);
+    std::vector<float> logits(size_t(cfg.vocab_size));
+    hip_ok(hipMemcpy(logits.data(), step.logits(), logits.size() * 4, hipMemcpyDeviceToHost), "logits");
+    std::ofstream f(out, std::ios::binary);
+    f.write(reinterpret_cast<const char*>(logits.data()), std::streamsize(logits.size() * 4));
+    std::printf("chain ok: %zu logits\n", logits.size());
+    return 0;
+}
+
 int main(int argc, char** argv) {
     std::setvbuf(stdout, nullptr, _IOLBF, 0);
     std::signal(SIGSEGV, on_fault);
@@ -365,6 +419,7 @@ int main(int argc, char** argv) {
         else if (cmd == "errors") rc = cmd_errors(argv[2]);
         else if (cmd == "gpu") rc = cmd_gpu(argv[2]);
         else if (cmd == "qmodel" && argc == 6) rc = cmd_qmodel(argv[2], argv[3], argv[4], argv[5]);
+        else if (cmd == "chain" && argc == 7) rc = cmd_chain(argv[2], argv[3], argv[4], std::atoll(argv[5]), argv[6]);
         if (rc == 0) std::fprintf(stderr, "test_host %s: all checks passed\n", cmd.c_str());
         return rc;
     } catch (const std::exception& e) {

@@ -129,3 +129,64 @@ def test_quantize_model_on_gpu_writes_the_reference_file(kind, fname, tmp_path):
     assert open(out, "rb").read() == open(os.path.join(TINY, fname), "rb").read()
     worst = float(o.split("worst group error")[1].split()[0])
     assert 0 < worst <= (1 / 200 if kind == "int8" else 2 / 15), worst
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_decode_step_through_the_host_layer(kind, tmp_path):
+    """The C++ host path end to end: quantize_model (GPU) writes a .llmq,
+    QuantModel::load reads it, DevQuantModel uploads it, gpu::DecodeStep
+    runs the chained decode step of one token; its logits match the
+    oracle's float64 forward of src/forward.cpp on the dequantised weights
+    (max |err| / max |ref| <= 1e-3)."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(4242)
+    H, I, nh, nkv, hd, V, L = 256, 512, 2, 1, 128, 300, 2
+    cfg = {"architectures": ["Qwen2ForCausalLM"], "hidden_size": H, "intermediate_size": I,
+           "num_attention_heads": nh, "num_key_value_heads": nkv, "num_hidden_layers": L, "vocab_size": V,
+           "rope_theta": 1000000.0, "rms_norm_eps": 1e-6, "tie_word_embeddings": False}
+    json.dump(cfg, open(tmp_path / "config.json", "w"))
+    mat = lambda r, c, sd=0.05: O.seeded_bf16(rng, (r, c), sd)
+    vec = lambda n, base=0.0: O.f32_to_bf16(base + rng.standard_normal(n).astype(np.float32) * np.float32(0.1))
+    ents = [("m", "model.embed_tokens.weight", mat(V, H, 0.5)), ("m", "lm_head.weight", mat(V, H)),
+            ("v", "model.norm.weight", vec(H, 1.0))]
+    for i in range(L):
+        p = f"model.layers.{i}."
+        ents += [("m", p + "self_attn.q_proj.weight", mat(nh * hd, H)), ("m", p + "self_attn.k_proj.weight", mat(nkv * hd, H)),
+                 ("m", p + "self_attn.v_proj.weight", mat(nkv * hd, H)), ("m", p + "self_attn.o_proj.weight", mat(H, nh * hd)),
+                 ("m", p + "mlp.gate_proj.weight", mat(I, H)), ("m", p + "mlp.up_proj.weight", mat(I, H)),
+                 ("m", p + "mlp.down_proj.weight", mat(H, I)), ("v", p + "input_layernorm.weight", vec(H, 1.0)),
+                 ("v", p + "post_attention_layernorm.weight", vec(H, 1.0)), ("v", p + "self_attn.q_proj.bias", vec(nh * hd)),
+                 ("v", p + "self_attn.k_proj.bias", vec(nkv * hd)), ("v", p + "self_attn.v_proj.bias", vec(nkv * hd))]
+    _write_tensors(str(tmp_path / "tensors.bin"), ents)
+    token = 123
+    out = str(tmp_path / "logits.bin")
+    print("host chain", kind, flush=True)
+    rc, o, e = run("chain", str(tmp_path / "tensors.bin"), str(tmp_path), kind, str(token), out, timeout=110)
+    assert rc == 0, o + e
+    got = np.fromfile(out, dtype=np.float32).astype(np.float64)
+    k = 1 if kind == "int4" else 0
+    t = {name: arr for _, name, arr in ents}
+
+    def dq(name):
+        a = t[name]
+        q, s, z = O.quantize(a, k)
+        return O.dequant_matrix(q, s, z, k, a.shape[0], a.shape[1])
+
+    model = {"cfg": dict(hidden=H, heads=nh, kv_heads=nkv, head_dim=hd, eps=1e-6),
+             "embed_dq": dq("model.embed_tokens.weight"), "head_dq": dq("lm_head.weight"),
+             "final_norm": t["model.norm.weight"], "layers": []}
+    for i in range(L):
+        p = f"model.layers.{i}."
+        model["layers"].append({
+            "q": dq(p + "self_attn.q_proj.weight"), "k": dq(p + "self_attn.k_proj.weight"),
+            "v": dq(p + "self_attn.v_proj.weight"), "o": dq(p + "self_attn.o_proj.weight"),
+            "gate": dq(p + "mlp.gate_proj.weight"), "up": dq(p + "mlp.up_proj.weight"),
+            "down": dq(p + "mlp.down_proj.weight"), "input_ln": t[p + "input_layernorm.weight"],
+            "post_ln": t[p + "post_attention_layernorm.weight"], "q_b": t[p + "self_attn.q_proj.bias"],
+            "k_b": t[p + "self_attn.k_proj.bias"], "v_b": t[p + "self_attn.v_proj.bias"]})
+    ref = O.decode_first_token_f64(model, token)["logits"]
+    rel = float(np.abs(got - ref).max() / np.abs(ref).max())
+    print(f"  logits max rel {rel:.3g}", flush=True)
+    assert rel <= 1e-3
