@@ -44,6 +44,8 @@ hipError_t create_workspace(Workspace* ws) {
     ws->xq = reinterpret_cast<int8_t*>(p + xf);
     ws->xmeta = reinterpret_cast<int4*>(p + xf + xq);
     ws->partials = reinterpret_cast<float*>(p + xf + xq + meta);
+    ws->xq_bytes = xq;
+    ws->xmeta_bytes = meta;
     return hipSuccess;
 }
 
@@ -93,6 +95,9 @@ hipError_t static_workspace(Workspace** out) {
         w.xq = reinterpret_cast<int8_t*>(p);
         w.xmeta = reinterpret_cast<int4*>(p + kStaticXq);
         w.partials = reinterpret_cast<float*>(p + kStaticXq + kStaticMeta);
+        w.xq_bytes = kStaticXq;
+        w.xmeta_bytes = kStaticMeta;
+        w.can_grow = false;
         g_static_ready[dev] = true;
     }
     *out = &g_static_ws[dev];
@@ -130,6 +135,41 @@ hipError_t get_workspace(hipStream_t stream, Workspace** out) {
         ws = w;
     }
     *out = ws;
+    return hipSuccess;
+}
+
+hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs,
+                         hipStream_t stream) {
+    const size_t op = size_t(T) * size_t(K) * 2 * (lo ? 2 : 1);
+    const size_t rows = align256(sizeof(float) * size_t(T));
+    if (op <= ws->xq_bytes && sizeof(float) * size_t(T) <= ws->xmeta_bytes) {
+        ws->invalidate_prep();
+        *ah = reinterpret_cast<_Float16*>(ws->xq);
+        *rs = reinterpret_cast<float*>(ws->xmeta);
+        return hipSuccess;
+    }
+    const size_t need = align256(op) + rows;
+    if (need > ws->gx_bytes) {
+        if (!ws->can_grow) return hipErrorInvalidValue;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return hipErrorStreamCaptureUnsupported;
+        if (ws->gx) {
+            // (earlier launches on the stream may still read the old buffer)
+            hipError_t e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return e;
+            (void)hipFree(ws->gx);
+            ws->gx = nullptr;
+            ws->gx_bytes = 0;
+        }
+        void* b = nullptr;
+        hipError_t e = hipMalloc(&b, need);
+        if (e != hipSuccess) return e;
+        ws->gx = b;
+        ws->gx_bytes = need;
+    }
+    *ah = static_cast<_Float16*>(ws->gx);
+    *rs = reinterpret_cast<float*>(static_cast<char*>(ws->gx) + align256(op));
     return hipSuccess;
 }
 
@@ -312,7 +352,7 @@ int iq_gemm(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, i
     iq::Workspace* ws = nullptr;
     const hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
     if (e != hipSuccess) return ws_status(e);
-    return from_hip(iq::launch_gemm(x, nullptr, to_qview(W), bias, T, y, ws->partials, static_cast<hipStream_t>(stream)));
+    return from_hip(iq::launch_gemm(x, nullptr, to_qview(W), bias, T, y, ws, static_cast<hipStream_t>(stream)));
 }
 
 int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int64_t T,
@@ -325,7 +365,7 @@ int iq_gemm_bf16x(const uint16_t* x, const iq_view* W, const uint16_t* bias, int
     iq::Workspace* ws = nullptr;
     const hipError_t e = iq::get_workspace(static_cast<hipStream_t>(stream), &ws);
     if (e != hipSuccess) return ws_status(e);
-    return from_hip(iq::launch_gemm(nullptr, x, to_qview(W), bias, T, y, ws->partials, static_cast<hipStream_t>(stream)));
+    return from_hip(iq::launch_gemm(nullptr, x, to_qview(W), bias, T, y, ws, static_cast<hipStream_t>(stream)));
 }
 
 int iq_linear(const float* x, const iq_view* W, const uint16_t* bias, int64_t T, int64_t in,

@@ -1560,9 +1560,14 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
         if (pl.ng > 0) return launch_gemv1(ws->xf, W, bias, y, n, pl, mode, stream, M, ws->partials);
         // (too many tiles for the split-K partials of this width): the
         // general path on the copy, the preparation left as it was
-        const Workspace keep = *ws;
+        const int keep_M = ws->prep_M, keep_kind = ws->prep_kind;
+        const int64_t keep_K = ws->prep_K;
         const hipError_t e = launch_gemv_multi(ws->xf, W, bias, y, n, M, ws, stream);
-        *ws = keep;
+        ws->prep_M = keep_M;
+        ws->prep_K = keep_K;
+        ws->prep_kind = keep_kind;
+        ws->prep_copy = true;
+        ws->prep_h = false;
         return e;
     }
     if (ws->prep_h) return launch_gemvh(W, bias, y, n, M, ws, stream);
@@ -1583,7 +1588,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         // 7B down 3584 x 18944 at 24 / 32 rows: 50.1 / 54.0 -> 37.4 / 38.4
         // us int8, gate 18944 x 3584 int4: 47.5 / 53.0 -> 44.7 / 46.7)
         for (int i = 0; i < n; i++) {
-            const hipError_t e = launch_gemm(x, nullptr, W[i], bias[i], M, y[i], ws->partials, stream);
+            const hipError_t e = launch_gemm(x, nullptr, W[i], bias[i], M, y[i], ws, stream);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;

@@ -30,6 +30,12 @@ struct Workspace {
                                // A operands [kMaxRowsGemv/16][kMaxKp/128][8 KiB] (gemvh)
     int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, sum X0, 256 sum X1 + sum X2, 0}
     float* partials = nullptr; // kPartialFloats
+    size_t xq_bytes = 0, xmeta_bytes = 0;
+    // the prefill GEMM's prepared activations when they exceed xq (grown on
+    // demand; null in the static workspace)
+    void* gx = nullptr;
+    size_t gx_bytes = 0;
+    bool can_grow = true;
     // Shape of the activations last prepared into xq/xmeta (host-side record).
     int prep_M = 0;
     int64_t prep_K = 0;
@@ -77,9 +83,16 @@ hipError_t launch_gemv_prepped_multi(const QView* W, const uint16_t* const* bias
 // shapes prepare x once into the workspace, then one launch per matrix.
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream);
-// part: the workspace's split-K partials (short T splits K over workgroups).
+// Uses the workspace for the prepared fp16 activations and the split-K
+// partials (short T splits K over workgroups).
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
-                       const uint16_t* bias, int64_t T, float* y, float* part, hipStream_t stream);
+                       const uint16_t* bias, int64_t T, float* y, Workspace* ws, hipStream_t stream);
+// Room for the prefill GEMM's prepared activations: T x K fp16 (x 2 with
+// lo) and T row factors.  Reuses xq / xmeta when they are large enough
+// (the preparation of iq_gemv_prep is then forgotten), else a buffer the
+// workspace grows (not while the stream is being captured).
+hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs,
+                         hipStream_t stream);
 
 // A validated stage program on the device (iq_chain.hip).
 struct Chain;

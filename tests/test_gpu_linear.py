@@ -94,6 +94,46 @@ def test_gemm_fp32(kind, T):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
+def test_gemm_fp32_precision(kind):
+    """fp32 activations spanning six decades within each row: the fp16
+    hi + lo operands (whole groups) and the three bf16 terms (ragged K) keep
+    about 22 significant bits, so the error stays below 2^-19 of the
+    conditioning sum -- a two-term bf16 split (about 16 bits) would not."""
+    rng = np.random.default_rng(77 + kind)
+    for T, N, K in ((96, 384, 3584), (520, 256, 1024), (40, 130, 130)):
+        W = QFix(rng, N, K, kind, sd=0.02)
+        x = (rng.standard_normal((T, K)) * 10.0 ** rng.uniform(-3, 3, (T, K))).astype(np.float32)
+        y = out_buffer(T, N)
+        say("gemm fp32 precision", kind, T, N, K)
+        ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
+        torch.cuda.synchronize()
+        worst, _ = check_linear(y, x, W, None, T, f"gemm fp32 precision kind={kind} T={T} {N}x{K}")
+        assert worst < 2.0 ** -19, (T, N, K, worst)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemm_fp32_nonfinite_row(kind):
+    """A row holding inf or NaN makes that row's outputs NaN; the other rows
+    are unaffected (fp16 operand path: the row's factor is NaN)."""
+    rng = np.random.default_rng(91 + kind)
+    T, N, K = 70, 256, 1024
+    W = QFix(rng, N, K, kind, sd=0.02)
+    x = rng.standard_normal((T, K), dtype=np.float32)
+    x[3, 17] = np.inf
+    x[50, 900] = np.nan
+    y = out_buffer(T, N)
+    say("gemm fp32 non-finite", kind)
+    ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()[: T * N].reshape(T, N)
+    assert np.all(np.isnan(got[3])) and np.all(np.isnan(got[50]))
+    keep = [m for m in range(T) if m not in (3, 50)]
+    ref, cond = O.linear_dq_f64(x[keep], W.dq, None)
+    err = np.abs(got[keep].astype(np.float64) - ref)
+    assert float((err / np.maximum(cond, 1e-30)).max()) <= 5e-6
+
+
+@pytest.mark.parametrize("kind", [0, 1])
 def test_gemm_bf16x(kind):
     rng = np.random.default_rng(9)
     # (48, 700, 3584): 64-row tiles with K split over workgroups
