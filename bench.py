@@ -286,8 +286,9 @@ def hbm_copy_rate(torch, reps=20):
 
 def bench_gemm(torch, ops, kind, T, N, K, reps=10, seed=5, fp32x=False):
     """Prefill GEMM at config 5: bf16 activations (iq_gemm_bf16x), or fp32
-    activations through the reference-compatible launch_gemm_tiled_q
-    (split into bf16 hi + lo inside the kernel, two MFMAs per product)."""
+    activations through the reference-compatible launch_gemm_tiled_q (one
+    preparation launch into fp16 hi + lo operands, then two MFMAs per
+    product; the timing includes the preparation)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     W = quantize_seeded(torch, ops, kind, N, K, g)
     xf = torch.randn(T, K, generator=g, device="cuda")
@@ -395,11 +396,24 @@ def profile_workload(torch, ops):
 
 def profile_gemm_workload(torch, ops):
     """Fixed short workload for `rocprofv3 --pmc` runs of the prefill GEMM
-    (config 5, T = 1024, bf16 activations): int8 and int4 gate/up 18944x3584
-    and down 3584x18944, each launched 2 + 3 times by bench_gemm."""
-    for kind in (0, 1):
-        for N, K in ((I7, H7), (H7, I7)):
-            bench_gemm(torch, ops, kind, 1024, N, K, reps=3)
+    (config 5, T = 1024): int8 and int4 gate/up 18944x3584 and down
+    3584x18944, bf16 then fp32 activations, each launched 2 + 3 times by
+    bench_gemm."""
+    for fp32x in (False, True):
+        for kind in (0, 1):
+            for N, K in ((I7, H7), (H7, I7)):
+                bench_gemm(torch, ops, kind, 1024, N, K, reps=3, fp32x=fp32x)
+    torch.cuda.synchronize()
+
+
+def profile_rows_workload(torch, ops, M):
+    """Fixed short workload for `rocprofv3` runs of the M-row decode set: 4
+    layers of the 7B int4 set at M activation rows (the launches of the timed
+    step at that width, preparation launches included), run 3 times."""
+    m4 = Model(torch, ops, 1, H7, I7, NH7 * 128, KV7 * 128, 4, head=None, seed=7)
+    st = Step(torch, ops, m4, M)
+    for _ in range(3):
+        st.run()
     torch.cuda.synchronize()
 
 
@@ -428,6 +442,8 @@ def main():
                     help="short fixed prefill-GEMM workload for rocprofv3 counter runs (prints nothing)")
     ap.add_argument("--profile-quantize", action="store_true",
                     help="short fixed quantize workload for rocprofv3 counter runs (prints nothing)")
+    ap.add_argument("--profile-rows", type=int, default=0,
+                    help="short fixed M-row decode-set workload for rocprofv3 runs (prints nothing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -446,6 +462,9 @@ def main():
         return
     if args.profile_quantize:
         profile_quantize_workload(torch, ops)
+        return
+    if args.profile_rows:
+        profile_rows_workload(torch, ops, args.profile_rows)
         return
     t_setup = time.perf_counter()
 

@@ -22,10 +22,16 @@
 // point and the activation exponent in fp32.  The slice sums are added in
 // wave order through LDS by the wave that finishes last (deterministic).
 //
-// RMSNorm needs the whole input vector: every thread of the workgroup loads
-// a part of it (16-byte loads, issued before the weights), the sum of
-// squares is reduced in double through LDS in a fixed order, and the raw
-// vector stays in LDS for the waves' slices.
+// RMSNorm needs the sum of squares of the whole input vector.  When the
+// input is the output of an earlier stage of the same chain (the residual
+// stream after o and down), that stage writes one partial sum of squares
+// per 16-row output tile as it stores the tile, and the consumer adds the
+// producer's partials in tile order (in double) before its slices' scale is
+// known: no extra pass over the vector.  Otherwise (the chain's first
+// input) every thread of the workgroup loads a part of the vector (16-byte
+// loads, issued before the weights), the sum of squares is reduced in
+// double through LDS in a fixed order, and the raw vector stays in LDS for
+// the waves' slices.
 //
 // A persistent variant (one cooperative launch for the whole program, grid
 // barriers between stages, next-stage weights requested before each
