@@ -42,6 +42,8 @@
 //    adds them in range order, so the result is deterministic and no
 //    counter has to be cleared between launches.
 //  * gemvh (2..32 rows, f16 split activations): see gemvh_kernel.
+//  * gemvs (9..16 rows on very wide calls, the same split operands shared
+//    through LDS by 8 tiles): see gemvs_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -1420,6 +1422,177 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
     }
 }
 
+// 9..16 rows on the prepared f16 split operands, the operands shared
+// through LDS: workgroup = 8 waves on 8 consecutive 16-row tiles (wave w:
+// tile 8 b + w, over every matrix of the call) and one K range of groups
+// [g0, g1).  Per group the workgroup copies the group's 8 KiB of A operands
+// (4 k-chunks x hi, lo) into LDS once (one 16-byte load per thread, the next
+// group's in registers), and every wave multiplies them by its own tile's
+// weights, which stream D groups ahead in registers.  A operand bytes read
+// from L2 per weight byte: 1 (int4) / 0.5 (int8) instead of the 8 / 4 of a
+// wave that loads the operands for its tile alone.  S > 1 ranges write fp32
+// partial sums that gemvt_reduce_kernel adds in range order.
+template <int KIND>
+__global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
+    constexpr int D = 4;  // weight groups in flight per wave
+    constexpr int WPG = KIND == 1 ? 1 : 2;
+    __shared__ __attribute__((aligned(16))) int4v_t As[2][512];
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = int(p.G);
+    const int nrb = (p.ntiles + 7) / 8;
+    const int rb = int(blockIdx.x) % nrb, range = int(blockIdx.x) / nrb;
+    const int g0 = range * p.gs, g1 = g0 + p.gs < G ? g0 + p.gs : G;
+    const int tile = rb * 8 + wave;
+    const bool tok = tile < p.ntiles;
+    const TileSel ts = select_tile(p, tok ? tile : p.ntiles - 1);
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const int64_t left = ts.m.N - ts.row0;
+    const int64_t rows = tok ? (left < 16 ? left : 16) : 0;
+    const rsrc_t rq = make_rsrc(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
+    const rsrc_t rs = make_rsrc(ts.m.scales + ts.row0 * G, rows * G * 2);
+    const rsrc_t rz = make_rsrc(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * kHGroupBytes);
+    const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
+    const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
+    const uint32_t vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
+
+    // Everything a group needs (its A operand share, this wave's weights,
+    // scale, zero point and row factors) is requested together, D groups
+    // ahead, into one of D register slots: the memory counter completes in
+    // request order, so a wait for one group's data never waits for a
+    // request made later than D - 1 groups before it.
+    struct Slot {
+        int4v_t a;
+        int4v_t w[WPG];
+        uint32_t s, z;
+        float4_t fx;
+    };
+    auto load = [&](int g, Slot& b) {
+        const uint32_t off = g < g1 ? 0u : kOob;
+        b.a = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(ra, uint32_t(tid * 16) + off,
+                                                                                 g * kHGroupBytes, 0));
+#pragma unroll
+        for (int h = 0; h < WPG; h++)
+            b.w[h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rq, vq + off, g * (KIND == 1 ? 64 : 128) + h * 16, 0));
+        b.s = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + off, g * 2, 0);
+        b.z = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + off, g, 0) : 0u;
+        b.fx = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rf, uint32_t(q * 16) + off, g * 64, 0));
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](const Slot& b, int buf) {
+        half8_t B[4];
+        if (KIND == 1) {
+            const uint32_t zb = zpair_1024(b.z), zc = zpair_64(b.z);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t o0, o1, o2, o3;
+                dq_int4_x8(uint32_t(b.w[0][j]), zb, zc, o0, o1, o2, o3);
+                B[j] = pack_h8(o0, o1, o2, o3);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t l0, h0, l1, h1;
+                const int4v_t& wv = b.w[j >> 1];
+                dq_int8_x4(uint32_t(wv[2 * (j & 1)]), l0, h0);
+                dq_int8_x4(uint32_t(wv[2 * (j & 1) + 1]), l1, h1);
+                B[j] = pack_h8(l0, h0, l1, h1);
+            }
+        }
+        float4_t Dv = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            Dv = mfma16(__builtin_bit_cast(half8_t, As[buf][(2 * j) * 64 + lane]), B[j], Dv);
+            Dv = mfma16(__builtin_bit_cast(half8_t, As[buf][(2 * j + 1) * 64 + lane]), B[j], Dv);
+        }
+        const float sc = __uint_as_float(b.s << 16);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(Dv[r], sc * b.fx[r], acc[r]);
+    };
+
+    Slot s0, s1, s2, s3;
+    load(g0, s0);
+    load(g0 + 1, s1);
+    load(g0 + 2, s2);
+    load(g0 + 3, s3);
+    As[0][tid] = s0.a;
+    // group g: operands in As[(g - g0) & 1] (stored at the previous step),
+    // weights in slot (g - g0) % D; the slot is refilled with group g + D
+    auto iter = [&](int g, Slot& cur, const Slot& next) {
+        __syncthreads();
+        const int par = (g - g0) & 1;
+        if (g + 1 < g1) As[par ^ 1][tid] = next.a;
+        compute(cur, par);
+        load(g + D, cur);
+    };
+    for (int g = g0; g < g1; g += D) {
+        iter(g, s0, s1);
+        if (g + 1 >= g1) break;
+        iter(g + 1, s1, s2);
+        if (g + 2 >= g1) break;
+        iter(g + 2, s2, s3);
+        if (g + 3 >= g1) break;
+        iter(g + 3, s3, s0);
+    }
+    if (!tok) return;
+    const int64_t ld = int64_t(p.ntiles) * 16;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = 4 * q + r;
+        if (m >= p.M || ln >= rows) continue;
+        if (p.S == 1) {
+            const int64_t row = ts.row0 + ln;
+            ts.m.y[int64_t(m) * ts.m.N + row] = acc[r] + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
+        } else {
+            p.part[(int64_t(range) * p.M + m) * ld + int64_t(tile) * 16 + ln] = acc[r];
+        }
+    }
+}
+
+// gemvs on n matrices, M in 9..16, on the prepared split operands (false:
+// the split-K partials would not fit).
+bool launch_gemvs(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
+                  hipStream_t stream, hipError_t* err) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    GemvParams p{};
+    int tiles = 0;
+    for (int i = 0; i < n; i++) {
+        p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i], W[i].rows, tiles};
+        tiles += int((W[i].rows + 15) / 16);
+    }
+    const int nrb = (tiles + 7) / 8;
+    // K ranges: enough workgroups for two per CU, at least 4 groups each
+    const int want = 2 * device_cu_count();
+    int S = (want + nrb - 1) / nrb;
+    S = std::max(1, std::min<int>(S, int(G / 4)));
+    int gs = int((G + S - 1) / S);
+    S = int((G + gs - 1) / gs);
+    if (S > 1 && int64_t(S) * M * tiles * 16 > kPartialFloats) return false;
+    p.nmat = n;
+    p.K = K;
+    p.G = G;
+    p.xq = ws->xq;
+    p.meta = ws->xmeta;
+    p.M = M;
+    p.gs = gs;
+    p.S = S;
+    p.ntiles = tiles;
+    p.part = ws->partials;
+    const unsigned grid = unsigned(nrb * S);
+    if (W[0].kind == 1) gemvs_kernel<1><<<grid, 512, 0, stream>>>(p);
+    else gemvs_kernel<0><<<grid, 512, 0, stream>>>(p);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && S > 1) {
+        const int64_t outs = int64_t(M) * tiles * 16;
+        gemvt_reduce_kernel<<<unsigned((outs + 255) / 256), 256, 0, stream>>>(p);
+        e = hipGetLastError();
+    }
+    *err = e;
+    return true;
+}
+
 // f16 split preparation of x [M][K] (M <= kMaxRowsGemv, K % 128 == 0).
 hipError_t launch_xhprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
     const int64_t G = K / kGroup, quads = (G + 3) / 4;
@@ -1604,6 +1777,17 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // The conversion below overwrites xq / xmeta: a preparation held there
     // (not a copy in xf) is gone, so iq_gemv_prepped must refuse to run on it.
     if (!ws->prep_copy) ws->invalidate_prep();
+    // 9..16 rows on very wide calls (the lm_head): gemvs, whose workgroups
+    // share each group's operands over 8 tiles through LDS (7B lm_head
+    // 152064 x 3584 int8 at 16 rows: 176 -> 139 us; on the layer shapes it
+    // measured no better than gemvh / gemvt: gate|up 41.7 -> 42.8, down
+    // 33.6 -> 34.5 us at its best K split)
+    if (M > 8 && M <= 16 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
+        hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
+        if (e != hipSuccess) return e;
+        if (launch_gemvs(W, bias, y, n, M, ws, stream, &e)) return e;
+        return launch_gemvh(W, bias, y, n, M, ws, stream);
+    }
     if (gemvh_preferred(K, M, total_tiles(W, n), W[0].kind)) {
         const hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;

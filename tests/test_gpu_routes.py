@@ -14,7 +14,9 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     bf16 and fp32 activations, int8 and int4;
   * gate|up (2 x 18944 x 3584) in one iq_gemv_multi call at 9, 12 and 16
     rows (the staged-limb gemvt kernel) and at 1 row;
-  * the int8 lm_head 152064 x 3584 at 1 and 16 rows;
+  * the int8 lm_head 152064 x 3584 at 1 and 16 rows, and wide calls
+    (>= 4096 tiles) at 9..16 rows (gemvs: operands shared through LDS over
+    8 tiles), both kinds, with ragged row counts and biases;
   * every other 7B decode matrix at 16 rows.
 """
 import numpy as np
@@ -128,6 +130,25 @@ def test_lm_head_int8(M):
     ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
     torch.cuda.synchronize()
     check_sampled(y, x, W, M, rng, f"lm_head M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [9, 13, 16])
+def test_wide_call_9_to_16_rows(kind, M):
+    """Over 4096 16-row tiles (here 65541 rows, the last tile ragged, and a
+    second matrix in the same call) at 9..16 rows: the gemvs route."""
+    rng = np.random.default_rng(4096 + 10 * M + kind)
+    K = 1024
+    Ws = [Packed(rng, 65541, K, kind), Packed(rng, 300, K, kind)]
+    bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
+    bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("wide 9..16 rows", kind, M)
+    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, M, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
+        check_sampled(y, x, W, M, rng, f"wide[{i}] kind={kind} M={M}", bias_bits=bb)
 
 
 @pytest.mark.parametrize("kind", [0, 1])
