@@ -1,12 +1,16 @@
 // iq_quant.hip -- on-device quantize + pack and the quantised embedding
 // gather for gfx950.
 //
-// quantize: bit-exact to llm::quantize (src/quant.cpp:34-84).  One wave64
-// covers four 128-column groups of one row: each 16-lane DPP row of the wave
-// owns one group, each lane 8 consecutive columns (one 16-byte load of bf16).
+// quantize: bit-exact to llm::quantize (src/quant.cpp:34-84).  Whole-group
+// rows (cols % 128 == 0, quantize8_kernel): one wave64 covers eight
+// 128-column groups of one row, 8 lanes per group, each lane 16 consecutive
+// columns (two 16-byte loads of bf16).  Ragged rows (quantize_kernel): four
+// groups per wave, each 16-lane DPP row one group, 8 columns per lane.
 // The group's absmax (int8) or [min,max] widened to 0 (int4) is reduced
-// inside the 16 lanes; every lane then derives the same bf16 scale and writes
-// its 8 codes (8 bytes int8, 4 bytes int4), so stores stay coalesced.
+// inside the group's lanes; every lane then derives the same bf16 scale and
+// writes its codes, so stores stay coalesced.  Groups whose scale is
+// ordinary (finite, not tiny) take a rounding path without per-value range
+// tests; a wave holding any other group takes the general path.
 // Arithmetic follows the reference operation by operation: fp32 correctly
 // rounded division, round-half-even (std::lrint under the default mode),
 // the reference's clamps, and its comparison forms for max/min so that NaN
@@ -18,6 +22,7 @@
 #include <algorithm>
 
 #include "iq_internal.h"
+#include "iq_limbs.h"
 
 namespace iq {
 
@@ -71,17 +76,35 @@ __device__ __forceinline__ int qdiv(float w, float s, float r) {
     return int(__builtin_rintf(tie ? h : t));
 }
 
+// qdiv for a group whose scale is finite, at least 2^-64 (not moved) and
+// positive, and whose values are finite or NaN: |w / s| <= 127 (int8) or
+// <= 15 (int4 range) so t is finite, and a NaN w gives 0, the reference's
+// result for it.  No per-value range test, no scaling by `up`.  r may be
+// v_rcp_f32's reciprocal (within 1 ulp of 1 / s): t = w r is then within
+// 2^-23 + 2^-24 < 2^-22 of q* relatively, inside qdiv's gap argument.
+__device__ __forceinline__ int qdiv_fast(float w, float s, float r) {
+    const float t = w * r;
+    const float h = __builtin_floorf(t) + 0.5f;
+    const bool tie = __builtin_fmaf(h, s, -w) == 0.0f;
+    // v_cvt_i32_f32 converts NaN to 0 (and saturates, which |t| <= 128 never
+    // reaches): the reference's code for a NaN value
+    int c;
+    __asm__("v_cvt_i32_f32 %0, %1" : "=v"(c) : "v"(__builtin_rintf(tie ? h : t)));
+    return c;
+}
+
 // Scale and reciprocal used by qdiv: very small scales (bf16 subnormals
 // included) are moved up by 2^64 together with the values (exact powers of
 // two), so that 1 / s stays finite.
 struct QScale {
-    float s, r, up;  // scale (moved), its reciprocal, factor applied to w
+    float s, up;  // scale (moved), factor applied to w
+    // correctly rounded reciprocal (qdiv); the fast path uses v_rcp_f32
+    __device__ float r() const { return 1.0f / s; }
 };
 __device__ __forceinline__ QScale qscale(float s) {
     QScale q;
     q.up = s < 5.421010862427522e-20f ? 1.8446744073709552e19f : 1.0f;  // 2^-64, 2^64
     q.s = s * q.up;
-    q.r = 1.0f / q.s;
     return q;
 }
 
@@ -112,11 +135,19 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const uint16_t* __r
             c.r += 1;
         }
     };
+    // Unconditional buffer loads (a row past the end or a group past the
+    // row reads zero without a memory access): no branch around the load,
+    // so the wait before an item's use covers only that item's request.
     auto fetch = [&](const Cursor& c) {
-        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (!FAST) return make_uint4(0, 0, 0, 0);
+        // (the cursor is the same in every lane of the wave)
+        const int64_t r = (int64_t(__builtin_amdgcn_readfirstlane(uint32_t(c.r >> 32))) << 32) |
+                          int64_t(__builtin_amdgcn_readfirstlane(uint32_t(c.r)));
+        const bool rok = r < rows;
+        const rsrc_t rw = make_rsrc(w + (rok ? r : 0) * cols, rok ? cols * 2 : 0);
         const int64_t gg = c.qd * 4 + (lane >> 4);
-        if (FAST && c.r < rows && gg < G) raw = *reinterpret_cast<const uint4*>(w + c.r * cols + gg * kGroup + (lane & 15) * 8);
-        return raw;
+        const uint32_t off = gg < G ? uint32_t((gg * kGroup + (lane & 15) * 8) * 2) : kOob;
+        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
     };
     constexpr int QD = 2;
     Cursor cc{first / quads, first % quads}, fc = cc;
@@ -165,12 +196,26 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const uint16_t* __r
         const uint16_t sb = f32_to_bf16(amax > 0.0f ? amax / 127.0f : 1.0f);
         const QScale qs = qscale(bf16_to_f32(sb));
         uint32_t lo = 0, hi = 0;
+        // every group of the wave on the fast path (the usual case), or the
+        // general one (non-finite values, tiny scales) for the whole wave
+        const bool plain = qs.up == 1.0f && qs.s < 3.0e38f;
+        if (__builtin_amdgcn_ballot_w64(!plain) == 0) {
+            const float rf = __builtin_amdgcn_rcpf(qs.s);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r), -127, 127);
-            const uint32_t b = uint32_t(uint8_t(int8_t(c)));
-            if (i < 4) lo |= b << (8 * i);
-            else hi |= b << (8 * (i - 4));
+            for (int i = 0; i < 8; i++) {
+                const int c = clampi(qdiv_fast(v[i], qs.s, rf), -127, 127);
+                const uint32_t b = uint32_t(uint8_t(int8_t(c)));
+                if (i < 4) lo |= b << (8 * i);
+                else hi |= b << (8 * (i - 4));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r()), -127, 127);
+                const uint32_t b = uint32_t(uint8_t(int8_t(c)));
+                if (i < 4) lo |= b << (8 * i);
+                else hi |= b << (8 * (i - 4));
+            }
         }
         if (!gvalid) continue;
         if ((lane & 15) == 0) scales[r * G + g] = sb;
@@ -194,12 +239,24 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const uint16_t* __r
         mx = row16_maxf(mx);
         const uint16_t sb = f32_to_bf16(mx > mn ? (mx - mn) / 15.0f : 1.0f);
         const QScale qs = qscale(bf16_to_f32(sb));
-        const int z = clampi(qdiv(-mn * qs.up, qs.s, qs.r), 0, 15);
         uint32_t packed = 0;
+        int z;
+        const bool plain = qs.up == 1.0f && qs.s < 3.0e38f;
+        if (__builtin_amdgcn_ballot_w64(!plain) == 0) {
+            const float rf = __builtin_amdgcn_rcpf(qs.s);
+            z = clampi(qdiv_fast(-mn, qs.s, rf), 0, 15);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r) + z, 0, 15);
-            packed |= uint32_t(c) << (4 * i);
+            for (int i = 0; i < 8; i++) {
+                const int c = clampi(qdiv_fast(v[i], qs.s, rf) + z, 0, 15);
+                packed |= uint32_t(c) << (4 * i);
+            }
+        } else {
+            z = clampi(qdiv(-mn * qs.up, qs.s, qs.r()), 0, 15);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r()) + z, 0, 15);
+                packed |= uint32_t(c) << (4 * i);
+            }
         }
         if (!gvalid) continue;
         if ((lane & 15) == 0) {
@@ -214,6 +271,160 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const uint16_t* __r
             for (int i = 0; i < nvalid; i += 2) qb[i / 2] = uint8_t((packed >> (4 * i)) & 0xFF);
         }
     }
+    }
+}
+
+// Max / min over the 8 lanes of a half DPP row (one quantisation group of
+// quantize8_kernel): half-row mirror, then two quad permutations.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float oct_maxf(float v) {
+    v = __builtin_fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));   // quad_perm 2,3,0,1
+    return __builtin_fmaxf(v, dpp_f<0xB1>(v));  // quad_perm 1,0,3,2
+}
+__device__ __forceinline__ float oct_minf(float v) {
+    v = __builtin_fminf(v, dpp_f<0x141>(v));
+    v = __builtin_fminf(v, dpp_f<0x4E>(v));
+    return __builtin_fminf(v, dpp_f<0xB1>(v));
+}
+
+// quantize for cols % 128 == 0: the arithmetic of quantize_kernel with 8
+// lanes per group and 16 columns per lane (two 16-byte loads), so the
+// per-group work (reductions, the scale's two divisions and its bf16
+// rounding, addresses) is spread over twice the values.  Items are (row,
+// 8 groups); rows whose group count is not a multiple of 8 leave the
+// surplus lanes of their last item idle.
+template <int KIND>
+__global__ __launch_bounds__(kQThreads) void quantize8_kernel(const uint16_t* __restrict__ w, int64_t rows,
+                                                              int64_t cols, int64_t G, int64_t octs,
+                                                              uint8_t* __restrict__ q, uint16_t* __restrict__ scales,
+                                                              uint8_t* __restrict__ zeros) {
+    const int lane = threadIdx.x & 63, sub = lane & 7;
+    const int64_t items = rows * octs;
+    const int64_t stride = int64_t(gridDim.x) * (kQThreads / 64);
+    const int64_t first = int64_t(blockIdx.x) * (kQThreads / 64) + (threadIdx.x >> 6);
+    if (first >= items) return;
+    const int64_t sr = stride / octs, so = stride % octs;
+    struct Cursor {
+        int64_t r, o;
+    };
+    auto advance = [&](Cursor& c) {
+        c.r += sr;
+        c.o += so;
+        if (c.o >= octs) {
+            c.o -= octs;
+            c.r += 1;
+        }
+    };
+    struct Raw {
+        uint4 a, b;
+    };
+    auto fetch = [&](const Cursor& c) {
+        const int64_t r = (int64_t(__builtin_amdgcn_readfirstlane(uint32_t(c.r >> 32))) << 32) |
+                          int64_t(__builtin_amdgcn_readfirstlane(uint32_t(c.r)));
+        const bool rok = r < rows;
+        const rsrc_t rw = make_rsrc(w + (rok ? r : 0) * cols, rok ? cols * 2 : 0);
+        const int64_t g = c.o * 8 + (lane >> 3);
+        const uint32_t off = g < G ? uint32_t((g * kGroup + sub * 16) * 2) : kOob;
+        Raw x;
+        x.a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
+        x.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 16, 0));
+        return x;
+    };
+    Cursor cc{first / octs, first % octs}, fc = cc;
+    Raw r0 = fetch(fc);
+    advance(fc);
+    Raw r1 = fetch(fc);
+    advance(fc);
+    for (; cc.r < rows; advance(cc)) {
+        const Raw cur = r0;
+        r0 = r1;
+        r1 = fetch(fc);
+        advance(fc);
+        const int64_t r = cc.r;
+        const int64_t g = cc.o * 8 + (lane >> 3);
+        const bool gvalid = g < G;
+        float v[16];
+        {
+            const uint32_t wd[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                v[2 * i] = __uint_as_float(wd[i] << 16);
+                v[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
+            }
+        }
+        const int64_t c0 = g * kGroup + sub * 16;
+        if (KIND == 0) {
+            // amax = std::max(amax, fabs(v)): comparisons skip NaN (quiet or
+            // signalling; a maxNum would turn a signalling NaN into NaN)
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float a = __builtin_fabsf(v[i]);
+                amax = amax < a ? a : amax;
+            }
+            amax = oct_maxf(amax);
+            const uint16_t sb = f32_to_bf16(amax > 0.0f ? amax / 127.0f : 1.0f);
+            const QScale qs = qscale(bf16_to_f32(sb));
+            uint32_t d[4] = {0, 0, 0, 0};
+            const bool plain = qs.up == 1.0f && qs.s < 3.0e38f;
+            if (__builtin_amdgcn_ballot_w64(!plain) == 0) {
+                const float rf = __builtin_amdgcn_rcpf(qs.s);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int c = clampi(qdiv_fast(v[i], qs.s, rf), -127, 127);
+                    d[i / 4] |= uint32_t(uint8_t(int8_t(c))) << (8 * (i % 4));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r()), -127, 127);
+                    d[i / 4] |= uint32_t(uint8_t(int8_t(c))) << (8 * (i % 4));
+                }
+            }
+            if (!gvalid) continue;
+            if (sub == 0) scales[r * G + g] = sb;
+            *reinterpret_cast<uint4*>(q + r * cols + c0) = make_uint4(d[0], d[1], d[2], d[3]);
+        } else {
+            float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                mn = v[i] < mn ? v[i] : mn;
+                mx = mx < v[i] ? v[i] : mx;
+            }
+            mn = oct_minf(mn);
+            mx = oct_maxf(mx);
+            const uint16_t sb = f32_to_bf16(mx > mn ? (mx - mn) / 15.0f : 1.0f);
+            const QScale qs = qscale(bf16_to_f32(sb));
+            uint32_t d[2] = {0, 0};
+            int z;
+            const bool plain = qs.up == 1.0f && qs.s < 3.0e38f;
+            if (__builtin_amdgcn_ballot_w64(!plain) == 0) {
+                const float rf = __builtin_amdgcn_rcpf(qs.s);
+                z = clampi(qdiv_fast(-mn, qs.s, rf), 0, 15);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int c = clampi(qdiv_fast(v[i], qs.s, rf) + z, 0, 15);
+                    d[i / 8] |= uint32_t(c) << (4 * (i % 8));
+                }
+            } else {
+                z = clampi(qdiv(-mn * qs.up, qs.s, qs.r()), 0, 15);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r()) + z, 0, 15);
+                    d[i / 8] |= uint32_t(c) << (4 * (i % 8));
+                }
+            }
+            if (!gvalid) continue;
+            if (sub == 0) {
+                scales[r * G + g] = sb;
+                zeros[r * G + g] = uint8_t(z);
+            }
+            *reinterpret_cast<uint2*>(q + (r * cols + c0) / 2) = make_uint2(d[0], d[1]);
+        }
     }
 }
 
@@ -257,6 +468,13 @@ hipError_t launch_quantize(const uint16_t* w, int64_t rows, int64_t cols, int ki
     const int64_t cap = int64_t(device_cu_count()) * 8;
     const unsigned grid = unsigned(std::min<int64_t>((waves + 3) / 4, cap));
     const bool fast = cols % kGroup == 0;
+    if (fast) {
+        const int64_t octs = (G + 7) / 8;
+        const unsigned g8 = unsigned(std::min<int64_t>((rows * octs + 3) / 4, cap));
+        if (kind == 0) quantize8_kernel<0><<<g8, kQThreads, 0, stream>>>(w, rows, cols, G, octs, q, scales, zeros);
+        else quantize8_kernel<1><<<g8, kQThreads, 0, stream>>>(w, rows, cols, G, octs, q, scales, zeros);
+        return hipGetLastError();
+    }
     if (kind == 0) {
         if (fast) quantize_kernel<0, true><<<grid, kQThreads, 0, stream>>>(w, rows, cols, G, quads, q, scales, zeros);
         else quantize_kernel<0, false><<<grid, kQThreads, 0, stream>>>(w, rows, cols, G, quads, q, scales, zeros);

@@ -110,3 +110,27 @@ def test_quantize_ties_and_extreme_scales(kind):
     assert np.array_equal(q, rq)
     if kind == 1:
         assert np.array_equal(z, rz)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_quantize_nan_in_finite_groups_and_mixed_waves(kind):
+    """NaN values inside otherwise finite groups (the reference skips them
+    in the group statistics and codes them 0), in waves whose other groups
+    are ordinary, next to waves holding an infinite value or a tiny scale
+    (which take the general rounding path for the whole wave)."""
+    rng = np.random.default_rng(31 + kind)
+    rows, cols = 64, 1024
+    w = O.seeded_bf16(rng, (rows, cols), 0.05)
+    nan = np.uint16(0x7FC0)
+    for r in range(0, rows, 3):
+        w[r, rng.integers(0, cols, 5)] = nan
+    w[5, 700] = np.uint16(0x7F80)            # +inf
+    w[9, 130:258] = O.f32_to_bf16(np.full(128, 1e-30, np.float32))  # tiny scale group
+    w[9, 200] = nan
+    say("quantize NaN groups", kind)
+    q, s, z = gpu_quantize(w, kind)
+    rq, rs, rz = O.quantize(w, kind)
+    assert np.array_equal(s, rs)
+    assert np.array_equal(q, rq)
+    if kind == 1:
+        assert np.array_equal(z, rz)
