@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "iq_internal.h"
+#include "iq_limbs.h"
 
 namespace iq {
 
@@ -137,6 +138,34 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
                        : static_cast<const void*>(p.xb + (xok[i] ? m : 0) * p.K + kbeg);
         xcol[i] = XF32 ? (c & 15) * 4 : (c & 7) * 8;  // element offset inside the step
     }
+    // Fast paths: buffer resources over this tile's rows (wave-uniform), so
+    // every global load of the K loop is unconditional (rows past T or N and
+    // groups past the range read zero without a memory access).  A load
+    // under a branch makes the compiler wait for all outstanding loads
+    // before the next use of any of them, which would serialise the
+    // two-steps-ahead pipeline.
+    constexpr int XE = XF32 ? 4 : 2;
+    const int64_t xrows = p.T - m0 < BM ? p.T - m0 : BM;
+    const int64_t nrows = p.N - n0 < BN ? p.N - n0 : BN;
+    const rsrc_t rx = make_rsrc(XF32 ? static_cast<const void*>(p.xf + m0 * p.K)
+                                     : static_cast<const void*>(p.xb + m0 * p.K), xrows * p.K * XE);
+    const rsrc_t rw = make_rsrc(p.q + n0 * row_bytes, nrows * row_bytes);
+    const rsrc_t rsc = make_rsrc(p.scales + n0 * p.G, nrows * p.G * 2);
+    const rsrc_t rzp = make_rsrc(KIND == 1 ? p.zeros + n0 * p.G : nullptr, KIND == 1 ? nrows * p.G : 0);
+    uint32_t xoff[XCH], woff[WCH], zoff = kOob;
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+        const int c = tid + NT * i;
+        const int row = XF32 ? c >> 4 : c >> 3;
+        xoff[i] = uint32_t((int64_t(row) * p.K + kbeg + xcol[i]) * XE);
+    }
+#pragma unroll
+    for (int i = 0; i < WCH; i++) {
+        const int c = tid + NT * i;
+        const int row = KIND == 1 ? c >> 1 : c >> 2;
+        woff[i] = wok[i] ? uint32_t(row * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg) + wcol[i]) : kOob;
+        if (KIND == 1 && i == 0) zoff = wok[0] ? uint32_t(row * p.G + gbeg) : kOob;
+    }
 
     auto load_step = [&](Regs& rg, int kt) {
         uint4* xr = rg.xr;
@@ -147,9 +176,7 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
         for (int i = 0; i < XCH; i++) {
             const int64_t k = k0 + xcol[i];
             if (FASTX) {
-                xr[i] = xok[i] ? (XF32 ? *reinterpret_cast<const uint4*>(static_cast<const float*>(xrow[i]) + k)
-                                       : *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xrow[i]) + k))
-                               : make_uint4(0, 0, 0, 0);
+                xr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff[i] + uint32_t(k0 * XE), 0, 0));
             } else if (XF32) {
                 const float* xp = static_cast<const float*>(xrow[i]);
                 float f[4];
@@ -168,10 +195,11 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
 #pragma unroll
         for (int i = 0; i < WCH; i++) {
             const int64_t off = (KIND == 1 ? k0 / 2 : k0) + wcol[i];
-            if (!wok[i]) {
+            if (FASTW) {
+                wr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rw, woff[i] + uint32_t(KIND == 1 ? k0 / 2 : k0), 0, 0));
+            } else if (!wok[i]) {
                 wr[i] = make_uint4(0, 0, 0, 0);
-            } else if (FASTW) {
-                wr[i] = *reinterpret_cast<const uint4*>(wrow[i] + off);
             } else {
                 uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -180,7 +208,8 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
                 wr[i] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
-        zr = (KIND == 1 && wok[0]) ? zrow[k0 / kGroup] : 0u;
+        if (KIND == 1 && FASTW) zr = __builtin_amdgcn_raw_buffer_load_b8(rzp, zoff + uint32_t(k0 / kGroup), 0, 0);
+        else zr = (KIND == 1 && wok[0]) ? zrow[k0 / kGroup] : 0u;
     };
 
     auto store_step = [&](const Regs& rg, int buf) {
@@ -221,7 +250,11 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
         for (int i = 0; i < WCH; i++) {
             const int c = tid + NT * i;
             const uint32_t d[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
-            if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;  // int4 at BN = 64: half the threads
+            // (int4 at BN = 64 or 512 threads: half the threads have no chunk;
+            // the test is compiled only there, a divergent branch around the
+            // conversion would make every step wait for all its loads)
+            if constexpr (WCH0 * NT < BN * (KIND == 1 ? 2 : 4) || WCH0 == 0)
+                if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;
             if (KIND == 1) {
                 const int row = c >> 1, kc = c & 1;
                 const int z = int(zr);
@@ -276,12 +309,20 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
     // Scales of this lane's two output columns: group g's are requested a
     // group ahead (a load waited on at the group's close would stall every
     // second step).
-    auto load_scales = [&](int64_t g, float (&s)[NJ]) {
+    // (buffer loads: no branch around them, see above)
+    uint32_t soff[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; j++)
-            s[j] = (nval[j] && g < glen) ? bf16_to_f32(p.scales[ncol[j] * p.G + gbeg + g]) : 0.0f;
+    for (int j = 0; j < NJ; j++) soff[j] = uint32_t(((ncol[j] - n0) * p.G + gbeg) * 2);
+    // (the raw bf16 bits are kept until the group closes: converting right
+    // after the request would wait for it there)
+    auto load_scales = [&](int64_t g, uint16_t (&s)[NJ]) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t off = (nval[j] && g < glen) ? soff[j] + uint32_t(g * 2) : kOob;
+            s[j] = __builtin_amdgcn_raw_buffer_load_b16(rsc, off, 0, 0);
+        }
     };
-    float s_cur[NJ], s_nxt[NJ];
+    uint16_t s_cur[NJ], s_nxt[NJ];  // raw bf16 bits (no ALU op on a load until it is used)
     load_scales(0, s_cur);
     load_scales(1, s_nxt);
 
@@ -333,7 +374,8 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
 #pragma unroll
                 for (int i = 0; i < NI; i++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] = __builtin_fmaf(s_cur[j], P[i][j][r], acc[i][j][r]);
+                    for (int r = 0; r < 16; r++)
+                        acc[i][j][r] = __builtin_fmaf(__uint_as_float(uint32_t(s_cur[j]) << 16), P[i][j][r], acc[i][j][r]);
                 s_cur[j] = s_nxt[j];
             }
             load_scales(kt / 2 + 2, s_nxt);
@@ -531,29 +573,44 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || 
         wcol[i] = KIND == 1 ? (c & 1) * 16 : (c & 3) * 16;
         if (KIND == 1 && i == 0) zrow = p.zeros + (wok[i] ? n : 0) * p.G + gbeg;
     }
-    int64_t xoff[XCH];
-    bool xok[XCH];
+    // buffer resources over this tile's rows: every load of the K loop is
+    // unconditional (out-of-range rows read zero), so the waits before a
+    // step's use cover only that step's requests
+    const int64_t xrows = p.T - m0 < BM ? p.T - m0 : BM;
+    const int64_t nrows = p.N - n0 < BN ? p.N - n0 : BN;
+    const rsrc_t rah = make_rsrc(p.ah + m0 * p.K, xrows * p.K * 2);
+    const rsrc_t ral = make_rsrc(LO ? p.al + m0 * p.K : nullptr, LO ? xrows * p.K * 2 : 0);
+    const rsrc_t rw = make_rsrc(p.q + n0 * row_bytes, nrows * row_bytes);
+    const rsrc_t rsc = make_rsrc(p.scales + n0 * p.G, nrows * p.G * 2);
+    const rsrc_t rzp = make_rsrc(KIND == 1 ? p.zeros + n0 * p.G : nullptr, KIND == 1 ? nrows * p.G : 0);
+    uint32_t xoff[XCH], woff[WCH], zoff = kOob;
 #pragma unroll
     for (int i = 0; i < XCH; i++) {
         const int c = tid + NT * i;
-        const int64_t m = m0 + (c >> 3);
-        xok[i] = m < p.T;
-        xoff[i] = (xok[i] ? m : 0) * p.K + kbeg + (c & 7) * 8;
+        xoff[i] = uint32_t((int64_t(c >> 3) * p.K + kbeg + (c & 7) * 8) * 2);
     }
+#pragma unroll
+    for (int i = 0; i < WCH; i++) {
+        const int c = tid + NT * i;
+        const int row = KIND == 1 ? c >> 1 : c >> 2;
+        woff[i] = wok[i] ? uint32_t(row * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg) + wcol[i]) : kOob;
+        if (KIND == 1 && i == 0) zoff = wok[0] ? uint32_t(row * p.G + gbeg) : kOob;
+    }
+    (void)wrow;
+    (void)zrow;
 
     auto load_step = [&](Regs& rg, int kt) {
-        const int64_t k0 = int64_t(kt) * BK;
+        const uint32_t k0 = uint32_t(kt) * BK;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
-            rg.xr[i] = xok[i] ? *reinterpret_cast<const uint4*>(p.ah + xoff[i] + k0) : make_uint4(0, 0, 0, 0);
-            if (LO) rg.xl[i] = xok[i] ? *reinterpret_cast<const uint4*>(p.al + xoff[i] + k0) : make_uint4(0, 0, 0, 0);
+            rg.xr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rah, xoff[i] + k0 * 2, 0, 0));
+            if (LO) rg.xl[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ral, xoff[i] + k0 * 2, 0, 0));
         }
 #pragma unroll
-        for (int i = 0; i < WCH; i++) {
-            const int64_t off = (KIND == 1 ? k0 / 2 : k0) + wcol[i];
-            rg.wr[i] = wok[i] ? *reinterpret_cast<const uint4*>(wrow[i] + off) : make_uint4(0, 0, 0, 0);
-        }
-        rg.zr = (KIND == 1 && wok[0]) ? zrow[k0 / kGroup] : 0u;
+        for (int i = 0; i < WCH; i++)
+            rg.wr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rw, woff[i] + (KIND == 1 ? k0 / 2 : k0), 0, 0));
+        rg.zr = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rzp, zoff + k0 / kGroup, 0, 0) : 0u;
     };
 
     auto store_step = [&](const Regs& rg, int buf) {
@@ -566,7 +623,8 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || 
 #pragma unroll
         for (int i = 0; i < WCH; i++) {
             const int c = tid + NT * i;
-            if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;  // int4 with fewer chunks than threads
+            if constexpr (WCH0 == 0)  // int4 with fewer chunks than threads
+                if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;
             const uint32_t d[4] = {rg.wr[i].x, rg.wr[i].y, rg.wr[i].z, rg.wr[i].w};
             if (KIND == 1) {
                 const int row = c >> 1, kc = c & 1;
@@ -605,12 +663,17 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || 
         ncol[j] = n0 + wn * (32 * NJ) + j * 32 + (lane & 31);
         nval[j] = ncol[j] < p.N;
     }
-    auto load_scales = [&](int64_t g, float (&sc)[NJ]) {
+    uint32_t soff[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; j++)
-            sc[j] = (nval[j] && g < glen) ? bf16_to_f32(p.scales[ncol[j] * p.G + gbeg + g]) : 0.0f;
+    for (int j = 0; j < NJ; j++) soff[j] = uint32_t(((ncol[j] - n0) * p.G + gbeg) * 2);
+    auto load_scales = [&](int64_t g, uint16_t (&sc)[NJ]) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t off = (nval[j] && g < glen) ? soff[j] + uint32_t(g * 2) : kOob;
+            sc[j] = __builtin_amdgcn_raw_buffer_load_b16(rsc, off, 0, 0);
+        }
     };
-    float s_cur[NJ], s_nxt[NJ];
+    uint16_t s_cur[NJ], s_nxt[NJ];  // raw bf16 bits (no ALU op on a load until it is used)
     load_scales(0, s_cur);
     load_scales(1, s_nxt);
 
@@ -651,7 +714,8 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || 
 #pragma unroll
                 for (int i = 0; i < NI; i++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] = __builtin_fmaf(s_cur[j], P[i][j][r], acc[i][j][r]);
+                    for (int r = 0; r < 16; r++)
+                        acc[i][j][r] = __builtin_fmaf(__uint_as_float(uint32_t(s_cur[j]) << 16), P[i][j][r], acc[i][j][r]);
                 s_cur[j] = s_nxt[j];
             }
             load_scales(kt / 2 + 2, s_nxt);
