@@ -313,6 +313,41 @@ def bench_gemm(torch, ops, kind, T, N, K, reps=10, seed=5, fp32x=False):
     return ms, 2.0 * T * N * K / (ms * 1e-3) / 1e12
 
 
+def bench_quantize_model(torch, ops):
+    """Config 5b: the 7B model's 198 matrices (bf16 ~N(0, 0.02), seeded)
+    quantised by iq_quantize one after another, int8 and int4; returns per
+    kind the total time, bf16 GB/s read and bytes read + written per
+    second."""
+    shapes = []
+    for _ in range(L7):
+        shapes += [(NH7 * 128, H7), (KV7 * 128, H7), (KV7 * 128, H7), (H7, NH7 * 128), (I7, H7), (I7, H7), (H7, I7)]
+    shapes += [(V7, H7), (V7, H7)]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    ws = [(torch.randn(r, c, generator=g, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+          for r, c in shapes]
+    params = sum(r * c for r, c in shapes)
+    res = {"matrices": len(shapes), "params": params}
+    for kind, kn in ((0, "int8"), (1, "int4")):
+        outs = [ops.alloc_quant(kind, r, c) for r, c in shapes]
+        for w, o in zip(ws[:8], outs[:8]):
+            ops.quantize(w, kind, out=o)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for w, o in zip(ws, outs):
+            ops.quantize(w, kind, out=o)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        written = sum(o.nbytes() for o in outs)
+        res[kn] = {"ms": round(ms, 3), "bf16_read_GBps": round(2 * params / (ms * 1e-3) / 1e9, 1),
+                   "GBps": round((2 * params + written) / (ms * 1e-3) / 1e9, 1),
+                   "frac_hbm_peak": round((2 * params + written) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del outs
+    del ws
+    return res
+
+
 def bench_gemv_single(torch, ops, kind, N, K, M, copies, reps=200, seed=11):
     """One matrix shape rotated over `copies` distinct weight copies (beyond the
     MALL), iq_gemv per call, captured in a graph of `copies` launches."""
@@ -566,6 +601,12 @@ def main():
             nb = 2 * I7 * H7 + out.nbytes()
             detail[f"quantize_{kn}_18944x3584"] = {"us": round(ms * 1e3, 1), "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
         del w
+        # config 5b: every matrix of the 7B model (28 layers x q,k,v,o,gate,up,
+        # down, the embedding and the lm_head: 7.6 G parameters) quantised on
+        # the device back to back, inputs resident (distinct buffers, far past
+        # the MALL); tools/quantize.cpp's loop runs this on the CPU
+        detail["quantize_7b_all"] = bench_quantize_model(torch, ops)
+        torch.cuda.empty_cache()
         # prefill GEMM (config 5), int8, bf16 activations, T = 1024
         for (N, K, nm) in ((I7, H7, "gate_up"), (H7, I7, "down")):
             for kind, kn in ((0, "int8"), (1, "int4")):
