@@ -1313,9 +1313,9 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
         const TileSel ts = select_tile(p, ok ? tb + t : p.ntiles - 1);
         const int64_t left = ts.m.N - ts.row0;
         const int64_t rows = ok ? (left < 16 ? left : 16) : 0;
-        rq[t] = make_rsrc(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
-        rs[t] = make_rsrc(ts.m.scales + ts.row0 * G, rows * G * 2);
-        rz[t] = make_rsrc(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+        rq[t] = make_rsrc_wave(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
+        rs[t] = make_rsrc_wave(ts.m.scales + ts.row0 * G, rows * G * 2);
+        rz[t] = make_rsrc_wave(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
     }
     constexpr int NA = PK ? 4 : 8;  // A operands per group
     const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * NA * 1024);
@@ -1327,7 +1327,10 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
         int4v_t a[NA];      // [j][term], or [j] with both terms (PK)
         float4_t fx;        // 2^-k of activation rows 4q .. 4q + 3
         int4v_t w[T][WPG];
-        uint32_t s[T], z[T];
+        // raw bits: widening a loaded value right after the request would
+        // wait for every request made before it
+        uint16_t s[T];
+        uint8_t z[T];
     };
     auto load = [&](int g, GB& b) {
 #pragma unroll
@@ -1383,7 +1386,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
                     D = mfma16(__builtin_bit_cast(half8_t, b.a[2 * j + 1]), B[j], D);
                 }
             }
-            const float s = __uint_as_float(b.s[t] << 16);
+            const float s = __uint_as_float(uint32_t(b.s[t]) << 16);
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(D[r], s * b.fx[r], acc[t][r]);
         }
@@ -1449,9 +1452,9 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
     const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
     const int64_t left = ts.m.N - ts.row0;
     const int64_t rows = tok ? (left < 16 ? left : 16) : 0;
-    const rsrc_t rq = make_rsrc(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
-    const rsrc_t rs = make_rsrc(ts.m.scales + ts.row0 * G, rows * G * 2);
-    const rsrc_t rz = make_rsrc(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+    const rsrc_t rq = make_rsrc_wave(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
+    const rsrc_t rs = make_rsrc_wave(ts.m.scales + ts.row0 * G, rows * G * 2);
+    const rsrc_t rz = make_rsrc_wave(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
     const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * kHGroupBytes);
     const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
     const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
@@ -1465,7 +1468,8 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
     struct Slot {
         int4v_t a;
         int4v_t w[WPG];
-        uint32_t s, z;
+        uint16_t s;  // raw bits (see gemvh_kernel)
+        uint8_t z;
         float4_t fx;
     };
     auto load = [&](int g, Slot& b) {
@@ -1507,7 +1511,7 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
             Dv = mfma16(__builtin_bit_cast(half8_t, As[buf][(2 * j) * 64 + lane]), B[j], Dv);
             Dv = mfma16(__builtin_bit_cast(half8_t, As[buf][(2 * j + 1) * 64 + lane]), B[j], Dv);
         }
-        const float sc = __uint_as_float(b.s << 16);
+        const float sc = __uint_as_float(uint32_t(b.s) << 16);
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(Dv[r], sc * b.fx[r], acc[r]);
     };

@@ -185,4 +185,17 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
 }
 
+// make_rsrc for a base and size that are the same in every lane of the wave
+// but derived from values the compiler cannot prove uniform (a tile picked
+// out of a kernel-argument table): taken from the first lane, so the
+// resource lives in scalar registers.  A per-lane resource compiles to a
+// loop over its distinct values around every load that uses it.
+__device__ __forceinline__ rsrc_t make_rsrc_wave(const void* base, int64_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(b));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(b >> 32));
+    const int n = __builtin_amdgcn_readfirstlane(int(bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>((uint64_t(hi) << 32) | lo), 0, n, 0x00020000);
+}
+
 }  // namespace iq
