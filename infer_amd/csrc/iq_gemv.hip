@@ -44,6 +44,8 @@
 //  * gemvh (2..32 rows, f16 split activations): see gemvh_kernel.
 //  * gemvs (9..16 rows on very wide calls, the same split operands shared
 //    through LDS by 8 tiles): see gemvs_kernel.
+//  * gemvr (9..16 rows on wide or long-K calls: a K range of up to 8 groups
+//    requested at once, operands shared through LDS): see gemvr_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -1555,6 +1557,166 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
     }
 }
 
+// 9..16 rows, a K range of at most 8 groups per workgroup, everything
+// requested at once: workgroup = 8 waves on 8 consecutive 16-row tiles;
+// each thread requests its 16-byte share of the range's A operands (8 KiB
+// per group) and each lane its row's scales, zero points and weights for
+// the whole range (64 contiguous bytes of one row per group, 8 groups in
+// flight per wave), like the 1-row kernel; the shares go to LDS, one
+// barrier, and every wave multiplies its weights by the range's operands
+// group by group as they land.  The row factors of the range are staged in
+// LDS too.  S > 1 ranges write fp32 partial sums (gemvt_reduce_kernel).
+template <int KIND>
+__global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
+    constexpr int NG = 8;
+    constexpr int WPG = KIND == 1 ? 1 : 2;
+    __shared__ __attribute__((aligned(16))) int4v_t As[NG][512];
+    __shared__ __attribute__((aligned(16))) float4_t Fs[NG][4];
+    const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = int(p.G);
+    const int nrb = (p.ntiles + 7) / 8;
+    const int rb = int(blockIdx.x) % nrb, range = int(blockIdx.x) / nrb;
+    const int g0 = range * p.gs, gs = (g0 + p.gs < G ? g0 + p.gs : G) - g0;
+    const int tile = rb * 8 + wave;
+    const bool tok = tile < p.ntiles;
+    const TileSel ts = select_tile(p, tok ? tile : p.ntiles - 1);
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const int64_t left = ts.m.N - ts.row0;
+    const int64_t rows = tok ? (left < 16 ? left : 16) : 0;
+    const rsrc_t rq = make_rsrc_wave(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
+    const rsrc_t rs = make_rsrc_wave(ts.m.scales + ts.row0 * G, rows * G * 2);
+    const rsrc_t rz = make_rsrc_wave(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * kHGroupBytes);
+    const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
+    const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
+    const uint32_t vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
+
+    // 1. the range's A operand shares and row factors (shared), then this
+    //    lane's scales, zero points and weights; slots past the range read
+    //    zero without a memory access (buffer range check)
+    int4v_t av[NG];
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+        av[i] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                ra, uint32_t(tid * 16) + (i < gs ? 0u : kOob), (g0 + i) * kHGroupBytes, 0));
+    float4_t fv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (tid < 4 * NG)
+        fv = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rf, uint32_t((tid & 3) * 16) + ((tid >> 2) < gs ? 0u : kOob), (g0 + (tid >> 2)) * 64, 0));
+    uint16_t sv[NG];
+    uint8_t zv[NG];
+    int4v_t wv[NG][WPG];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const uint32_t o = i < gs ? 0u : kOob;
+        sv[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + o, (g0 + i) * 2, 0);
+        zv[i] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + o, g0 + i, 0) : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const uint32_t o = i < gs ? 0u : kOob;
+#pragma unroll
+        for (int h = 0; h < WPG; h++)
+            wv[i][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rq, vq + o, (g0 + i) * (KIND == 1 ? 64 : 128) + h * 16, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < NG; i++) As[i][tid] = av[i];
+    if (tid < 4 * NG) Fs[tid >> 2][tid & 3] = fv;
+    __syncthreads();
+
+    // 2. the groups in order, each as its weights land
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        if (i >= gs) continue;  // workgroup-uniform
+        half8_t B[4];
+        if (KIND == 1) {
+            const uint32_t zb = zpair_1024(zv[i]), zc = zpair_64(zv[i]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t o0, o1, o2, o3;
+                dq_int4_x8(uint32_t(wv[i][0][j]), zb, zc, o0, o1, o2, o3);
+                B[j] = pack_h8(o0, o1, o2, o3);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t l0, h0, l1, h1;
+                const int4v_t& w = wv[i][j >> 1];
+                dq_int8_x4(uint32_t(w[2 * (j & 1)]), l0, h0);
+                dq_int8_x4(uint32_t(w[2 * (j & 1) + 1]), l1, h1);
+                B[j] = pack_h8(l0, h0, l1, h1);
+            }
+        }
+        float4_t Dv = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            Dv = mfma16(__builtin_bit_cast(half8_t, As[i][(2 * j) * 64 + lane]), B[j], Dv);
+            Dv = mfma16(__builtin_bit_cast(half8_t, As[i][(2 * j + 1) * 64 + lane]), B[j], Dv);
+        }
+        const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
+        const float4_t fx = Fs[i][q];
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(Dv[r], sc * fx[r], acc[r]);
+    }
+    if (!tok) return;
+    const int64_t ld = int64_t(p.ntiles) * 16;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = 4 * q + r;
+        if (m >= p.M || ln >= rows) continue;
+        if (p.S == 1) {
+            const int64_t row = ts.row0 + ln;
+            ts.m.y[int64_t(m) * ts.m.N + row] = acc[r] + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
+        } else {
+            p.part[(int64_t(range) * p.M + m) * ld + int64_t(tile) * 16 + ln] = acc[r];
+        }
+    }
+}
+
+// gemvr on n matrices, M in 9..16 (false: the partial sums would not fit).
+bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
+                  hipStream_t stream, hipError_t* err) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    GemvParams p{};
+    int tiles = 0;
+    for (int i = 0; i < n; i++) {
+        p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i], W[i].rows, tiles};
+        tiles += int((W[i].rows + 15) / 16);
+    }
+    const int nrb = (tiles + 7) / 8;
+    // ranges of at most 8 groups, and enough workgroups for two per CU
+    const int want = 2 * device_cu_count();
+    int S = int((G + 7) / 8);
+    S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
+    const int gs = int((G + S - 1) / S);
+    S = int((G + gs - 1) / gs);
+    if (S > 1 && int64_t(S) * M * tiles * 16 > kPartialFloats) return false;
+    p.nmat = n;
+    p.K = K;
+    p.G = G;
+    p.xq = ws->xq;
+    p.meta = ws->xmeta;
+    p.M = M;
+    p.gs = gs;
+    p.S = S;
+    p.ntiles = tiles;
+    p.part = ws->partials;
+    const unsigned grid = unsigned(nrb * S);
+    if (W[0].kind == 1) gemvr_kernel<1><<<grid, 512, 0, stream>>>(p);
+    else gemvr_kernel<0><<<grid, 512, 0, stream>>>(p);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && S > 1) {
+        const int64_t outs = int64_t(M) * tiles * 16;
+        gemvt_reduce_kernel<<<unsigned((outs + 255) / 256), 256, 0, stream>>>(p);
+        e = hipGetLastError();
+    }
+    *err = e;
+    return true;
+}
+
 // gemvs on n matrices, M in 9..16, on the prepared split operands (false:
 // the split-K partials would not fit).
 bool launch_gemvs(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
@@ -1790,6 +1952,16 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;
         if (launch_gemvs(W, bias, y, n, M, ws, stream, &e)) return e;
+        return launch_gemvh(W, bias, y, n, M, ws, stream);
+    }
+    // 9..16 rows on wide or long-K layer calls (7B gate|up 2368 tiles, down
+    // G = 148): gemvr, every request of a K range made at once (int4 at 16
+    // rows: gate|up 41.5 -> 38.3, down 34.3 -> 30.7 us; narrow short-K
+    // calls such as q|k|v and o lose: 13.7 -> 18.9, 10.7 -> 18.4 us)
+    if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
+        hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
+        if (e != hipSuccess) return e;
+        if (launch_gemvr(W, bias, y, n, M, ws, stream, &e)) return e;
         return launch_gemvh(W, bias, y, n, M, ws, stream);
     }
     if (gemvh_preferred(K, M, total_tiles(W, n), W[0].kind)) {
