@@ -1566,11 +1566,13 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
 // barrier, and every wave multiplies its weights by the range's operands
 // group by group as they land.  The row factors of the range are staged in
 // LDS too.  S > 1 ranges write fp32 partial sums (gemvt_reduce_kernel).
-template <int KIND>
+template <int KIND, bool PK>
 __global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
     constexpr int NG = 8;
     constexpr int WPG = KIND == 1 ? 1 : 2;
-    __shared__ __attribute__((aligned(16))) int4v_t As[NG][512];
+    constexpr int GB = PK ? kHGroupBytes / 2 : kHGroupBytes;  // operand bytes per group
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    __shared__ __attribute__((aligned(16))) int8_t As[NG][kHGroupBytes];
     __shared__ __attribute__((aligned(16))) float4_t Fs[NG][4];
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1587,7 +1589,7 @@ __global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
     const rsrc_t rq = make_rsrc_wave(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
     const rsrc_t rs = make_rsrc_wave(ts.m.scales + ts.row0 * G, rows * G * 2);
     const rsrc_t rz = make_rsrc_wave(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
-    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * kHGroupBytes);
+    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * GB);
     const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
     const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
     const uint32_t vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
@@ -1596,10 +1598,14 @@ __global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
     //    lane's scales, zero points and weights; slots past the range read
     //    zero without a memory access (buffer range check)
     int4v_t av[NG];
+    u32x2_t ah[NG];
 #pragma unroll
-    for (int i = 0; i < NG; i++)
-        av[i] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                ra, uint32_t(tid * 16) + (i < gs ? 0u : kOob), (g0 + i) * kHGroupBytes, 0));
+    for (int i = 0; i < NG; i++) {
+        const uint32_t o = i < gs ? 0u : kOob;
+        if (PK) ah[i] = __builtin_amdgcn_raw_buffer_load_b64(ra, uint32_t(tid * 8) + o, (g0 + i) * GB, 0);
+        else av[i] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(ra, uint32_t(tid * 16) + o,
+                                                                                       (g0 + i) * GB, 0));
+    }
     float4_t fv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (tid < 4 * NG)
         fv = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
@@ -1622,7 +1628,10 @@ __global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
                                                        rq, vq + o, (g0 + i) * (KIND == 1 ? 64 : 128) + h * 16, 0));
     }
 #pragma unroll
-    for (int i = 0; i < NG; i++) As[i][tid] = av[i];
+    for (int i = 0; i < NG; i++) {
+        if (PK) *reinterpret_cast<u32x2_t*>(&As[i][tid * 8]) = ah[i];
+        else *reinterpret_cast<int4v_t*>(&As[i][tid * 16]) = av[i];
+    }
     if (tid < 4 * NG) Fs[tid >> 2][tid & 3] = fv;
     __syncthreads();
 
@@ -1651,17 +1660,29 @@ __global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
             }
         }
         float4_t Dv = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int4v_t* Ai = reinterpret_cast<const int4v_t*>(As[i]);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            Dv = mfma16(__builtin_bit_cast(half8_t, As[i][(2 * j) * 64 + lane]), B[j], Dv);
-            Dv = mfma16(__builtin_bit_cast(half8_t, As[i][(2 * j + 1) * 64 + lane]), B[j], Dv);
+            if (PK) {
+                // one operand per k-chunk: A rows 0..7 the hi, 8..15 the lo terms
+                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[j * 64 + lane]), B[j], Dv);
+            } else {
+                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[(2 * j) * 64 + lane]), B[j], Dv);
+                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[(2 * j + 1) * 64 + lane]), B[j], Dv);
+            }
         }
         const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
-        const float4_t fx = Fs[i][q];
+        // (PK: lanes of D rows 8..15 hold the lo terms of rows 0..7)
+        const float4_t fx = Fs[i][PK ? q & 1 : q];
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(Dv[r], sc * fx[r], acc[r]);
     }
-    if (!tok) return;
+    if (PK) {
+        // row m's lo-term sums sit 32 lanes above its hi-term sums
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] += __shfl_down(acc[r], 32, 64);
+    }
+    if (!tok || (PK && q >= 2)) return;
     const int64_t ld = int64_t(p.ntiles) * 16;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -1676,7 +1697,8 @@ __global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
     }
 }
 
-// gemvr on n matrices, M in 9..16 (false: the partial sums would not fit).
+// gemvr on n matrices, M in 2..16 (prepared by launch_xhprep: the packed
+// hi/lo operands up to 8 rows; false: the partial sums would not fit).
 bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
                   hipStream_t stream, hipError_t* err) {
     const int64_t K = W[0].cols, G = W[0].groups;
@@ -1705,8 +1727,13 @@ bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, 
     p.ntiles = tiles;
     p.part = ws->partials;
     const unsigned grid = unsigned(nrb * S);
-    if (W[0].kind == 1) gemvr_kernel<1><<<grid, 512, 0, stream>>>(p);
-    else gemvr_kernel<0><<<grid, 512, 0, stream>>>(p);
+    if (M <= 8) {
+        if (W[0].kind == 1) gemvr_kernel<1, true><<<grid, 512, 0, stream>>>(p);
+        else gemvr_kernel<0, true><<<grid, 512, 0, stream>>>(p);
+    } else {
+        if (W[0].kind == 1) gemvr_kernel<1, false><<<grid, 512, 0, stream>>>(p);
+        else gemvr_kernel<0, false><<<grid, 512, 0, stream>>>(p);
+    }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && S > 1) {
         const int64_t outs = int64_t(M) * tiles * 16;
@@ -1931,6 +1958,17 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
+    }
+    // 5..8 rows on very wide calls (the lm_head): gemvr on the packed hi/lo
+    // operands (7B lm_head 152064 x 3584 int8 at 5 / 8 rows: 166 -> 131 /
+    // 166 -> 158 us; on the layer shapes it only matched gemvt / gemvh, and
+    // at 2..4 rows the 1-row kernel's 4-row instance is far faster)
+    if (M >= 5 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
+        if (!ws->prep_copy) ws->invalidate_prep();
+        hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
+        if (e != hipSuccess) return e;
+        if (launch_gemvr(W, bias, y, n, M, ws, stream, &e)) return e;
+        return launch_gemvh(W, bias, y, n, M, ws, stream);
     }
     if (gemv1_rows_preferred(M, total_tiles(W, n), G)) {
         // the 1-row kernel converts x itself; 2..8 rows share each weight

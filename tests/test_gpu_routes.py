@@ -14,9 +14,11 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     bf16 and fp32 activations, int8 and int4;
   * gate|up (2 x 18944 x 3584) in one iq_gemv_multi call at 9, 12 and 16
     rows (the staged-limb gemvt kernel) and at 1 row;
-  * the int8 lm_head 152064 x 3584 at 1 and 16 rows, and wide calls
-    (>= 4096 tiles) at 9..16 rows (gemvs: operands shared through LDS over
-    8 tiles), both kinds, with ragged row counts and biases;
+  * the int8 lm_head 152064 x 3584 at 1, 5 and 16 rows, and wide calls
+    (>= 4096 tiles) at 5..16 rows (gemvr / gemvs: operands shared through
+    LDS over 8 tiles), both kinds, with ragged row counts and biases;
+  * gate|up at 9..16 rows and down at 16 rows take gemvr (a K range
+    requested at once);
   * every other 7B decode matrix at 16 rows.
 """
 import numpy as np
@@ -118,7 +120,7 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 5, 16])
 def test_lm_head_int8(M):
     """The int8 lm_head 152064 x 3584 (9504 tiles)."""
     rng = np.random.default_rng(152064 + M)
@@ -133,10 +135,11 @@ def test_lm_head_int8(M):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M", [9, 13, 16])
-def test_wide_call_9_to_16_rows(kind, M):
+@pytest.mark.parametrize("M", [5, 8, 9, 13, 16])
+def test_wide_call_5_to_16_rows(kind, M):
     """Over 4096 16-row tiles (here 65541 rows, the last tile ragged, and a
-    second matrix in the same call) at 9..16 rows: the gemvs route."""
+    second matrix in the same call) at 5..16 rows: the gemvr route on the
+    packed hi/lo operands (5..8 rows) and the gemvs route (9..16)."""
     rng = np.random.default_rng(4096 + 10 * M + kind)
     K = 1024
     Ws = [Packed(rng, 65541, K, kind), Packed(rng, 300, K, kind)]
