@@ -1566,14 +1566,14 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
 // barrier, and every wave multiplies its weights by the range's operands
 // group by group as they land.  The row factors of the range are staged in
 // LDS too.  S > 1 ranges write fp32 partial sums (gemvt_reduce_kernel).
-template <int KIND, bool PK>
-__global__ __launch_bounds__(512, 2) void gemvr_kernel(const GemvParams p) {
-    constexpr int NG = 8;
+template <int KIND, bool PK, int NG>
+__global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvParams p) {
     constexpr int WPG = KIND == 1 ? 1 : 2;
     constexpr int GB = PK ? kHGroupBytes / 2 : kHGroupBytes;  // operand bytes per group
     typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-    __shared__ __attribute__((aligned(16))) int8_t As[NG][kHGroupBytes];
+    __shared__ __attribute__((aligned(16))) int8_t As[NG][GB];
     __shared__ __attribute__((aligned(16))) float4_t Fs[NG][4];
+    static_assert(4 * NG <= 512, "row factors: one 16-byte load per thread");
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = int(p.G);
@@ -1709,9 +1709,11 @@ bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, 
         tiles += int((W[i].rows + 15) / 16);
     }
     const int nrb = (tiles + 7) / 8;
-    // ranges of at most 8 groups, and enough workgroups for two per CU
+    // ranges of at most 8 groups (16: one workgroup per CU, 7B gate|up at
+    // 16 rows 38.5 -> 53.9 us), and enough workgroups for two per CU
+    constexpr int ngr = 8;
     const int want = 2 * device_cu_count();
-    int S = int((G + 7) / 8);
+    int S = int((G + ngr - 1) / ngr);
     S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
     const int gs = int((G + S - 1) / S);
     S = int((G + gs - 1) / gs);
@@ -1728,11 +1730,11 @@ bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, 
     p.part = ws->partials;
     const unsigned grid = unsigned(nrb * S);
     if (M <= 8) {
-        if (W[0].kind == 1) gemvr_kernel<1, true><<<grid, 512, 0, stream>>>(p);
-        else gemvr_kernel<0, true><<<grid, 512, 0, stream>>>(p);
+        if (W[0].kind == 1) gemvr_kernel<1, true, 8><<<grid, 512, 0, stream>>>(p);
+        else gemvr_kernel<0, true, 8><<<grid, 512, 0, stream>>>(p);
     } else {
-        if (W[0].kind == 1) gemvr_kernel<1, false><<<grid, 512, 0, stream>>>(p);
-        else gemvr_kernel<0, false><<<grid, 512, 0, stream>>>(p);
+        if (W[0].kind == 1) gemvr_kernel<1, false, 8><<<grid, 512, 0, stream>>>(p);
+        else gemvr_kernel<0, false, 8><<<grid, 512, 0, stream>>>(p);
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && S > 1) {
