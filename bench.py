@@ -205,6 +205,18 @@ def kernel_roofline(torch, step, only_kind=None):
     return tot_b, tot_ms, n, per_shape
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the baseline's record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, model, seconds=10.0, threads=1):
     """oracle/iq_oracle.c iqo_linear_q_f32 (= src/forward.cpp:35-47 over
     dequant(), one thread) on layer matrices of the same model, until about
@@ -406,6 +418,11 @@ def bench_decode_chain(torch, ops, model, steps, warmup):
     out = {"us_per_step": round(ms * 1e3, 1), "GBps": round(wb / (ms * 1e-3) / 1e9, 1),
            "frac_hbm_peak": round(wb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "launches": len(step.chain.stages) + 1, "weight_bytes": int(wb),
+           # the quantised linears of one decode step per second (attention
+           # over a KV cache, sampling and the host are not in it; the
+           # reference's 7B int4 end to end: 126 tok/s on an RTX 5070 Ti,
+           # README.md:57)
+           "steps_per_s_linears_only": round(1e3 / ms, 1),
            "logits_finite": bool(torch.isfinite(step.logits).all().item())}
     del gr, step
     return out
@@ -556,7 +573,7 @@ def main():
         cpu_gbs, cpu_sample = cpu_baseline(torch, m4, args.cpu_seconds)
         cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": "oracle iqo_linear_q_f32 (src/forward.cpp:35-47 over dequant(), scalar fp32, "
-                         "1 thread) on the 7B int4 layer matrices at 1 row: " + cpu_sample}
+                         "1 thread) on the 7B int4 layer matrices at 1 row: " + cpu_sample + "; host CPU: " + cpu_model()}
         # the same port over the host's cores (at most 16, the box's share)
         nth = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
         cpu_all, cpu_all_sample = cpu_baseline(torch, m4, args.cpu_seconds / 2, threads=nth)
