@@ -559,19 +559,14 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || 
     };
     Regs r0, r1;
 
-    const uint8_t* wrow[WCH];
-    const uint8_t* zrow = nullptr;
     bool wok[WCH];
     int wcol[WCH];
 #pragma unroll
     for (int i = 0; i < WCH; i++) {
         const int c = tid + NT * i;
         const int row = KIND == 1 ? c >> 1 : c >> 2;
-        const int64_t n = n0 + row;
-        wok[i] = row < BN && n < p.N;
-        wrow[i] = p.q + (wok[i] ? n : 0) * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg);
+        wok[i] = row < BN && n0 + row < p.N;
         wcol[i] = KIND == 1 ? (c & 1) * 16 : (c & 3) * 16;
-        if (KIND == 1 && i == 0) zrow = p.zeros + (wok[i] ? n : 0) * p.G + gbeg;
     }
     // buffer resources over this tile's rows: every load of the K loop is
     // unconditional (out-of-range rows read zero), so the waits before a
@@ -596,9 +591,6 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || 
         woff[i] = wok[i] ? uint32_t(row * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg) + wcol[i]) : kOob;
         if (KIND == 1 && i == 0) zoff = wok[0] ? uint32_t(row * p.G + gbeg) : kOob;
     }
-    (void)wrow;
-    (void)zrow;
-
     auto load_step = [&](Regs& rg, int kt) {
         const uint32_t k0 = uint32_t(kt) * BK;
 #pragma unroll
