@@ -44,8 +44,8 @@
 //  * gemvh (2..32 rows, f16 split activations): see gemvh_kernel.
 //  * gemvs (9..16 rows on very wide calls, the same split operands shared
 //    through LDS by 8 tiles): see gemvs_kernel.
-//  * gemvr (9..16 rows on wide or long-K calls: a K range of up to 8 groups
-//    requested at once, operands shared through LDS): see gemvr_kernel.
+//  * gemvr (5..16 rows on wide or long-K calls: a K range of up to 8 groups
+//    requested at once, operands made from x in LDS): see gemvr_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -1225,6 +1225,34 @@ bool launch_gemvt(const QView* W, const uint16_t* const* bias, float* const* y, 
 // it reaches are NaN).  Every A operand is then one contiguous 1 KiB load.
 constexpr int kHGroupBytes = 4 * 2 * 64 * 16;  // prepared bytes per (block, group)
 
+// The f16 split of one lane's 8 values of a (row, group): all 16 lanes of a
+// DPP row hold the group's 128 values (the group maximum is taken across
+// them).  ho / lo: the hi and lo terms in operand slot order (perm8 for int4
+// weights); fac: 2^-k, or NaN when the group holds a non-finite value.
+template <bool PERM>
+__device__ __forceinline__ void xh_split8(const float (&v)[8], half8_t& ho, half8_t& lo, float& fac) {
+    uint32_t am = 0, nf = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
+        nf |= a >= 0x7F800000u ? 1u : 0u;
+        am = a > am ? a : am;
+    }
+    am = row16_max_u32(nf ? 0u : am);
+    const bool fin = row16_or(nf) == 0;
+    // amax = f 2^E, f in [0.5, 1): k = 15 - E puts amax 2^k in [2^14, 2^15)
+    const int k = (am > 0 && fin) ? 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(am)) : 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float s = fin ? __builtin_amdgcn_ldexpf(v[e], k) : 0.0f;
+        const _Float16 h = _Float16(s);
+        const int slot = PERM ? 2 * (e & 3) + (e >> 2) : e;
+        ho[slot] = h;
+        lo[slot] = _Float16(s - float(h));
+    }
+    fac = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
+}
+
 // PK (M <= 8): one A operand per k-chunk holds both terms, rows 0..7 the hi
 // and rows 8..15 the lo terms of the 8 activation rows (4 KiB per group,
 // half the operand bytes and MFMAs); the kernel adds the two halves of each
@@ -1242,50 +1270,23 @@ __global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x
     float v[8];
     load_x8<1>(x + int64_t(m < M ? m : 0) * K, (gvalid && m < M ? g : 0) * kGroup + j16 * 8,
                (gvalid && m < M) ? K : 0, v);
-    uint32_t am = 0, nf = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
-        nf |= a >= 0x7F800000u ? 1u : 0u;
-        am = a > am ? a : am;
-    }
-    am = row16_max_u32(nf ? 0u : am);
-    const bool fin = row16_or(nf) == 0;
-    // amax = f 2^E, f in [0.5, 1): k = 15 - E puts amax 2^k in [2^14, 2^15)
-    const int k = (am > 0 && fin) ? 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(am)) : 0;
-    _Float16 hi[8], lo[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float s = fin ? __builtin_amdgcn_ldexpf(v[e], k) : 0.0f;
-        const _Float16 h = _Float16(s);
-        hi[e] = h;
-        lo[e] = _Float16(s - float(h));
-    }
+    half8_t ho, lo2;
+    float fac;
+    xh_split8<PERM>(v, ho, lo2, fac);
     if (!gvalid) return;
-    _Float16 ho[8], lo2[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int slot = PERM ? 2 * (e & 3) + (e >> 2) : e;
-        ho[slot] = hi[e];
-        lo2[slot] = lo[e];
-    }
     const int b = m >> 4, i = m & 15, q = j16 >> 2, jj = j16 & 3;
     if (PK) {
         if (m >= 8) return;
         _Float16* base = xh + (g * (kHGroupBytes / 2)) / 2;
-        *reinterpret_cast<half8_t*>(base + (jj * 64 + i + 16 * q) * 8) =
-            half8_t{ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
-        *reinterpret_cast<half8_t*>(base + (jj * 64 + i + 8 + 16 * q) * 8) =
-            half8_t{lo2[0], lo2[1], lo2[2], lo2[3], lo2[4], lo2[5], lo2[6], lo2[7]};
+        *reinterpret_cast<half8_t*>(base + (jj * 64 + i + 16 * q) * 8) = ho;
+        *reinterpret_cast<half8_t*>(base + (jj * 64 + i + 8 + 16 * q) * 8) = lo2;
     } else {
         _Float16* base = xh + ((int64_t(b) * G + g) * kHGroupBytes) / 2;
         const int l = i + 16 * q;
-        *reinterpret_cast<half8_t*>(base + ((jj * 2 + 0) * 64 + l) * 8) =
-            half8_t{ho[0], ho[1], ho[2], ho[3], ho[4], ho[5], ho[6], ho[7]};
-        *reinterpret_cast<half8_t*>(base + ((jj * 2 + 1) * 64 + l) * 8) =
-            half8_t{lo2[0], lo2[1], lo2[2], lo2[3], lo2[4], lo2[5], lo2[6], lo2[7]};
+        *reinterpret_cast<half8_t*>(base + ((jj * 2 + 0) * 64 + l) * 8) = ho;
+        *reinterpret_cast<half8_t*>(base + ((jj * 2 + 1) * 64 + l) * 8) = lo2;
     }
-    if (j16 == 0) xfx[(int64_t(b) * G + g) * 16 + i] = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
+    if (j16 == 0) xfx[(int64_t(b) * G + g) * 16 + i] = fac;
 }
 
 // Workgroup = T consecutive 16-row tiles (of any of the call's matrices) x
@@ -1557,23 +1558,23 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
     }
 }
 
-// 9..16 rows, a K range of at most 8 groups per workgroup, everything
+// 5..16 rows, a K range of at most 8 groups per workgroup, everything
 // requested at once: workgroup = 8 waves on 8 consecutive 16-row tiles;
-// each thread requests its 16-byte share of the range's A operands (8 KiB
-// per group) and each lane its row's scales, zero points and weights for
-// the whole range (64 contiguous bytes of one row per group, 8 groups in
-// flight per wave), like the 1-row kernel; the shares go to LDS, one
-// barrier, and every wave multiplies its weights by the range's operands
-// group by group as they land.  The row factors of the range are staged in
-// LDS too.  S > 1 ranges write fp32 partial sums (gemvt_reduce_kernel).
+// each thread requests its share of the range's activations (fp32, 16 rows
+// x 8 groups, no preparation launch) and each lane its row's scales, zero
+// points and weights for the whole range (64 contiguous bytes of one row
+// per group, 8 groups in flight per wave), like the 1-row kernel.  While
+// the weights are in flight the workgroup makes the range's f16 split
+// operands and row factors in LDS exactly as xhprep_kernel makes them
+// (xh_split8; PK: the packed form), one barrier, and every wave multiplies
+// its weights by the range's operands group by group as they land.  S > 1
+// ranges write fp32 partial sums (gemvt_reduce_kernel).
 template <int KIND, bool PK, int NG>
 __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvParams p) {
     constexpr int WPG = KIND == 1 ? 1 : 2;
     constexpr int GB = PK ? kHGroupBytes / 2 : kHGroupBytes;  // operand bytes per group
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
     __shared__ __attribute__((aligned(16))) int8_t As[NG][GB];
     __shared__ __attribute__((aligned(16))) float4_t Fs[NG][4];
-    static_assert(4 * NG <= 512, "row factors: one 16-byte load per thread");
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = int(p.G);
@@ -1589,27 +1590,34 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     const rsrc_t rq = make_rsrc_wave(ts.m.q + ts.row0 * row_bytes, rows * row_bytes);
     const rsrc_t rs = make_rsrc_wave(ts.m.scales + ts.row0 * G, rows * G * 2);
     const rsrc_t rz = make_rsrc_wave(KIND == 1 ? ts.m.zeros + ts.row0 * G : nullptr, KIND == 1 ? rows * G : 0);
-    const rsrc_t ra = make_rsrc(p.xq, int64_t(G) * GB);
-    const rsrc_t rf = make_rsrc(p.meta, int64_t(G) * 64);
     const uint32_t vq = uint32_t(ln * row_bytes + q * (KIND == 1 ? 16 : 32));
     const uint32_t vs = uint32_t(ln * G) * 2, vz = uint32_t(ln * G);
 
-    // 1. the range's A operand shares and row factors (shared), then this
-    //    lane's scales, zero points and weights; slots past the range read
-    //    zero without a memory access (buffer range check)
-    int4v_t av[NG];
-    u32x2_t ah[NG];
+    // 1. the range's activations, then this lane's scales, zero points and
+    //    weights; slots past the range (and rows past M) read zero without
+    //    a memory access (buffer range check).  Activation task t = tid +
+    //    512 u is lane t % 16 of (row m, group i), 8 values.
+    constexpr int NX = (PK ? 8 : 16) * NG * 16 / 512;
+    static_assert(NX * 512 == (PK ? 8 : 16) * NG * 16, "whole DPP rows per task set");
+    float xv[NX][8];
+    {
+        const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
 #pragma unroll
-    for (int i = 0; i < NG; i++) {
-        const uint32_t o = i < gs ? 0u : kOob;
-        if (PK) ah[i] = __builtin_amdgcn_raw_buffer_load_b64(ra, uint32_t(tid * 8) + o, (g0 + i) * GB, 0);
-        else av[i] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(ra, uint32_t(tid * 16) + o,
-                                                                                       (g0 + i) * GB, 0));
+        for (int u = 0; u < NX; u++) {
+            const int t = tid + 512 * u, j16 = t & 15, pr = t >> 4;
+            const int m = PK ? pr & 7 : pr & 15, i = PK ? pr >> 3 : pr >> 4;
+            const uint32_t o = (i < gs && m < p.M)
+                                   ? uint32_t((int64_t(m) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
+                                   : kOob;
+            const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
+            const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xv[u][e] = a[e];
+                xv[u][4 + e] = b[e];
+            }
+        }
     }
-    float4_t fv = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (tid < 4 * NG)
-        fv = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                              rf, uint32_t((tid & 3) * 16) + ((tid >> 2) < gs ? 0u : kOob), (g0 + (tid >> 2)) * 64, 0));
     uint16_t sv[NG];
     uint8_t zv[NG];
     int4v_t wv[NG][WPG];
@@ -1627,15 +1635,29 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
             wv[i][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                        rq, vq + o, (g0 + i) * (KIND == 1 ? 64 : 128) + h * 16, 0));
     }
+    // 2. the operands and factors of the range (all 16 lanes of each
+    //    (row, group) together), then one barrier
 #pragma unroll
-    for (int i = 0; i < NG; i++) {
-        if (PK) *reinterpret_cast<u32x2_t*>(&As[i][tid * 8]) = ah[i];
-        else *reinterpret_cast<int4v_t*>(&As[i][tid * 16]) = av[i];
+    for (int u = 0; u < NX; u++) {
+        const int t = tid + 512 * u, j16 = t & 15, pr = t >> 4;
+        const int m = PK ? pr & 7 : pr & 15, i = PK ? pr >> 3 : pr >> 4;
+        const int qq = j16 >> 2, jj = j16 & 3;
+        half8_t ho, lo;
+        float fac;
+        xh_split8<KIND == 1>(xv[u], ho, lo, fac);
+        half8_t* dst = reinterpret_cast<half8_t*>(As[i]);
+        if (PK) {
+            dst[jj * 64 + m + 16 * qq] = ho;
+            dst[jj * 64 + m + 8 + 16 * qq] = lo;
+        } else {
+            dst[(jj * 2) * 64 + m + 16 * qq] = ho;
+            dst[(jj * 2 + 1) * 64 + m + 16 * qq] = lo;
+        }
+        if (j16 == 0) reinterpret_cast<float*>(Fs[i])[m] = fac;
     }
-    if (tid < 4 * NG) Fs[tid >> 2][tid & 3] = fv;
     __syncthreads();
 
-    // 2. the groups in order, each as its weights land
+    // 3. the groups in order, each as its weights land
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < NG; i++) {
@@ -1697,9 +1719,9 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     }
 }
 
-// gemvr on n matrices, M in 2..16 (prepared by launch_xhprep: the packed
-// hi/lo operands up to 8 rows; false: the partial sums would not fit).
-bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
+// gemvr on n matrices, M in 5..16, straight from x (false: the partial sums
+// would not fit).
+bool launch_gemvr(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
                   hipStream_t stream, hipError_t* err) {
     const int64_t K = W[0].cols, G = W[0].groups;
     GemvParams p{};
@@ -1721,8 +1743,7 @@ bool launch_gemvr(const QView* W, const uint16_t* const* bias, float* const* y, 
     p.nmat = n;
     p.K = K;
     p.G = G;
-    p.xq = ws->xq;
-    p.meta = ws->xmeta;
+    p.x = x;
     p.M = M;
     p.gs = gs;
     p.S = S;
@@ -1961,15 +1982,17 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         }
         return hipSuccess;
     }
-    // 5..8 rows on very wide calls (the lm_head): gemvr on the packed hi/lo
-    // operands (7B lm_head 152064 x 3584 int8 at 5 / 8 rows: 166 -> 131 /
-    // 166 -> 158 us; on the layer shapes it only matched gemvt / gemvh, and
-    // at 2..4 rows the 1-row kernel's 4-row instance is far faster)
-    if (M >= 5 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
+    // 5..8 rows on wide or long-K calls: gemvr on the packed hi/lo operands
+    // (7B int4 at 5 / 8 rows: gate|up 34.5 -> 28.7 / 35.1 -> 29.2, down
+    // 27.6 -> 24.0 / 27.4 -> 25.0 us against gemvt / gemvh; lm_head 152064 x
+    // 3584 int8: 166 -> 121 / 166 -> 155 us; at 2..4 rows the 1-row
+    // kernel's 4-row instance is far faster)
+    if (M >= 5 && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
+        hipError_t e = hipSuccess;
+        if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
         if (!ws->prep_copy) ws->invalidate_prep();
-        hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
+        e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;
-        if (launch_gemvr(W, bias, y, n, M, ws, stream, &e)) return e;
         return launch_gemvh(W, bias, y, n, M, ws, stream);
     }
     if (gemv1_rows_preferred(M, total_tiles(W, n), G)) {
@@ -1996,12 +2019,14 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     }
     // 9..16 rows on wide or long-K layer calls (7B gate|up 2368 tiles, down
     // G = 148): gemvr, every request of a K range made at once (int4 at 16
-    // rows: gate|up 41.5 -> 38.3, down 34.3 -> 30.7 us; narrow short-K
-    // calls such as q|k|v and o lose: 13.7 -> 18.9, 10.7 -> 18.4 us)
+    // rows: gate|up 41.5 -> 38.3, down 34.3 -> 28.6 us; narrow short-K
+    // calls such as q|k|v and o lose: 13.7 -> 18.9, 10.7 -> 18.4 us; the
+    // lm_head stays on gemvs above: 138 against 180 us)
     if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
-        hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
+        hipError_t e = hipSuccess;
+        if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
+        e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;
-        if (launch_gemvr(W, bias, y, n, M, ws, stream, &e)) return e;
         return launch_gemvh(W, bias, y, n, M, ws, stream);
     }
     if (gemvh_preferred(K, M, total_tiles(W, n), W[0].kind)) {

@@ -17,8 +17,9 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
   * the int8 lm_head 152064 x 3584 at 1, 5 and 16 rows, and wide calls
     (>= 4096 tiles) at 5..16 rows (gemvr / gemvs: operands shared through
     LDS over 8 tiles), both kinds, with ragged row counts and biases;
-  * gate|up at 9..16 rows and down at 16 rows take gemvr (a K range
-    requested at once);
+  * gate|up and down at 5..16 rows take gemvr (a K range requested at
+    once, the f16 split operands made from x inside the kernel), with a
+    non-finite activation in two rows;
   * every other 7B decode matrix at 16 rows.
 """
 import numpy as np
@@ -152,6 +153,29 @@ def test_wide_call_5_to_16_rows(kind, M):
     torch.cuda.synchronize()
     for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
         check_sampled(y, x, W, M, rng, f"wide[{i}] kind={kind} M={M}", bias_bits=bb)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [6, 12])
+def test_gemvr_nonfinite_rows(kind, M):
+    """gemvr (7B gate|up and down shapes at 6 and 12 rows): an inf in row 0
+    and a NaN in row 1 make every output of those rows non-finite; the
+    other rows match the oracle."""
+    rng = np.random.default_rng(7100 + 10 * M + kind)
+    for K, Ns in ((3584, (18944, 18944)), (18944, (3584,))):
+        Ws = [Packed(rng, N, K, kind) for N in Ns]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        x[0, K - 3] = np.inf
+        x[1, 200] = np.nan
+        ys = [out_buffer(M, W.rows) for W in Ws]
+        say("gemvr non-finite rows", kind, M, K, Ns)
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], None, M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y) in enumerate(zip(Ws, ys)):
+            got = y.detach().cpu().numpy().reshape(-1)[: M * W.rows].reshape(M, W.rows)
+            assert not np.any(np.isfinite(got[:2])), f"gemvr[{i}] K={K}: finite output in a non-finite row"
+            check_sampled(y[2 * W.rows:], x[2:], W, M - 2, rng,
+                          f"gemvr[{i}] K={K} kind={kind} M={M} rows 2..")
 
 
 @pytest.mark.parametrize("kind", [0, 1])
