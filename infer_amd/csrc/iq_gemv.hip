@@ -46,6 +46,8 @@
 //    through LDS by 8 tiles): see gemvs_kernel.
 //  * gemvr (5..16 rows on wide or long-K calls: a K range of up to 8 groups
 //    requested at once, operands made from x in LDS): see gemvr_kernel.
+//  * gemvq (9..16 rows on wide calls: gemvr's scheme on 32-row tiles and
+//    the 32 x 32 matrix instruction): see gemvq_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -1719,6 +1721,155 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     }
 }
 
+// 9..16 rows on v_mfma_f32_32x32x16_f16: like gemvr (a K range of at most
+// NG groups per workgroup, every request made at once, operands made from x
+// in LDS while the weights are in flight), but each wave takes 32 weight
+// rows (a 32-row tile of one matrix), and one A operand holds both terms of
+// all 16 activation rows (A rows 0..15 the hi, 16..31 the lo terms), so each
+// 1 KiB operand read from LDS feeds 32 weight rows instead of 16.  K order
+// inside a group: lane half h = l / 32 of chunk c (16 columns per MFMA)
+// covers columns 64 h + 8 c .. + 8 (int4 slots in perm8 order), so a lane's
+// weights of a group are 32 (int4) or 64 (int8) contiguous bytes of its
+// row.  D lane l, register r: A row 8 (r / 4) + 4 h + r % 4, weight row
+// l % 32; registers r and r + 8 hold the two terms of one activation row.
+// S > 1 ranges write fp32 partial sums in the 16-row tile order of the
+// other kernels (gemvt_reduce_kernel adds them).
+template <int KIND, int NG>
+__global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
+    constexpr int NW = KIND == 1 ? 2 : 4;  // 16-byte weight loads per lane and group
+    __shared__ __attribute__((aligned(16))) half8_t Aq[NG][8][64];  // [group][chunk][lane]
+    __shared__ __attribute__((aligned(16))) float Fq[NG][16];
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = int(p.G);
+    const int rb = int(blockIdx.x) % p.nrb, range = int(blockIdx.x) / p.nrb;
+    const int g0 = range * p.gs, gs = (g0 + p.gs < G ? g0 + p.gs : G) - g0;
+    // this wave's 32-row tile: matrix i holds tiles [t0, t0 + ceil(N / 32))
+    const int tile = rb * 8 + wave;
+    MatRef mr = p.mat[0];
+    int t0 = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxMulti; i++) {
+        if (i < p.nmat) {
+            if (tile >= tot) {
+                mr = p.mat[i];
+                t0 = tot;
+            }
+            tot += int((p.mat[i].N + 31) / 32);
+        }
+    }
+    const bool tok = tile < tot;
+    const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
+    const int64_t row0 = int64_t(tok ? tile - t0 : 0) * 32;
+    const int64_t left = mr.N - row0;
+    const int64_t rows = tok ? (left < 32 ? left : 32) : 0;
+    const rsrc_t rq = make_rsrc_wave(mr.q + row0 * row_bytes, rows * row_bytes);
+    const rsrc_t rs = make_rsrc_wave(mr.scales + row0 * G, rows * G * 2);
+    const rsrc_t rz = make_rsrc_wave(KIND == 1 ? mr.zeros + row0 * G : nullptr, KIND == 1 ? rows * G : 0);
+    const uint32_t vq = uint32_t(l32 * row_bytes + h * NW * 16);
+    const uint32_t vs = uint32_t(l32 * G) * 2, vz = uint32_t(l32 * G);
+
+    // 1. the range's activations (task t = tid + 512 u: lane t % 16 of
+    //    (row m, group i), 8 values), then this lane's scales, zero points
+    //    and weights; slots past the range and rows past M read zero
+    //    without a memory access (buffer range check)
+    constexpr int NX = 16 * NG * 16 / 512;
+    static_assert(NX * 512 == 16 * NG * 16, "whole DPP rows per task set");
+    float xv[NX][8];
+    {
+        const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
+#pragma unroll
+        for (int u = 0; u < NX; u++) {
+            const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = t >> 8;
+            const uint32_t o = (i < gs && m < p.M)
+                                   ? uint32_t((int64_t(m) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
+                                   : kOob;
+            const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
+            const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xv[u][e] = a[e];
+                xv[u][4 + e] = b[e];
+            }
+        }
+    }
+    uint16_t sv[NG];
+    uint8_t zv[NG];
+    int4v_t wv[NG][NW];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const uint32_t o = i < gs ? 0u : kOob;
+        sv[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + o, (g0 + i) * 2, 0);
+        zv[i] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + o, g0 + i, 0) : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const uint32_t o = i < gs ? 0u : kOob;
+#pragma unroll
+        for (int c = 0; c < NW; c++)
+            wv[i][c] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rq, vq + o, (g0 + i) * (KIND == 1 ? 64 : 128) + c * 16, 0));
+    }
+
+    // 2. the range's operands and factors (16 lanes per (row, group)):
+    //    octet j16 = 8 h' + c of row m goes to chunk c, lanes m + 32 h'
+    //    (hi) and m + 16 + 32 h' (lo); then one barrier
+#pragma unroll
+    for (int u = 0; u < NX; u++) {
+        const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = t >> 8;
+        half8_t ho, lo;
+        float fac;
+        xh_split8<KIND == 1>(xv[u], ho, lo, fac);
+        Aq[i][j16 & 7][m + 32 * (j16 >> 3)] = ho;
+        Aq[i][j16 & 7][m + 16 + 32 * (j16 >> 3)] = lo;
+        if (j16 == 0) Fq[i][m] = fac;
+    }
+    __syncthreads();
+
+    // 3. the groups in order, each as its weights land
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        if (i >= gs) continue;  // workgroup-uniform
+        float16_t D = {};
+        const uint32_t zb = zpair_1024(zv[i]), zc = zpair_64(zv[i]);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            half8_t B;
+            if (KIND == 1) {
+                uint32_t o0, o1, o2, o3;
+                dq_int4_x8(uint32_t(wv[i][c >> 2][c & 3]), zb, zc, o0, o1, o2, o3);
+                B = pack_h8(o0, o1, o2, o3);
+            } else {
+                uint32_t l0, h0, l1, h1;
+                const int4v_t& w = wv[i][c >> 1];
+                dq_int8_x4(uint32_t(w[2 * (c & 1)]), l0, h0);
+                dq_int8_x4(uint32_t(w[2 * (c & 1) + 1]), l1, h1);
+                B = pack_h8(l0, h0, l1, h1);
+            }
+            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[i][c][lane], B, D, 0, 0, 0);
+        }
+        const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
+        const float4_t f0 = *reinterpret_cast<const float4_t*>(&Fq[i][4 * h]);
+        const float4_t f1 = *reinterpret_cast<const float4_t*>(&Fq[i][8 + 4 * h]);
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+            acc[r] = __builtin_fmaf(D[r] + D[r + 8], sc * (r < 4 ? f0[r] : f1[r - 4]), acc[r]);
+    }
+    if (!tok || l32 >= rows) return;
+    const int64_t ld = int64_t(p.ntiles) * 16;
+    const int64_t row = row0 + l32;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+        if (m >= p.M) continue;
+        if (p.S == 1)
+            mr.y[int64_t(m) * mr.N + row] = acc[r] + (mr.bias ? bf16_to_f32(mr.bias[row]) : 0.0f);
+        else
+            p.part[(int64_t(range) * p.M + m) * ld + int64_t(mr.tile0) * 16 + row] = acc[r];
+    }
+}
+
 // gemvr on n matrices, M in 5..16, straight from x (false: the partial sums
 // would not fit).
 bool launch_gemvr(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
@@ -1757,6 +1908,51 @@ bool launch_gemvr(const float* x, const QView* W, const uint16_t* const* bias, f
         if (W[0].kind == 1) gemvr_kernel<1, false, 8><<<grid, 512, 0, stream>>>(p);
         else gemvr_kernel<0, false, 8><<<grid, 512, 0, stream>>>(p);
     }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && S > 1) {
+        const int64_t outs = int64_t(M) * tiles * 16;
+        gemvt_reduce_kernel<<<unsigned((outs + 255) / 256), 256, 0, stream>>>(p);
+        e = hipGetLastError();
+    }
+    *err = e;
+    return true;
+}
+
+// gemvq on n matrices, M in 9..16, straight from x (false: the partial sums
+// would not fit).
+bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
+                  Workspace* ws, hipStream_t stream, hipError_t* err) {
+    const int64_t K = W[0].cols, G = W[0].groups;
+    GemvParams p{};
+    int tiles = 0, t32 = 0;
+    for (int i = 0; i < n; i++) {
+        p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, bias[i], y[i], W[i].rows, tiles};
+        tiles += int((W[i].rows + 15) / 16);
+        t32 += int((W[i].rows + 31) / 32);
+    }
+    const int nrb = (t32 + 7) / 8;
+    // ranges of at most ngr groups (the weights of a range are held in
+    // registers: 64 per lane), and enough workgroups for two per CU
+    const int ngr = W[0].kind == 1 ? 6 : 4;
+    const int want = 2 * device_cu_count();
+    int S = int((G + ngr - 1) / ngr);
+    S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
+    const int gs = int((G + S - 1) / S);
+    S = int((G + gs - 1) / gs);
+    if (S > 1 && int64_t(S) * M * tiles * 16 > kPartialFloats) return false;
+    p.nmat = n;
+    p.K = K;
+    p.G = G;
+    p.x = x;
+    p.M = M;
+    p.gs = gs;
+    p.S = S;
+    p.nrb = nrb;
+    p.ntiles = tiles;
+    p.part = ws->partials;
+    const unsigned grid = unsigned(nrb * S);
+    if (W[0].kind == 1) gemvq_kernel<1, 6><<<grid, 512, 0, stream>>>(p);
+    else gemvq_kernel<0, 4><<<grid, 512, 0, stream>>>(p);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && S > 1) {
         const int64_t outs = int64_t(M) * tiles * 16;
@@ -2021,9 +2217,13 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // G = 148): gemvr, every request of a K range made at once (int4 at 16
     // rows: gate|up 41.5 -> 38.3, down 34.3 -> 28.6 us; narrow short-K
     // calls such as q|k|v and o lose: 13.7 -> 18.9, 10.7 -> 18.4 us; the
-    // lm_head stays on gemvs above: 138 against 180 us)
+    // lm_head stays on gemvs above: 138 against 180 us), and on wide calls
+    // gemvq, half the operand reads per weight (int4 gate|up at 12 / 16
+    // rows: 36.0 -> 31.2 / 38.3 -> 33.7 us; int8 44.1 -> 44.3, unchanged;
+    // down loses with its shorter K ranges: 28.8 -> 34.2)
     if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
         hipError_t e = hipSuccess;
+        if (total_tiles(W, n) >= 1024 && launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
         e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;

@@ -13,13 +13,15 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     tiles >= 2 x CUs, i.e. the 128 x 128 tile instance (NJ = 2, BM = 128),
     bf16 and fp32 activations, int8 and int4;
   * gate|up (2 x 18944 x 3584) in one iq_gemv_multi call at 9, 12 and 16
-    rows (the staged-limb gemvt kernel) and at 1 row;
+    rows (gemvq: 32-row tiles on the 32 x 32 matrix instruction, both terms
+    of all 16 rows in one operand) and at 1 row;
   * the int8 lm_head 152064 x 3584 at 1, 5 and 16 rows, and wide calls
     (>= 4096 tiles) at 5..16 rows (gemvr / gemvs: operands shared through
     LDS over 8 tiles), both kinds, with ragged row counts and biases;
-  * gate|up and down at 5..16 rows take gemvr (a K range requested at
-    once, the f16 split operands made from x inside the kernel), with a
-    non-finite activation in two rows;
+  * gate|up and down at 5..8 rows and down at 9..16 take gemvr (a K range
+    requested at once, the f16 split operands made from x inside the
+    kernel), gate|up at 9..16 gemvq, with a non-finite activation in two
+    rows;
   * every other 7B decode matrix at 16 rows.
 """
 import numpy as np
@@ -153,6 +155,28 @@ def test_wide_call_5_to_16_rows(kind, M):
     torch.cuda.synchronize()
     for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
         check_sampled(y, x, W, M, rng, f"wide[{i}] kind={kind} M={M}", bias_bits=bb)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [9, 16])
+def test_gemvq_ragged_matrices(kind, M):
+    """gemvq (1024..4095 16-row tiles at 9..16 rows) on matrices whose rows
+    are not a multiple of 32: 20005 + 309 + 48 rows in one call, with
+    biases, so the 32-row tiles of the second and third matrix start inside
+    the first one's last 16-row tile pair and the split-K partials of each
+    land in the 16-row tile order of the reduction."""
+    rng = np.random.default_rng(3232 + 10 * M + kind)
+    K = 1024
+    Ws = [Packed(rng, N, K, kind) for N in (20005, 309, 48)]
+    bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
+    bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("gemvq ragged", kind, M)
+    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, M, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
+        check_sampled(y, x, W, M, rng, f"gemvq[{i}] kind={kind} M={M}", bias_bits=bb)
 
 
 @pytest.mark.parametrize("kind", [0, 1])
