@@ -28,7 +28,7 @@
 // conditioning sum |w*x| (tests/test_ops_gpu.cu:199-206).  Non-finite
 // activations make the affected outputs NaN.
 //
-// Two kernels:
+// Kernels:
 //  * gemv1 (1 row, the decode step): workgroup = W waves on one tile of 16
 //    output rows, the waves split K (reduced through LDS, deterministic; no
 //    cross-workgroup traffic).  A wave requests all weight words, scales and
