@@ -79,17 +79,21 @@ __device__ __forceinline__ int qdiv(float w, float s, float r) {
 // qdiv for a group whose scale is finite, at least 2^-64 (not moved) and
 // positive, and whose values are finite or NaN: |w / s| <= 127 (int8) or
 // <= 15 (int4 range) so t is finite, and a NaN w gives 0, the reference's
-// result for it.  No per-value range test, no scaling by `up`.  r may be
-// v_rcp_f32's reciprocal (within 1 ulp of 1 / s): t = w r is then within
-// 2^-23 + 2^-24 < 2^-22 of q* relatively, inside qdiv's gap argument.
+// result for it.  No per-value range test, no scaling by `up`, and no tie
+// test: with r within one ulp of 1 / s (v_rcp_f32), t = w r and one
+// correction q = fma(fma(-t, s, w), r, t) give exactly the correctly
+// rounded fp32 quotient w / s for every pair of bf16 values whose ratio
+// lies in [2^-30, 2^10) (checked exhaustively over all significand pairs,
+// both signs and the three candidate reciprocals: tests/cpp/
+// quant_div_check.c); smaller ratios round to 0 either way.  rint(q) is
+// then lrint of the reference's quotient, ties to even included.
 __device__ __forceinline__ int qdiv_fast(float w, float s, float r) {
     const float t = w * r;
-    const float h = __builtin_floorf(t) + 0.5f;
-    const bool tie = __builtin_fmaf(h, s, -w) == 0.0f;
-    // v_cvt_i32_f32 converts NaN to 0 (and saturates, which |t| <= 128 never
+    const float q = __builtin_fmaf(__builtin_fmaf(-t, s, w), r, t);
+    // v_cvt_i32_f32 converts NaN to 0 (and saturates, which |q| <= 128 never
     // reaches): the reference's code for a NaN value
     int c;
-    __asm__("v_cvt_i32_f32 %0, %1" : "=v"(c) : "v"(__builtin_rintf(tie ? h : t)));
+    __asm__("v_cvt_i32_f32 %0, %1" : "=v"(c) : "v"(__builtin_rintf(q)));
     return c;
 }
 
