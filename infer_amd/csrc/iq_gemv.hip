@@ -2219,7 +2219,8 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // calls such as q|k|v and o lose: 13.7 -> 18.9, 10.7 -> 18.4 us; the
     // lm_head stays on gemvs above: 138 against 180 us), and on wide calls
     // gemvq, half the operand reads per weight (int4 gate|up at 12 / 16
-    // rows: 36.0 -> 31.2 / 38.3 -> 33.7 us; int8 44.1 -> 44.3, unchanged;
+    // rows: 36.0 -> 31.2 / 38.3 -> 33.7 us; int8 at 9 rows 40.2 -> 39.9,
+    // at 16 its partial sums do not fit and gemvr runs;
     // down loses with its shorter K ranges: 28.8 -> 34.2)
     if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
         hipError_t e = hipSuccess;
