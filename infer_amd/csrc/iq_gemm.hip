@@ -911,13 +911,14 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
     // 18944 at T = 64 / 256: 115 / 186 -> 58 / 170 us, but at T = 128 (a
     // narrow matrix, already split over K) 93 -> 103: kept at 128 rows there
     const bool short_t = T <= 64 || (T > 128 && T <= 256) || (T <= 128 && W.rows >= 8192);
-    // 256-row tiles (8 waves) for long bf16 prefills of int4 weights: each
-    // dequantised weight tile (nibble unpack + zero point, the costlier
-    // conversion) feeds twice the MFMAs.  7B at T = 1024: int4 gate|up 255 ->
-    // 221 us, down 327 -> 264 us; int8 gate|up 231 -> 260 us (slower: one
-    // 8-wave workgroup per CU leaves the step barriers uncovered), so int8
-    // keeps 128-row tiles.
-    const bool big = !x_f32 && fastw && fastx && T >= 512 && W.kind == 1;
+    // 256-row tiles (8 waves) for long bf16 prefills of narrow int4
+    // matrices: each dequantised weight tile (nibble unpack + zero point,
+    // the costlier conversion) feeds twice the MFMAs.  7B at T = 1024 with
+    // 256 / 128 rows: int4 down 259 / 275 us, int4 gate|up 235 / 208 us,
+    // int8 down 269 / 249 us (one 8-wave workgroup per CU leaves the step
+    // barriers uncovered, which costs more than the conversion saves on a
+    // wide matrix or with int8's cheaper conversion).
+    const bool big = !x_f32 && fastw && fastx && T >= 512 && W.kind == 1 && W.rows < 8192;
     const int bm = (short_t && fastw && fastx) ? 64 : (big ? 256 : 128);
     p.tiles_m = int((T + bm - 1) / bm);
     if (x_f32) {
