@@ -42,7 +42,7 @@
 //    adds them in range order, so the result is deterministic and no
 //    counter has to be cleared between launches.
 //  * gemvh (2..32 rows, f16 split activations): see gemvh_kernel.
-//  * gemvs (9..16 rows on very wide calls, the same split operands shared
+//  * gemvs (7..16 rows on very wide calls, the same split operands shared
 //    through LDS by 8 tiles): see gemvs_kernel.
 //  * gemvr (5..16 rows on wide or long-K calls: a K range of up to 8 groups
 //    requested at once, operands made from x in LDS): see gemvr_kernel.
@@ -1430,7 +1430,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
     }
 }
 
-// 9..16 rows on the prepared f16 split operands, the operands shared
+// 7..16 rows on the prepared f16 split operands (16-row blocks), shared
 // through LDS: workgroup = 8 waves on 8 consecutive 16-row tiles (wave w:
 // tile 8 b + w, over every matrix of the call) and one K range of groups
 // [g0, g1).  Per group the workgroup copies the group's 8 KiB of A operands
@@ -2006,14 +2006,17 @@ bool launch_gemvs(const QView* W, const uint16_t* const* bias, float* const* y, 
 }
 
 // f16 split preparation of x [M][K] (M <= kMaxRowsGemv, K % 128 == 0).
-hipError_t launch_xhprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream) {
+// pk: the packed form up to 8 rows (false: 16-row blocks at any M, the form
+// gemvs reads).
+hipError_t launch_xhprep(const float* x, int M, int64_t K, int kind, Workspace* ws, hipStream_t stream,
+                         bool pk = true) {
     const int64_t G = K / kGroup, quads = (G + 3) / 4;
     const int nb = (M + 15) / 16;
     const int64_t waves = int64_t(nb) * 16 * quads;
     const unsigned grid = unsigned((waves + 3) / 4);
     _Float16* xh = reinterpret_cast<_Float16*>(ws->xq);
     float* xfx = reinterpret_cast<float*>(ws->xmeta);
-    if (M <= 8) {
+    if (M <= 8 && pk) {
         if (kind == 1) xhprep_kernel<true, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
         else xhprep_kernel<false, true><<<grid, 256, 0, stream>>>(x, M, K, G, quads, nb, xh, xfx);
     } else {
@@ -2183,6 +2186,15 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // 27.6 -> 24.0 / 27.4 -> 25.0 us against gemvt / gemvh; lm_head 152064 x
     // 3584 int8: 166 -> 121 / 166 -> 155 us; at 2..4 rows the 1-row
     // kernel's 4-row instance is far faster)
+    // 7..8 rows on very wide calls (the lm_head): gemvs on the 16-row
+    // operand blocks (7B lm_head int8 at 7 / 8 rows: 163 -> 135 / 163 -> 138
+    // us; at 5 / 6 rows gemvr stays ahead, 121 / 124 against 137 / 138)
+    if (M >= 7 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
+        if (!ws->prep_copy) ws->invalidate_prep();
+        hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream, false);
+        if (e != hipSuccess) return e;
+        if (launch_gemvs(W, bias, y, n, M, ws, stream, &e)) return e;
+    }
     if (M >= 5 && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
         hipError_t e = hipSuccess;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;

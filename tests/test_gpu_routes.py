@@ -16,8 +16,9 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     rows (gemvq: 32-row tiles on the 32 x 32 matrix instruction, both terms
     of all 16 rows in one operand) and at 1 row;
   * the int8 lm_head 152064 x 3584 at 1, 5 and 16 rows, and wide calls
-    (>= 4096 tiles) at 5..16 rows (gemvr / gemvs: operands shared through
-    LDS over 8 tiles), both kinds, with ragged row counts and biases;
+    (>= 4096 tiles) at 5..16 rows (gemvr at 5..6, gemvs at 7..16: operands
+    shared through LDS over 8 tiles), both kinds, with ragged row counts and
+    biases;
   * gate|up and down at 5..8 rows and down at 9..16 take gemvr (a K range
     requested at once, the f16 split operands made from x inside the
     kernel), gate|up at 9..16 gemvq, with a non-finite activation in two
@@ -138,11 +139,12 @@ def test_lm_head_int8(M):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M", [5, 8, 9, 13, 16])
+@pytest.mark.parametrize("M", [5, 7, 8, 9, 13, 16])
 def test_wide_call_5_to_16_rows(kind, M):
     """Over 4096 16-row tiles (here 65541 rows, the last tile ragged, and a
     second matrix in the same call) at 5..16 rows: the gemvr route on the
-    packed hi/lo operands (5..8 rows) and the gemvs route (9..16)."""
+    packed hi/lo operands (5..6 rows) and the gemvs route on 16-row operand
+    blocks (7..16)."""
     rng = np.random.default_rng(4096 + 10 * M + kind)
     K = 1024
     Ws = [Packed(rng, 65541, K, kind), Packed(rng, 300, K, kind)]
