@@ -183,6 +183,28 @@ def test_gemvq_ragged_matrices(kind, M):
 
 @pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [6, 12])
+def test_in_kernel_operands_unaligned_x(kind, M):
+    """gemvr (6 rows) and gemvq (12 rows), which read fp32 x themselves, on
+    an activation block that starts 4 bytes past a 16-byte boundary (7B
+    gate|up in one call)."""
+    rng = np.random.default_rng(4444 + 10 * M + kind)
+    K = 3584
+    Ws = [Packed(rng, 18944, K, kind) for _ in range(2)]
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    buf = torch.zeros(M * K + 4, dtype=torch.float32, device="cuda")
+    xd = buf[1:1 + M * K]
+    xd.copy_(torch.from_numpy(x.reshape(-1)).cuda())
+    assert xd.data_ptr() % 16 == 4
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("in-kernel operands, unaligned x", kind, M)
+    ops.gemv_multi(xd, [W.view for W in Ws], None, M, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y) in enumerate(zip(Ws, ys)):
+        check_sampled(y, x, W, M, rng, f"unaligned x [{i}] kind={kind} M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [6, 12])
 def test_gemvr_nonfinite_rows(kind, M):
     """gemvr (7B gate|up and down shapes at 6 and 12 rows): an inf in row 0
     and a NaN in row 1 make every output of those rows non-finite; the
