@@ -21,7 +21,7 @@
  * arguments are rejected on the host (nothing was enqueued), or a positive
  * hipError_t when the HIP runtime reported an error.  No exception crosses
  * this boundary.  The library keeps one workspace (activation operands,
- * split-K partial sums; about 35 MB) per (device, stream) pair, allocated on
+ * split-K partial sums; about 83 MB) per (device, stream) pair, allocated on
  * the first call that needs it: calls on different streams may overlap, and
  * calls on one stream are ordered by the stream.  A stream under graph
  * capture cannot allocate: without its own workspace (iq_init_stream before

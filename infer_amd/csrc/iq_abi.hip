@@ -32,7 +32,7 @@ hipError_t create_workspace(Workspace* ws) {
     // limbs (3 B per value) or f16 hi + lo (4 B per value)
     const size_t xq = align256(size_t(kMaxRowsGemv) * gmax * 4 * kGroup);
     const size_t meta = align256(sizeof(int4) * gmax * kMaxRowsGemv);
-    const size_t part = align256(sizeof(float) * kPartialFloats);
+    const size_t part = align256(sizeof(float) * kStreamPartialFloats);
     const size_t total = xf + xq + meta + part;
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, total);
@@ -44,6 +44,7 @@ hipError_t create_workspace(Workspace* ws) {
     ws->xq = reinterpret_cast<int8_t*>(p + xf);
     ws->xmeta = reinterpret_cast<int4*>(p + xf + xq);
     ws->partials = reinterpret_cast<float*>(p + xf + xq + meta);
+    ws->part_floats = kStreamPartialFloats;
     ws->xq_bytes = xq;
     ws->xmeta_bytes = meta;
     return hipSuccess;
@@ -95,6 +96,7 @@ hipError_t static_workspace(Workspace** out) {
         w.xq = reinterpret_cast<int8_t*>(p);
         w.xmeta = reinterpret_cast<int4*>(p + kStaticXq);
         w.partials = reinterpret_cast<float*>(p + kStaticXq + kStaticMeta);
+        w.part_floats = kPartialFloats;
         w.xq_bytes = kStaticXq;
         w.xmeta_bytes = kStaticMeta;
         w.can_grow = false;

@@ -895,6 +895,10 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
         // 24 of three bf16 terms at 1.5x the MFMAs: 7B at T = 1024, gate
         // 18944 x 3584 int4 648 -> 440 us, down 1053 -> 681 us; T = 32:
         // 74 -> 50, 70 -> 48 us)
+        if (x_f32) {
+            hipError_t e = hipSuccess;
+            if (launch_gemm_rows(x_f32, W, bias, T, y, ws, stream, &e)) return e;
+        }
         if (x_f32 && W.cols % kGroup == 0 && xa % 16 == 0) return launch_gemmh(x_f32, W, bias, T, y, ws, stream);
     }
     GemmParams p;

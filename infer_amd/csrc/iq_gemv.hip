@@ -1733,12 +1733,15 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
 // row.  D lane l, register r: A row 8 (r / 4) + 4 h + r % 4, weight row
 // l % 32; registers r and r + 8 hold the two terms of one activation row.
 // S > 1 ranges write fp32 partial sums in the 16-row tile order of the
-// other kernels (gemvt_reduce_kernel adds them).
-template <int KIND, int NG>
+// other kernels (gemvt_reduce_kernel adds them).  MB = 2 (17..32 rows):
+// MB blocks of 16 activation rows, each group's dequantised weights (one
+// chunk at a time) multiplied by every block's operand before the next
+// chunk, so the weights are read and converted once for all the rows.
+template <int KIND, int NG, int MB>
 __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     constexpr int NW = KIND == 1 ? 2 : 4;  // 16-byte weight loads per lane and group
-    __shared__ __attribute__((aligned(16))) half8_t Aq[NG][8][64];  // [group][chunk][lane]
-    __shared__ __attribute__((aligned(16))) float Fq[NG][16];
+    __shared__ __attribute__((aligned(16))) half8_t Aq[MB][NG][8][64];  // [block][group][chunk][lane]
+    __shared__ __attribute__((aligned(16))) float Fq[MB][NG][16];
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = int(p.G);
@@ -1770,19 +1773,21 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     const uint32_t vs = uint32_t(l32 * G) * 2, vz = uint32_t(l32 * G);
 
     // 1. the range's activations (task t = tid + 512 u: lane t % 16 of
-    //    (row m, group i), 8 values), then this lane's scales, zero points
-    //    and weights; slots past the range and rows past M read zero
-    //    without a memory access (buffer range check)
-    constexpr int NX = 16 * NG * 16 / 512;
-    static_assert(NX * 512 == 16 * NG * 16, "whole DPP rows per task set");
+    //    (row 16 b + m, group i), 8 values, b = (t / 256) / NG, i = (t /
+    //    256) % NG), then this lane's scales, zero points and weights;
+    //    slots past the range and rows past M read zero without a memory
+    //    access (buffer range check)
+    constexpr int NX = MB * 16 * NG * 16 / 512;
+    static_assert(NX * 512 == MB * 16 * NG * 16, "whole DPP rows per task set");
     float xv[NX][8];
     {
         const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
 #pragma unroll
         for (int u = 0; u < NX; u++) {
-            const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = t >> 8;
-            const uint32_t o = (i < gs && m < p.M)
-                                   ? uint32_t((int64_t(m) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
+            const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG;
+            const int row = 16 * ((t >> 8) / NG) + m;
+            const uint32_t o = (i < gs && row < p.M)
+                                   ? uint32_t((int64_t(row) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
                                    : kOob;
             const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
             const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
@@ -1816,22 +1821,28 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     //    (hi) and m + 16 + 32 h' (lo); then one barrier
 #pragma unroll
     for (int u = 0; u < NX; u++) {
-        const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = t >> 8;
+        const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG, b = (t >> 8) / NG;
         half8_t ho, lo;
         float fac;
         xh_split8<KIND == 1>(xv[u], ho, lo, fac);
-        Aq[i][j16 & 7][m + 32 * (j16 >> 3)] = ho;
-        Aq[i][j16 & 7][m + 16 + 32 * (j16 >> 3)] = lo;
-        if (j16 == 0) Fq[i][m] = fac;
+        Aq[b][i][j16 & 7][m + 32 * (j16 >> 3)] = ho;
+        Aq[b][i][j16 & 7][m + 16 + 32 * (j16 >> 3)] = lo;
+        if (j16 == 0) Fq[b][i][m] = fac;
     }
     __syncthreads();
 
     // 3. the groups in order, each as its weights land
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[MB][8];
+#pragma unroll
+    for (int b = 0; b < MB; b++)
+#pragma unroll
+        for (int r = 0; r < 8; r++) acc[b][r] = 0.0f;
 #pragma unroll
     for (int i = 0; i < NG; i++) {
         if (i >= gs) continue;  // workgroup-uniform
-        float16_t D = {};
+        float16_t D[MB];
+#pragma unroll
+        for (int b = 0; b < MB; b++) D[b] = float16_t{};
         const uint32_t zb = zpair_1024(zv[i]), zc = zpair_64(zv[i]);
 #pragma unroll
         for (int c = 0; c < 8; c++) {
@@ -1847,26 +1858,33 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
                 dq_int8_x4(uint32_t(w[2 * (c & 1) + 1]), l1, h1);
                 B = pack_h8(l0, h0, l1, h1);
             }
-            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[i][c][lane], B, D, 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < MB; b++) D[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[b][i][c][lane], B, D[b], 0, 0, 0);
         }
         const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
-        const float4_t f0 = *reinterpret_cast<const float4_t*>(&Fq[i][4 * h]);
-        const float4_t f1 = *reinterpret_cast<const float4_t*>(&Fq[i][8 + 4 * h]);
 #pragma unroll
-        for (int r = 0; r < 8; r++)
-            acc[r] = __builtin_fmaf(D[r] + D[r + 8], sc * (r < 4 ? f0[r] : f1[r - 4]), acc[r]);
+        for (int b = 0; b < MB; b++) {
+            const float4_t f0 = *reinterpret_cast<const float4_t*>(&Fq[b][i][4 * h]);
+            const float4_t f1 = *reinterpret_cast<const float4_t*>(&Fq[b][i][8 + 4 * h]);
+#pragma unroll
+            for (int r = 0; r < 8; r++)
+                acc[b][r] = __builtin_fmaf(D[b][r] + D[b][r + 8], sc * (r < 4 ? f0[r] : f1[r - 4]), acc[b][r]);
+        }
     }
     if (!tok || l32 >= rows) return;
     const int64_t ld = int64_t(p.ntiles) * 16;
     const int64_t row = row0 + l32;
 #pragma unroll
-    for (int r = 0; r < 8; r++) {
-        const int m = 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m >= p.M) continue;
-        if (p.S == 1)
-            mr.y[int64_t(m) * mr.N + row] = acc[r] + (mr.bias ? bf16_to_f32(mr.bias[row]) : 0.0f);
-        else
-            p.part[(int64_t(range) * p.M + m) * ld + int64_t(mr.tile0) * 16 + row] = acc[r];
+    for (int b = 0; b < MB; b++) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const int m = 16 * b + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (m >= p.M) continue;
+            if (p.S == 1)
+                mr.y[int64_t(m) * mr.N + row] = acc[b][r] + (mr.bias ? bf16_to_f32(mr.bias[row]) : 0.0f);
+            else
+                p.part[(int64_t(range) * p.M + m) * ld + int64_t(mr.tile0) * 16 + row] = acc[b][r];
+        }
     }
 }
 
@@ -1918,8 +1936,20 @@ bool launch_gemvr(const float* x, const QView* W, const uint16_t* const* bias, f
     return true;
 }
 
-// gemvq on n matrices, M in 9..16, straight from x (false: the partial sums
-// would not fit).
+// 17..32 rows on gemvq's two 16-row blocks instead of the GEMM's 64-row
+// tiles, for wide calls and long rows (7B, fp32 activations, int8 / int4 at
+// 17 / 32 rows: gate 18944 x 3584 43.9 -> 29.9 / 48.7 -> 34.7 us, down 3584
+// x 18944 43.3 -> 35.8 / 46.3 -> 38.1 us); narrower calls with shorter rows
+// stay on the GEMM (1.5B down 1536 x 8960 at 17 rows 22.9 against 30.1 us;
+// 7B o 18.6 against 20.2), and so do 33..64 rows (ranges of 2 groups: their
+// partial sums cost more than the tiles save, 7B gate at 48 rows 50.0 ->
+// 51.3 us).
+bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K) {
+    return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 1024 || K / kGroup >= 128);
+}
+
+// gemvq on n matrices, M in 9..32, straight from x (false: M out of range,
+// or the partial sums would not fit the workspace's capacity).
 bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                   Workspace* ws, hipStream_t stream, hipError_t* err) {
     const int64_t K = W[0].cols, G = W[0].groups;
@@ -1931,15 +1961,18 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
         t32 += int((W[i].rows + 31) / 32);
     }
     const int nrb = (t32 + 7) / 8;
+    if (M < 9 || M > 32) return false;
     // ranges of at most ngr groups (the weights of a range are held in
-    // registers: 64 per lane), and enough workgroups for two per CU
-    const int ngr = W[0].kind == 1 ? 6 : 4;
+    // registers: 64 per lane at one row block; the operands of 2 blocks x 4
+    // groups fill 64 KiB of LDS), and enough workgroups for two per CU
+    const int mb = M <= 16 ? 1 : 2;
+    const int ngr = mb == 2 ? 4 : (W[0].kind == 1 ? 6 : 4);
     const int want = 2 * device_cu_count();
     int S = int((G + ngr - 1) / ngr);
     S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
     const int gs = int((G + S - 1) / S);
     S = int((G + gs - 1) / gs);
-    if (S > 1 && int64_t(S) * M * tiles * 16 > kPartialFloats) return false;
+    if (S > 1 && int64_t(S) * M * tiles * 16 > ws->part_floats) return false;
     p.nmat = n;
     p.K = K;
     p.G = G;
@@ -1951,8 +1984,13 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
     p.ntiles = tiles;
     p.part = ws->partials;
     const unsigned grid = unsigned(nrb * S);
-    if (W[0].kind == 1) gemvq_kernel<1, 6><<<grid, 512, 0, stream>>>(p);
-    else gemvq_kernel<0, 4><<<grid, 512, 0, stream>>>(p);
+    if (mb == 1) {
+        if (W[0].kind == 1) gemvq_kernel<1, 6, 1><<<grid, 512, 0, stream>>>(p);
+        else gemvq_kernel<0, 4, 1><<<grid, 512, 0, stream>>>(p);
+    } else {
+        if (W[0].kind == 1) gemvq_kernel<1, 4, 2><<<grid, 512, 0, stream>>>(p);
+        else gemvq_kernel<0, 4, 2><<<grid, 512, 0, stream>>>(p);
+    }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && S > 1) {
         const int64_t outs = int64_t(M) * tiles * 16;
@@ -2170,6 +2208,10 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
+    if (gemvq_rows_preferred(M, total_tiles(W, n), K)) {
+        hipError_t e = hipSuccess;
+        if (launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
+    }
     if (M > 16) {
         // 17..32 rows: the prefill GEMM's 64-row tiles beat two 16-row GEMV
         // blocks (1.5B gate 8960 x 1536 at 32 rows: 23.0 -> 16.2 us int8;
@@ -2250,6 +2292,12 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     hipError_t e = launch_xprep_limbs(x, M, K, W[0].kind, ws, stream);
     if (e != hipSuccess) return e;
     return launch_batched_multi(W, bias, y, n, M, ws, stream);
+}
+
+bool launch_gemm_rows(const float* x, const QView& W, const uint16_t* bias, int64_t T, float* y, Workspace* ws,
+                      hipStream_t stream, hipError_t* err) {
+    if (!gemvq_rows_preferred(T, int((W.rows + 15) / 16), W.cols)) return false;
+    return launch_gemvq(x, &W, &bias, &y, 1, int(T), ws, stream, err);
 }
 
 hipError_t launch_gemv(const float* x, const QView& W, const uint16_t* bias, int M, float* y,

@@ -29,7 +29,8 @@ struct Workspace {
     int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs, or the f16 hi/lo
                                // A operands [kMaxRowsGemv/16][kMaxKp/128][8 KiB] (gemvh)
     int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, sum X0, 256 sum X1 + sum X2, 0}
-    float* partials = nullptr; // kPartialFloats
+    float* partials = nullptr; // part_floats (>= kPartialFloats)
+    int64_t part_floats = 0;   // capacity of partials
     size_t xq_bytes = 0, xmeta_bytes = 0;
     // the prefill GEMM's prepared activations when they exceed xq (grown on
     // demand; null in the static workspace)
@@ -54,7 +55,8 @@ struct Workspace {
 
 constexpr int kMaxRowsGemv = 32;            // GpuBatch::kMaxRows (kernels/batch_gpu.h:80)
 constexpr int64_t kMaxKp = 131072;          // padded K limit of the GEMV
-constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K partials
+constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K partials (every workspace)
+constexpr int64_t kStreamPartialFloats = int64_t(16) << 20;  // 64 MiB in a per-stream workspace
 
 // Returns the workspace of (current device, stream), allocating it on first
 // use.  Every stream has its own, so calls on different streams never share
@@ -85,6 +87,11 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
                              int n, int M, Workspace* ws, hipStream_t stream);
 // Uses the workspace for the prepared fp16 activations and the split-K
 // partials (short T splits K over workgroups).
+// 17..32 activation rows (fp32) on gemvq's two 16-row blocks, the f16
+// split made in the kernel, where that beats the GEMM's tiles (wide or
+// long-K matrices); false: not applicable, nothing launched.
+bool launch_gemm_rows(const float* x, const QView& W, const uint16_t* bias, int64_t T, float* y, Workspace* ws,
+                      hipStream_t stream, hipError_t* err);
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
                        const uint16_t* bias, int64_t T, float* y, Workspace* ws, hipStream_t stream);
 // Room for the prefill GEMM's prepared activations: T x K fp16 (x 2 with

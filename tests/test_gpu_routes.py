@@ -19,6 +19,8 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     (>= 4096 tiles) at 5..16 rows (gemvr at 5..6, gemvs at 7..16: operands
     shared through LDS over 8 tiles), both kinds, with ragged row counts and
     biases;
+  * 17..32 rows on gemvq's two 16-row blocks (7B gate|up and down, ragged
+    matrices, the fp32 GEMM entry);
   * gate|up and down at 5..8 rows and down at 9..16 take gemvr (a K range
     requested at once, the f16 split operands made from x inside the
     kernel), gate|up at 9..16 gemvq, with a non-finite activation in two
@@ -179,6 +181,38 @@ def test_gemvq_ragged_matrices(kind, M):
     torch.cuda.synchronize()
     for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
         check_sampled(y, x, W, M, rng, f"gemvq[{i}] kind={kind} M={M}", bias_bits=bb)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [17, 24, 32])
+def test_gemvq_two_row_blocks(kind, M):
+    """17..32 rows on gemvq's two 16-row blocks: 7B gate|up (one call) and
+    down (K = 18944) with biases, ragged matrices (20005 + 309 + 48 rows,
+    K = 1024) in one call, and the fp32 GEMM entry (iq_gemm) on 7B gate."""
+    rng = np.random.default_rng(1732 + 10 * M + kind)
+    cases = ((3584, (18944, 18944)), (18944, (3584,)), (1024, (20005, 309, 48)))
+    for K, Ns in cases:
+        Ws = [Packed(rng, N, K, kind) for N in Ns]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        bias_bits = [O.seeded_bf16(rng, (N,), 0.5) for N in Ns]
+        bds = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+        ys = [out_buffer(M, W.rows) for W in Ws]
+        say("gemvq two blocks", kind, M, K, Ns)
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bds, M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y) in enumerate(zip(Ws, ys)):
+            check_sampled(y, x, W, M, rng, f"gemvq M={M} K={K} N={Ns[i]} kind={kind}", bias_bits[i])
+    K, N = 3584, 18944
+    W = Packed(rng, N, K, kind)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[M - 1, 77] = np.inf
+    y = out_buffer(M, N)
+    say("gemvq via iq_gemm", kind, M)
+    ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+    torch.cuda.synchronize()
+    got = y.detach().cpu().numpy().reshape(-1)[: M * N].reshape(M, N)
+    assert not np.any(np.isfinite(got[M - 1])), "finite output in the non-finite row"
+    check_sampled(y[: (M - 1) * N].contiguous(), x[: M - 1], W, M - 1, rng, f"iq_gemm M={M} kind={kind}")
 
 
 @pytest.mark.parametrize("kind", [0, 1])
