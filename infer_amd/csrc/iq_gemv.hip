@@ -46,8 +46,9 @@
 //    through LDS by 8 tiles): see gemvs_kernel.
 //  * gemvr (5..16 rows on wide or long-K calls: a K range of up to 8 groups
 //    requested at once, operands made from x in LDS): see gemvr_kernel.
-//  * gemvq (9..16 rows on wide calls: gemvr's scheme on 32-row tiles and
-//    the 32 x 32 matrix instruction): see gemvq_kernel.
+//  * gemvq (9..16 rows on wide int4 calls, 17..32 rows on wide or long-K
+//    calls: gemvr's scheme on 32-row tiles and the 32 x 32 matrix
+//    instruction, up to two 16-row blocks): see gemvq_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -2273,12 +2274,13 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // calls such as q|k|v and o lose: 13.7 -> 18.9, 10.7 -> 18.4 us; the
     // lm_head stays on gemvs above: 138 against 180 us), and on wide calls
     // gemvq, half the operand reads per weight (int4 gate|up at 12 / 16
-    // rows: 36.0 -> 31.2 / 38.3 -> 33.7 us; int8 at 9 rows 40.2 -> 39.9,
-    // at 16 its partial sums do not fit and gemvr runs;
+    // rows: 36.0 -> 31.2 / 38.3 -> 33.7 us; int8 stays on gemvr: 40.2
+    // against 39.9 at 9 rows, 44.1 against 45.3 at 16;
     // down loses with its shorter K ranges: 28.8 -> 34.2)
     if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
         hipError_t e = hipSuccess;
-        if (total_tiles(W, n) >= 1024 && launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
+        if (W[0].kind == 1 && total_tiles(W, n) >= 1024 && launch_gemvq(x, W, bias, y, n, M, ws, stream, &e))
+            return e;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
         e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;

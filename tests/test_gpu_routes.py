@@ -13,8 +13,8 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     tiles >= 2 x CUs, i.e. the 128 x 128 tile instance (NJ = 2, BM = 128),
     bf16 and fp32 activations, int8 and int4;
   * gate|up (2 x 18944 x 3584) in one iq_gemv_multi call at 9, 12 and 16
-    rows (gemvq: 32-row tiles on the 32 x 32 matrix instruction, both terms
-    of all 16 rows in one operand) and at 1 row;
+    rows (int4 on gemvq: 32-row tiles on the 32 x 32 matrix instruction,
+    both terms of all 16 rows in one operand; int8 on gemvr) and at 1 row;
   * the int8 lm_head 152064 x 3584 at 1, 5 and 16 rows, and wide calls
     (>= 4096 tiles) at 5..16 rows (gemvr at 5..6, gemvs at 7..16: operands
     shared through LDS over 8 tiles), both kinds, with ragged row counts and
@@ -164,8 +164,8 @@ def test_wide_call_5_to_16_rows(kind, M):
 @pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [9, 16])
 def test_gemvq_ragged_matrices(kind, M):
-    """gemvq (1024..4095 16-row tiles at 9..16 rows) on matrices whose rows
-    are not a multiple of 32: 20005 + 309 + 48 rows in one call, with
+    """gemvq (int4; int8 takes gemvr) at 1024..4095 16-row tiles and 9..16
+    rows, on matrices whose rows are not a multiple of 32: 20005 + 309 + 48 rows in one call, with
     biases, so the 32-row tiles of the second and third matrix start inside
     the first one's last 16-row tile pair and the split-K partials of each
     land in the 16-row tile order of the reduction."""
