@@ -22,6 +22,7 @@
 // Block order is XCD-aware: consecutive tiles along the activation rows of
 // one weight-column block land on the same XCD, so a weight tile is fetched
 // from HBM once per XCD and re-read from that XCD's L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "iq_internal.h"
@@ -439,42 +440,65 @@ struct GemmhParams {
     float* part;
 };
 
-// One workgroup per activation row.
-template <bool XF32, bool PERM, bool LO>
-__global__ __launch_bounds__(256) void gemm_xprep_kernel(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
-                                                         int64_t K, _Float16* __restrict__ ah,
-                                                         _Float16* __restrict__ al, float* __restrict__ rs) {
-    const int64_t m = blockIdx.x;
+// The fp16 hi + lo operands of fp32 activations, 2^e per row: one row
+// over `seg` workgroups (grid T x seg).  Each workgroup takes the row's
+// largest |x| (and whether anything is non-finite) over the whole row, then
+// converts its segment of the row's 8-value chunks.  Both passes request
+// four 32-byte chunks per thread at a time through a buffer resource over
+// the row (chunks past the end read zero), so a long row costs a few
+// memory latencies, not one per chunk.  RES (rows of at most 8 chunks per
+// thread, seg = 1): every chunk is requested once, kept in registers
+// through the reduction and converted from there (one memory latency).
+template <bool PERM, bool LO, bool RES>
+__global__ __launch_bounds__(512) void gemm_xprep_kernel(const float* __restrict__ xf, int64_t K, int seg,
+                                                         _Float16* __restrict__ ah, _Float16* __restrict__ al,
+                                                         float* __restrict__ rs) {
+    constexpr int NT = 512, U = 4;
+    const int64_t m = blockIdx.x / seg;
+    const int s = int(blockIdx.x % seg);
     const int tid = threadIdx.x;
-    __shared__ uint32_t red[2][4];
-    auto load8 = [&](int64_t k, float (&v)[8]) {
-        if (XF32) {
-            const float4 a = *reinterpret_cast<const float4*>(xf + m * K + k);
-            const float4 b = *reinterpret_cast<const float4*>(xf + m * K + k + 4);
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {
-            const uint4 a = *reinterpret_cast<const uint4*>(xb + m * K + k);
-            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    __shared__ uint32_t red[2][NT / 64];
+    const rsrc_t rx = make_rsrc(xf + m * K, K * 4);
+    const int64_t nch = K / 8;
+    auto load8 = [&](int64_t ch, float (&v)[8]) {
+        const uint32_t off = ch < nch ? uint32_t(ch * 32) : kOob;
+        const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+        const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 16, 0));
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                v[2 * e] = __uint_as_float(w[e] << 16);
-                v[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
-            }
+        for (int e = 0; e < 4; e++) {
+            v[e] = a[e];
+            v[4 + e] = b[e];
         }
     };
     // 1. largest |x| (as bits: order-preserving for non-negative floats) and
     //    whether anything is non-finite
     uint32_t am = 0, nf = 0;
-    for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
-        float v[8];
-        load8(k, v);
+    constexpr int NR = RES ? 8 : 1;
+    float vr[NR][8];
+    if constexpr (RES) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t a = __float_as_uint(v[e]) & 0x7FFFFFFFu;
-            nf |= a >= 0x7F800000u ? 1u : 0u;
-            am = a > am ? a : am;
-        }
+        for (int j = 0; j < NR; j++) load8(tid + j * NT, vr[j]);
+#pragma unroll
+        for (int j = 0; j < NR; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t a = __float_as_uint(vr[j][e]) & 0x7FFFFFFFu;
+                nf |= a >= 0x7F800000u ? 1u : 0u;
+                am = a > am ? a : am;
+            }
+    }
+    for (int64_t c0 = tid; !RES && c0 < nch; c0 += U * NT) {
+        float v[U][8];
+#pragma unroll
+        for (int j = 0; j < U; j++) load8(c0 + j * NT, v[j]);
+#pragma unroll
+        for (int j = 0; j < U; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t a = __float_as_uint(v[j][e]) & 0x7FFFFFFFu;
+                nf |= a >= 0x7F800000u ? 1u : 0u;
+                am = a > am ? a : am;
+            }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -490,7 +514,7 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const float* __restrict
     am = red[0][0];
     nf = red[1][0];
 #pragma unroll
-    for (int w = 1; w < 4; w++) {
+    for (int w = 1; w < NT / 64; w++) {
         am = red[0][w] > am ? red[0][w] : am;
         nf |= red[1][w];
     }
@@ -498,12 +522,9 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const float* __restrict
     // that 2^-e is a normal float
     int e = (am > 0 && !nf) ? 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(am)) : 0;
     e = e > 126 ? 126 : (e < -126 ? -126 : e);
-    if (tid == 0) rs[m] = nf ? __builtin_nanf("") : __builtin_amdgcn_ldexpf(1.0f, -e);
-    // 2. the operands
-    for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
-        float v[8];
-        load8(k, v);
-        _Float16 h[8], l[8];
+    if (s == 0 && tid == 0) rs[m] = nf ? __builtin_nanf("") : __builtin_amdgcn_ldexpf(1.0f, -e);
+    auto store8 = [&](int64_t ch, const float (&v)[8]) {
+        half8_t h, l;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int c = PERM ? perm8(i) : i;
@@ -511,8 +532,27 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const float* __restrict
             h[i] = _Float16(sv);
             l[i] = _Float16(sv - float(h[i]));
         }
-        *reinterpret_cast<half8_t*>(ah + m * K + k) = half8_t{h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
-        if (LO) *reinterpret_cast<half8_t*>(al + m * K + k) = half8_t{l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
+        *reinterpret_cast<half8_t*>(ah + m * K + ch * 8) = h;
+        if (LO) *reinterpret_cast<half8_t*>(al + m * K + ch * 8) = l;
+    };
+    if constexpr (RES) {
+#pragma unroll
+        for (int j = 0; j < NR; j++)
+            if (tid + j * NT < nch) store8(tid + j * NT, vr[j]);
+        return;
+    }
+    // 2. this workgroup's chunks [cb, ce) of the row
+    const int64_t cps = (nch + seg - 1) / seg, cb = s * cps, ce = cb + cps < nch ? cb + cps : nch;
+    for (int64_t c0 = cb + tid; c0 < ce; c0 += U * NT) {
+        float v[U][8];
+#pragma unroll
+        for (int j = 0; j < U; j++) load8(c0 + j * NT < ce ? c0 + j * NT : nch, v[j]);
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const int64_t ch = c0 + j * NT;
+            if (ch >= ce) break;
+            store8(ch, v[j]);
+        }
     }
 }
 
@@ -838,9 +878,18 @@ hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias
     if (e != hipSuccess) return e;
     _Float16* al = lo ? ah + T * K : nullptr;
     const bool perm = W.kind == 1;
-    const unsigned rows = unsigned(T);
-    if (perm) gemm_xprep_kernel<true, true, true><<<rows, 256, 0, stream>>>(x_f32, nullptr, K, ah, al, rs);
-    else gemm_xprep_kernel<true, false, true><<<rows, 256, 0, stream>>>(x_f32, nullptr, K, ah, al, rs);
+    // rows of up to 8 chunks per thread in registers, one workgroup each;
+    // longer rows over enough workgroups for two per CU (at most 8)
+    const bool res = K <= 8 * 512 * 8;
+    const int seg = res ? 1 : int(std::min<int64_t>(8, std::max<int64_t>(1, (2 * device_cu_count() + T - 1) / T)));
+    const unsigned grid = unsigned(T * seg);
+    if (res) {
+        if (perm) gemm_xprep_kernel<true, true, true><<<grid, 512, 0, stream>>>(x_f32, K, seg, ah, al, rs);
+        else gemm_xprep_kernel<false, true, true><<<grid, 512, 0, stream>>>(x_f32, K, seg, ah, al, rs);
+    } else {
+        if (perm) gemm_xprep_kernel<true, true, false><<<grid, 512, 0, stream>>>(x_f32, K, seg, ah, al, rs);
+        else gemm_xprep_kernel<false, true, false><<<grid, 512, 0, stream>>>(x_f32, K, seg, ah, al, rs);
+    }
     GemmhParams p;
     p.ah = ah; p.al = al; p.rs = rs;
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
