@@ -1942,11 +1942,12 @@ bool launch_gemvr(const float* x, const QView* W, const uint16_t* const* bias, f
 // 17 / 32 rows: gate 18944 x 3584 43.9 -> 29.9 / 48.7 -> 34.7 us, down 3584
 // x 18944 43.3 -> 35.8 / 46.3 -> 38.1 us); narrower calls with shorter rows
 // stay on the GEMM (1.5B down 1536 x 8960 at 17 rows 22.9 against 30.1 us;
-// 7B o 18.6 against 20.2), and so do 33..64 rows (ranges of 2 groups: their
-// partial sums cost more than the tiles save, 7B gate at 48 rows 50.0 ->
-// 51.3 us).
-bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K) {
-    return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 1024 || K / kGroup >= 128);
+// 7B o 18.6 against 20.2) unless the call holds several matrices, which the
+// GEMM takes one launch sequence each (7B q|k|v at 24 / 32 rows 59 / 63 us),
+// and so do 33..64 rows (ranges of 2 groups: their partial sums cost more
+// than the tiles save, 7B gate at 48 rows 50.0 -> 51.3 us).
+bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K, int n) {
+    return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 1024 || K / kGroup >= 128 || n > 1);
 }
 
 // gemvq on n matrices, M in 9..32, straight from x (false: M out of range,
@@ -2209,7 +2210,7 @@ hipError_t launch_gemv_prepped(const QView& W, const uint16_t* bias, int M, floa
 hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* const* bias, float* const* y,
                              int n, int M, Workspace* ws, hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
-    if (gemvq_rows_preferred(M, total_tiles(W, n), K)) {
+    if (gemvq_rows_preferred(M, total_tiles(W, n), K, n)) {
         hipError_t e = hipSuccess;
         if (launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
     }
@@ -2298,7 +2299,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
 
 bool launch_gemm_rows(const float* x, const QView& W, const uint16_t* bias, int64_t T, float* y, Workspace* ws,
                       hipStream_t stream, hipError_t* err) {
-    if (!gemvq_rows_preferred(T, int((W.rows + 15) / 16), W.cols)) return false;
+    if (!gemvq_rows_preferred(T, int((W.rows + 15) / 16), W.cols, 1)) return false;
     return launch_gemvq(x, &W, &bias, &y, 1, int(T), ws, stream, err);
 }
 

@@ -186,11 +186,12 @@ def test_gemvq_ragged_matrices(kind, M):
 @pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [17, 24, 32])
 def test_gemvq_two_row_blocks(kind, M):
-    """17..32 rows on gemvq's two 16-row blocks: 7B gate|up (one call) and
-    down (K = 18944) with biases, ragged matrices (20005 + 309 + 48 rows,
-    K = 1024) in one call, and the fp32 GEMM entry (iq_gemm) on 7B gate."""
+    """17..32 rows on gemvq's two 16-row blocks: 7B gate|up (one call),
+    down (K = 18944) and q|k|v (a narrow call of three matrices) with
+    biases, ragged matrices (20005 + 309 + 48 rows, K = 1024) in one call,
+    and the fp32 GEMM entry (iq_gemm) on 7B gate."""
     rng = np.random.default_rng(1732 + 10 * M + kind)
-    cases = ((3584, (18944, 18944)), (18944, (3584,)), (1024, (20005, 309, 48)))
+    cases = ((3584, (18944, 18944)), (18944, (3584,)), (3584, (3584, 512, 512)), (1024, (20005, 309, 48)))
     for K, Ns in cases:
         Ws = [Packed(rng, N, K, kind) for N in Ns]
         x = rng.standard_normal((M, K), dtype=np.float32)
