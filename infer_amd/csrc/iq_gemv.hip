@@ -123,7 +123,8 @@ struct GemvParams {
     float* part;
     int M, S, gs, nrb;
     int ntiles;  // 1-row kernel: 16-row tiles over all matrices
-    int kr, gr;  // 1-row kernel: K ranges (workgroups per tile) and groups per range
+    int kr, gr;  // 1-row kernel: K ranges (workgroups per tile) and groups per range;
+                 // gemvq: kr consecutive K ranges per workgroup
 };
 
 // 16 bytes of a row at byte offset `off`, zero past `row_bytes` (unaligned
@@ -1738,7 +1739,7 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
 // MB blocks of 16 activation rows, each group's dequantised weights (one
 // chunk at a time) multiplied by every block's operand before the next
 // chunk, so the weights are read and converted once for all the rows.
-template <int KIND, int NG, int MB>
+template <int KIND, int NG, int MB, bool LOOP>
 __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     constexpr int NW = KIND == 1 ? 2 : 4;  // 16-byte weight loads per lane and group
     __shared__ __attribute__((aligned(16))) half8_t Aq[MB][NG][8][64];  // [block][group][chunk][lane]
@@ -1747,7 +1748,6 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = int(p.G);
     const int rb = int(blockIdx.x) % p.nrb, range = int(blockIdx.x) / p.nrb;
-    const int g0 = range * p.gs, gs = (g0 + p.gs < G ? g0 + p.gs : G) - g0;
     // this wave's 32-row tile: matrix i holds tiles [t0, t0 + ceil(N / 32))
     const int tile = rb * 8 + wave;
     MatRef mr = p.mat[0];
@@ -1773,103 +1773,111 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     const uint32_t vq = uint32_t(l32 * row_bytes + h * NW * 16);
     const uint32_t vs = uint32_t(l32 * G) * 2, vz = uint32_t(l32 * G);
 
-    // 1. the range's activations (task t = tid + 512 u: lane t % 16 of
-    //    (row 16 b + m, group i), 8 values, b = (t / 256) / NG, i = (t /
-    //    256) % NG), then this lane's scales, zero points and weights;
-    //    slots past the range and rows past M read zero without a memory
-    //    access (buffer range check)
-    constexpr int NX = MB * 16 * NG * 16 / 512;
-    static_assert(NX * 512 == MB * 16 * NG * 16, "whole DPP rows per task set");
-    float xv[NX][8];
-    {
-        const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
-#pragma unroll
-        for (int u = 0; u < NX; u++) {
-            const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG;
-            const int row = 16 * ((t >> 8) / NG) + m;
-            const uint32_t o = (i < gs && row < p.M)
-                                   ? uint32_t((int64_t(row) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
-                                   : kOob;
-            const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
-            const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                xv[u][e] = a[e];
-                xv[u][4 + e] = b[e];
-            }
-        }
-    }
-    uint16_t sv[NG];
-    uint8_t zv[NG];
-    int4v_t wv[NG][NW];
-#pragma unroll
-    for (int i = 0; i < NG; i++) {
-        const uint32_t o = i < gs ? 0u : kOob;
-        sv[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + o, (g0 + i) * 2, 0);
-        zv[i] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + o, g0 + i, 0) : 0u;
-    }
-#pragma unroll
-    for (int i = 0; i < NG; i++) {
-        const uint32_t o = i < gs ? 0u : kOob;
-#pragma unroll
-        for (int c = 0; c < NW; c++)
-            wv[i][c] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       rq, vq + o, (g0 + i) * (KIND == 1 ? 64 : 128) + c * 16, 0));
-    }
-
-    // 2. the range's operands and factors (16 lanes per (row, group)):
-    //    octet j16 = 8 h' + c of row m goes to chunk c, lanes m + 32 h'
-    //    (hi) and m + 16 + 32 h' (lo); then one barrier
-#pragma unroll
-    for (int u = 0; u < NX; u++) {
-        const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG, b = (t >> 8) / NG;
-        half8_t ho, lo;
-        float fac;
-        xh_split8<KIND == 1>(xv[u], ho, lo, fac);
-        Aq[b][i][j16 & 7][m + 32 * (j16 >> 3)] = ho;
-        Aq[b][i][j16 & 7][m + 16 + 32 * (j16 >> 3)] = lo;
-        if (j16 == 0) Fq[b][i][m] = fac;
-    }
-    __syncthreads();
-
-    // 3. the groups in order, each as its weights land
     float acc[MB][8];
 #pragma unroll
     for (int b = 0; b < MB; b++)
 #pragma unroll
         for (int r = 0; r < 8; r++) acc[b][r] = 0.0f;
+    // LOOP: p.kr consecutive K ranges per workgroup (when the partial sums
+    // of one range per workgroup would not fit), accumulated in registers
+    const int nit = LOOP ? p.kr : 1;
+    for (int it = 0; it < nit; it++) {
+        const int g0 = (range * nit + it) * p.gs;
+        const int gs = g0 >= G ? 0 : (g0 + p.gs < G ? g0 + p.gs : G) - g0;
+        if (it > 0) __syncthreads();  // the previous range's operands are read
+        // 1. the range's activations (task t = tid + 512 u: lane t % 16 of
+        //    (row 16 b + m, group i), 8 values, b = (t / 256) / NG, i = (t /
+        //    256) % NG), then this lane's scales, zero points and weights;
+        //    slots past the range and rows past M read zero without a memory
+        //    access (buffer range check)
+        constexpr int NX = MB * 16 * NG * 16 / 512;
+        static_assert(NX * 512 == MB * 16 * NG * 16, "whole DPP rows per task set");
+        float xv[NX][8];
+        {
+            const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
 #pragma unroll
-    for (int i = 0; i < NG; i++) {
-        if (i >= gs) continue;  // workgroup-uniform
-        float16_t D[MB];
+            for (int u = 0; u < NX; u++) {
+                const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG;
+                const int row = 16 * ((t >> 8) / NG) + m;
+                const uint32_t o = (i < gs && row < p.M)
+                                       ? uint32_t((int64_t(row) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
+                                       : kOob;
+                const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
+                const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
 #pragma unroll
-        for (int b = 0; b < MB; b++) D[b] = float16_t{};
-        const uint32_t zb = zpair_1024(zv[i]), zc = zpair_64(zv[i]);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            half8_t B;
-            if (KIND == 1) {
-                uint32_t o0, o1, o2, o3;
-                dq_int4_x8(uint32_t(wv[i][c >> 2][c & 3]), zb, zc, o0, o1, o2, o3);
-                B = pack_h8(o0, o1, o2, o3);
-            } else {
-                uint32_t l0, h0, l1, h1;
-                const int4v_t& w = wv[i][c >> 1];
-                dq_int8_x4(uint32_t(w[2 * (c & 1)]), l0, h0);
-                dq_int8_x4(uint32_t(w[2 * (c & 1) + 1]), l1, h1);
-                B = pack_h8(l0, h0, l1, h1);
+                for (int e = 0; e < 4; e++) {
+                    xv[u][e] = a[e];
+                    xv[u][4 + e] = b[e];
+                }
             }
-#pragma unroll
-            for (int b = 0; b < MB; b++) D[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[b][i][c][lane], B, D[b], 0, 0, 0);
         }
-        const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
+        uint16_t sv[NG];
+        uint8_t zv[NG];
+        int4v_t wv[NG][NW];
 #pragma unroll
-        for (int b = 0; b < MB; b++) {
-            const float4_t f0 = *reinterpret_cast<const float4_t*>(&Fq[b][i][4 * h]);
-            const float4_t f1 = *reinterpret_cast<const float4_t*>(&Fq[b][i][8 + 4 * h]);
+        for (int i = 0; i < NG; i++) {
+            const uint32_t o = i < gs ? 0u : kOob;
+            sv[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + o, (g0 + i) * 2, 0);
+            zv[i] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + o, g0 + i, 0) : 0u;
+        }
 #pragma unroll
-            for (int r = 0; r < 8; r++)
-                acc[b][r] = __builtin_fmaf(D[b][r] + D[b][r + 8], sc * (r < 4 ? f0[r] : f1[r - 4]), acc[b][r]);
+        for (int i = 0; i < NG; i++) {
+            const uint32_t o = i < gs ? 0u : kOob;
+#pragma unroll
+            for (int c = 0; c < NW; c++)
+                wv[i][c] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           rq, vq + o, (g0 + i) * (KIND == 1 ? 64 : 128) + c * 16, 0));
+        }
+
+        // 2. the range's operands and factors (16 lanes per (row, group)):
+        //    octet j16 = 8 h' + c of row m goes to chunk c, lanes m + 32 h'
+        //    (hi) and m + 16 + 32 h' (lo); then one barrier
+#pragma unroll
+        for (int u = 0; u < NX; u++) {
+            const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG, b = (t >> 8) / NG;
+            half8_t ho, lo;
+            float fac;
+            xh_split8<KIND == 1>(xv[u], ho, lo, fac);
+            Aq[b][i][j16 & 7][m + 32 * (j16 >> 3)] = ho;
+            Aq[b][i][j16 & 7][m + 16 + 32 * (j16 >> 3)] = lo;
+            if (j16 == 0) Fq[b][i][m] = fac;
+        }
+        __syncthreads();
+
+        // 3. the groups in order, each as its weights land
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            if (i >= gs) continue;  // workgroup-uniform
+            float16_t D[MB];
+#pragma unroll
+            for (int b = 0; b < MB; b++) D[b] = float16_t{};
+            const uint32_t zb = zpair_1024(zv[i]), zc = zpair_64(zv[i]);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                half8_t B;
+                if (KIND == 1) {
+                    uint32_t o0, o1, o2, o3;
+                    dq_int4_x8(uint32_t(wv[i][c >> 2][c & 3]), zb, zc, o0, o1, o2, o3);
+                    B = pack_h8(o0, o1, o2, o3);
+                } else {
+                    uint32_t l0, h0, l1, h1;
+                    const int4v_t& w = wv[i][c >> 1];
+                    dq_int8_x4(uint32_t(w[2 * (c & 1)]), l0, h0);
+                    dq_int8_x4(uint32_t(w[2 * (c & 1) + 1]), l1, h1);
+                    B = pack_h8(l0, h0, l1, h1);
+                }
+#pragma unroll
+                for (int b = 0; b < MB; b++) D[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Aq[b][i][c][lane], B, D[b], 0, 0, 0);
+            }
+            const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
+#pragma unroll
+            for (int b = 0; b < MB; b++) {
+                const float4_t f0 = *reinterpret_cast<const float4_t*>(&Fq[b][i][4 * h]);
+                const float4_t f1 = *reinterpret_cast<const float4_t*>(&Fq[b][i][8 + 4 * h]);
+#pragma unroll
+                for (int r = 0; r < 8; r++)
+                    acc[b][r] = __builtin_fmaf(D[b][r] + D[b][r + 8], sc * (r < 4 ? f0[r] : f1[r - 4]), acc[b][r]);
+            }
         }
     }
     if (!tok || l32 >= rows) return;
@@ -1950,8 +1958,8 @@ bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K, int n) {
     return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 1024 || K / kGroup >= 128 || n > 1);
 }
 
-// gemvq on n matrices, M in 9..32, straight from x (false: M out of range,
-// or the partial sums would not fit the workspace's capacity).
+// gemvq on n matrices, M in 9..32, straight from x (false: M out of range;
+// partial sums beyond the workspace are avoided by looping over K ranges).
 bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                   Workspace* ws, hipStream_t stream, hipError_t* err) {
     const int64_t K = W[0].cols, G = W[0].groups;
@@ -1974,7 +1982,14 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
     S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
     const int gs = int((G + S - 1) / S);
     S = int((G + gs - 1) / gs);
-    if (S > 1 && int64_t(S) * M * tiles * 16 > ws->part_floats) return false;
+    // partial sums beyond the workspace: fewer workgroups along K, each
+    // taking L consecutive ranges (one per workgroup at L = 1)
+    int L = 1;
+    if (S > 1 && int64_t(S) * M * tiles * 16 > ws->part_floats) {
+        const int64_t fit = ws->part_floats / (int64_t(M) * tiles * 16);
+        L = int((S + fit - 1) / std::max<int64_t>(fit, 1));
+        S = (S + L - 1) / L;
+    }
     p.nmat = n;
     p.K = K;
     p.G = G;
@@ -1982,16 +1997,27 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
     p.M = M;
     p.gs = gs;
     p.S = S;
+    p.kr = L;
     p.nrb = nrb;
     p.ntiles = tiles;
     p.part = ws->partials;
     const unsigned grid = unsigned(nrb * S);
     if (mb == 1) {
-        if (W[0].kind == 1) gemvq_kernel<1, 6, 1><<<grid, 512, 0, stream>>>(p);
-        else gemvq_kernel<0, 4, 1><<<grid, 512, 0, stream>>>(p);
+        if (W[0].kind == 1) {
+            if (L > 1) gemvq_kernel<1, 6, 1, true><<<grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<1, 6, 1, false><<<grid, 512, 0, stream>>>(p);
+        } else {
+            if (L > 1) gemvq_kernel<0, 4, 1, true><<<grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<0, 4, 1, false><<<grid, 512, 0, stream>>>(p);
+        }
     } else {
-        if (W[0].kind == 1) gemvq_kernel<1, 4, 2><<<grid, 512, 0, stream>>>(p);
-        else gemvq_kernel<0, 4, 2><<<grid, 512, 0, stream>>>(p);
+        if (W[0].kind == 1) {
+            if (L > 1) gemvq_kernel<1, 4, 2, true><<<grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<1, 4, 2, false><<<grid, 512, 0, stream>>>(p);
+        } else {
+            if (L > 1) gemvq_kernel<0, 4, 2, true><<<grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<0, 4, 2, false><<<grid, 512, 0, stream>>>(p);
+        }
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && S > 1) {

@@ -216,6 +216,29 @@ def test_gemvq_two_row_blocks(kind, M):
     check_sampled(y[: (M - 1) * N].contiguous(), x[: M - 1], W, M - 1, rng, f"iq_gemm M={M} kind={kind}")
 
 
+def test_gemvq_looped_k_ranges():
+    """gemvq where one K range per workgroup would need more partial sums
+    than the workspace holds, so each workgroup loops over several ranges:
+    the int8 lm_head at 32 rows (per-stream workspace) and int4 7B gate at
+    32 rows through iq_gemv_noalloc (the static array's smaller capacity)."""
+    rng = np.random.default_rng(3232032)
+    M, K = 32, 3584
+    W = Packed(rng, 152064, K, 0)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    y = out_buffer(M, W.rows)
+    say("gemvq looped: lm_head int8", M)
+    ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, None, M, K, W.rows, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x, W, M, rng, "looped lm_head int8 M=32")
+    del W
+    W = Packed(rng, 18944, K, 1)
+    y = out_buffer(M, W.rows)
+    say("gemvq looped: noalloc int4 gate", M)
+    ops.gemv_noalloc(torch.from_numpy(x).cuda(), W.view, None, M, K, W.rows, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x, W, M, rng, "looped noalloc int4 gate M=32")
+
+
 @pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [6, 12])
 def test_in_kernel_operands_unaligned_x(kind, M):
