@@ -939,16 +939,21 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
                        const uint16_t* bias, int64_t T, float* y, Workspace* ws, hipStream_t stream) {
     {
         const uintptr_t xa = x_f32 ? reinterpret_cast<uintptr_t>(x_f32) : reinterpret_cast<uintptr_t>(x_bf16);
-        // fp32 activations on whole 128-column groups: the fp16 operand path
-        // (faster at every T measured, and 22 significant bits against the
-        // 24 of three bf16 terms at 1.5x the MFMAs: 7B at T = 1024, gate
-        // 18944 x 3584 int4 648 -> 440 us, down 1053 -> 681 us; T = 32:
-        // 74 -> 50, 70 -> 48 us)
+        // fp32 activations: 17..32 rows of wide or long-K matrices on
+        // gemvq's row blocks; past 32 rows on whole 128-column groups the
+        // fp16 operand path (22 significant bits against the 24 of three
+        // bf16 terms at 1.5x the MFMAs, and faster: 7B at T = 1024, gate
+        // 18944 x 3584 int4 648 -> 440 us, down 1053 -> 681 us); up to 32
+        // rows the three-term split inside gemm_kernel, whose single launch
+        // beats the preparation launch on the narrower matrices left here
+        // (1.5B at 32 rows: o 1536 x 1536 16.9 -> 11.6 us, down 1536 x 8960
+        // 25.4 -> 21.8; 7B o 22.9 either way)
         if (x_f32) {
             hipError_t e = hipSuccess;
             if (launch_gemm_rows(x_f32, W, bias, T, y, ws, stream, &e)) return e;
         }
-        if (x_f32 && W.cols % kGroup == 0 && xa % 16 == 0) return launch_gemmh(x_f32, W, bias, T, y, ws, stream);
+        if (x_f32 && T > 32 && W.cols % kGroup == 0 && xa % 16 == 0)
+            return launch_gemmh(x_f32, W, bias, T, y, ws, stream);
     }
     GemmParams p;
     p.part = ws->partials;

@@ -2255,7 +2255,9 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // (7B int4 at 5 / 8 rows: gate|up 34.5 -> 28.7 / 35.1 -> 29.2, down
     // 27.6 -> 24.0 / 27.4 -> 25.0 us against gemvt / gemvh; lm_head 152064 x
     // 3584 int8: 166 -> 121 / 166 -> 155 us; at 2..4 rows the 1-row
-    // kernel's 4-row instance is far faster)
+    // kernel's 4-row instance is far faster; not at G = 70: 1.5B down
+    // 1536 x 8960 at 5 / 8 rows 13.2 / 13.1 us elsewhere against 18.5 /
+    // 20.2 on gemvr, and 15.4 against 21.3 at 16 rows)
     // 7..8 rows on very wide calls (the lm_head): gemvs on the 16-row
     // operand blocks (7B lm_head int8 at 7 / 8 rows: 163 -> 135 / 163 -> 138
     // us; at 5 / 6 rows gemvr stays ahead, 121 / 124 against 137 / 138)
@@ -2265,7 +2267,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         if (e != hipSuccess) return e;
         if (launch_gemvs(W, bias, y, n, M, ws, stream, &e)) return e;
     }
-    if (M >= 5 && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
+    if (M >= 5 && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
         hipError_t e = hipSuccess;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
         if (!ws->prep_copy) ws->invalidate_prep();
@@ -2304,7 +2306,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // rows: 36.0 -> 31.2 / 38.3 -> 33.7 us; int8 stays on gemvr: 40.2
     // against 39.9 at 9 rows, 44.1 against 45.3 at 16;
     // down loses with its shorter K ranges: 28.8 -> 34.2)
-    if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 64)) {
+    if (M > 8 && M <= 16 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
         hipError_t e = hipSuccess;
         if (W[0].kind == 1 && total_tiles(W, n) >= 1024 && launch_gemvq(x, W, bias, y, n, M, ws, stream, &e))
             return e;
