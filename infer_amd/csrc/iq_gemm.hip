@@ -791,8 +791,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
                                                           float* __restrict__ y) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= T * N) return;
-    float sum = 0.0f;
-    for (int s = 0; s < S; s++) sum += part[int64_t(s) * T * N + i];
+    const float sum = sum_slices(part, S, T * N, i);
     y[i] = sum + (bias ? bf16_to_f32(bias[i % N]) : 0.0f);
 }
 

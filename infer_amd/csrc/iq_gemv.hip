@@ -856,8 +856,7 @@ __global__ __launch_bounds__(256) void gemvt_reduce_kernel(const GemvParams p) {
     const TileSel ts = select_tile(p, int(c >> 4));
     const int64_t row = ts.row0 + (c & 15);
     if (row >= ts.m.N) return;
-    float sum = 0.0f;
-    for (int s = 0; s < p.S; s++) sum += p.part[(int64_t(s) * p.M + m) * ld + c];
+    const float sum = sum_slices(p.part, p.S, int64_t(p.M) * ld, int64_t(m) * ld + c);
     ts.m.y[int64_t(m) * ts.m.N + row] = sum + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
 }
 
@@ -866,8 +865,7 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restric
                                                           const uint16_t* __restrict__ bias, float* __restrict__ y) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= int64_t(M) * N) return;
-    float sum = 0.0f;
-    for (int s = 0; s < S; s++) sum += part[int64_t(s) * M * N + i];
+    const float sum = sum_slices(part, S, int64_t(M) * N, i);
     y[i] = sum + (bias ? bf16_to_f32(bias[i % N]) : 0.0f);
 }
 
