@@ -25,7 +25,9 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     requested at once, the f16 split operands made from x inside the
     kernel), gate|up at 9..16 gemvq, with a non-finite activation in two
     rows;
-  * every other 7B decode matrix at 16 rows.
+  * every other 7B decode matrix at 16 rows;
+  * every row count where the routing changes, on narrow, wide and long-K
+    shapes.
 """
 import numpy as np
 import pytest
@@ -214,6 +216,27 @@ def test_gemvq_two_row_blocks(kind, M):
     got = y.detach().cpu().numpy().reshape(-1)[: M * N].reshape(M, N)
     assert not np.any(np.isfinite(got[M - 1])), "finite output in the non-finite row"
     check_sampled(y[: (M - 1) * N].contiguous(), x[: M - 1], W, M - 1, rng, f"iq_gemm M={M} kind={kind}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_route_boundaries(kind):
+    """Every row count where the GEMV routing changes (1..9, 12, 16, 17,
+    24, 31, 32) on three shapes that fall on different sides of the width
+    and K thresholds: narrow and ragged (3000 x 2048), wide (20000 x 1024,
+    >= 1024 tiles) and long rows (1024 x 16512, G = 129 >= 128), with a
+    bias, against the oracle."""
+    rng = np.random.default_rng(5150 + kind)
+    for N, K in ((3000, 2048), (20000, 1024), (1024, 16512)):
+        W = Packed(rng, N, K, kind)
+        bb = O.seeded_bf16(rng, (N,), 0.5)
+        bd = torch.from_numpy(bb.view(np.int16)).cuda()
+        for M in (1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32):
+            x = rng.standard_normal((M, K), dtype=np.float32)
+            y = out_buffer(M, N)
+            say("route boundaries", kind, N, K, M)
+            ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, bd, M, K, N, y)
+            torch.cuda.synchronize()
+            check_sampled(y, x, W, M, rng, f"boundaries {N}x{K} M={M} kind={kind}", bias_bits=bb)
 
 
 def test_gemvq_looped_k_ranges():
