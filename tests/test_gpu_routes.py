@@ -27,7 +27,8 @@ Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
     rows;
   * every other 7B decode matrix at 16 rows;
   * every row count where the routing changes, on narrow, wide and long-K
-    shapes.
+    shapes, and every T where the prefill GEMM's choices change, both
+    activation types.
 """
 import numpy as np
 import pytest
@@ -237,6 +238,33 @@ def test_route_boundaries(kind):
             ops.launch_gemv_batched_q(torch.from_numpy(x).cuda(), W.view, bd, M, K, N, y)
             torch.cuda.synchronize()
             check_sampled(y, x, W, M, rng, f"boundaries {N}x{K} M={M} kind={kind}", bias_bits=bb)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemm_t_boundaries(kind):
+    """iq_gemm (fp32 activations) and iq_gemm_bf16x across the T where the
+    GEMM's choices change (gemvq's row blocks at 17..32 on wide matrices,
+    the in-kernel split up to 32, the prepared fp16 operands past it, 64-,
+    128- and 256-row tiles, split K): 17, 32, 33, 64, 65, 128, 129, 256,
+    257 and 520 rows on a wide (20000 x 1024) and a narrow ragged (3000 x
+    2048) matrix, 17..257 on long rows (1024 x 16512), against the oracle."""
+    rng = np.random.default_rng(6160 + kind)
+    for N, K, Ts in ((20000, 1024, (17, 32, 33, 64, 65, 128, 129, 256, 257, 520)),
+                     (3000, 2048, (17, 32, 33, 64, 65, 128, 129, 256, 257, 520)),
+                     (1024, 16512, (17, 32, 33, 64, 129, 257))):
+        W = Packed(rng, N, K, kind)
+        for T in Ts:
+            x = rng.standard_normal((T, K), dtype=np.float32)
+            say("gemm T boundaries", kind, N, K, T)
+            y = out_buffer(T, N)
+            ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
+            torch.cuda.synchronize()
+            check_sampled(y, x, W, T, rng, f"iq_gemm {N}x{K} T={T} kind={kind}")
+            xb = O.f32_to_bf16(x)
+            y = out_buffer(T, N)
+            ops.launch_gemm_bf16x(torch.from_numpy(xb.view(np.int16)).cuda(), W.view, None, T, K, N, y)
+            torch.cuda.synchronize()
+            check_sampled(y, O.bf16_to_f32(xb), W, T, rng, f"iq_gemm_bf16x {N}x{K} T={T} kind={kind}")
 
 
 def test_gemvq_looped_k_ranges():
