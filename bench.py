@@ -25,7 +25,8 @@ Also reported (measured after the timed region, outside it):
              from profiles/gemv_int4_7b_m1_traffic.json (rocprofv3 counters);
   cpu_baseline  the reference CPU path (src/forward.cpp linear over dequant(),
              restated in oracle/iq_oracle.c) on a bounded sample, 1 thread;
-  detail     per-shape GB/s of the 1-row launches, int4 at 16 rows, the decode
+  detail     per-shape GB/s of the 1-row launches, int4 at 16 rows (and at
+             2, 4, 8 and 32 rows: 7b_int4_rows_sweep), the decode
              step chained as the engine runs it (norms, attention at position
              0, SwiGLU, residuals fused into the GEMV stages), the int8 set
              at 1 and 16 rows, the prefill GEMM (config 5), on-device
@@ -569,6 +570,16 @@ def main():
                                  "GBps": round(st16.bytes / (ms16 * 1e-3) / 1e9, 1),
                                  "ratio_vs_m1": round(ms16 / ms_wall, 3)}
         del g16, st16
+        # the same step at the other batch widths of the reference's decode
+        # (GpuBatch::kMaxRows = 32): time and ratio to the 1-row step
+        sweep = {}
+        for M in (2, 4, 8, 32):
+            stm = Step(torch, ops, m4, M)
+            gm = stm.capture()
+            msm, _ = time_graph(torch, gm, args.steps, args.warmup)
+            sweep[str(M)] = {"us_per_step": round(msm * 1e3, 1), "ratio_vs_m1": round(msm / ms_wall, 3)}
+            del gm, stm
+        detail["7b_int4_rows_sweep"] = sweep
         detail["7b_int4_decode_chain_m1"] = bench_decode_chain(torch, ops, m4, args.steps, args.warmup)
         cpu_gbs, cpu_sample = cpu_baseline(torch, m4, args.cpu_seconds)
         cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
