@@ -1978,15 +1978,21 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
     const int want = 2 * device_cu_count();
     int S = int((G + ngr - 1) / ngr);
     S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
-    const int gs = int((G + S - 1) / S);
+    int gs = int((G + S - 1) / S);
     S = int((G + gs - 1) / gs);
     // partial sums beyond the workspace: fewer workgroups along K, each
     // taking L consecutive ranges (one per workgroup at L = 1)
     int L = 1;
+    int ngl = ngr;  // ranges of the looped instance
     if (S > 1 && int64_t(S) * M * tiles * 16 > ws->part_floats) {
+        // (int8 at two row blocks loops over 2-group ranges: 110 VGPRs,
+        // two workgroups per CU, against 150 with 4)
+        if (W[0].kind == 0 && mb == 2) ngl = 2;
+        const int R = int((G + ngl - 1) / ngl);
+        gs = int((G + R - 1) / R);
         const int64_t fit = ws->part_floats / (int64_t(M) * tiles * 16);
-        L = int((S + fit - 1) / std::max<int64_t>(fit, 1));
-        S = (S + L - 1) / L;
+        L = int((R + fit - 1) / std::max<int64_t>(fit, 1));
+        S = (R + L - 1) / L;
     }
     p.nmat = n;
     p.K = K;
@@ -2013,7 +2019,7 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
             if (L > 1) gemvq_kernel<1, 4, 2, true><<<grid, 512, 0, stream>>>(p);
             else gemvq_kernel<1, 4, 2, false><<<grid, 512, 0, stream>>>(p);
         } else {
-            if (L > 1) gemvq_kernel<0, 4, 2, true><<<grid, 512, 0, stream>>>(p);
+            if (L > 1) gemvq_kernel<0, 2, 2, true><<<grid, 512, 0, stream>>>(p);
             else gemvq_kernel<0, 4, 2, false><<<grid, 512, 0, stream>>>(p);
         }
     }
