@@ -946,12 +946,15 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
         // rows the three-term split inside gemm_kernel, whose single launch
         // beats the preparation launch on the narrower matrices left here
         // (1.5B at 32 rows: o 1536 x 1536 16.9 -> 11.6 us, down 1536 x 8960
-        // 25.4 -> 21.8; 7B o 22.9 either way)
+        // 25.4 -> 21.8; 7B o 22.9 either way), and so up to 64 rows on
+        // matrices of at most 2^24 weights (T = 64: 1.5B o 15.6 -> 10.2, down
+        // 24.1 -> 19.7, 7B o 23.7 -> 21.4 us; 7B gate 44.8 against 64.7)
         if (x_f32) {
             hipError_t e = hipSuccess;
             if (launch_gemm_rows(x_f32, W, bias, T, y, ws, stream, &e)) return e;
         }
-        if (x_f32 && T > 32 && W.cols % kGroup == 0 && xa % 16 == 0)
+        const bool split_in_kernel = T <= 32 || (T <= 64 && W.rows * W.cols <= (int64_t(1) << 24));
+        if (x_f32 && !split_in_kernel && W.cols % kGroup == 0 && xa % 16 == 0)
             return launch_gemmh(x_f32, W, bias, T, y, ws, stream);
     }
     GemmParams p;
