@@ -247,10 +247,12 @@ def test_gemm_t_boundaries(kind):
     the in-kernel split up to 32, the prepared fp16 operands past it, 64-,
     128- and 256-row tiles, split K): 17, 32, 33, 64, 65, 128, 129, 256,
     257 and 520 rows on a wide (20000 x 1024) and a narrow ragged (3000 x
-    2048) matrix, 17..257 on long rows (1024 x 16512), against the oracle."""
+    2048) matrix, 65..257 on a small one (520 x 3584, under 2^22 weights),
+    17..257 on long rows (1024 x 16512), against the oracle."""
     rng = np.random.default_rng(6160 + kind)
     for N, K, Ts in ((20000, 1024, (17, 32, 33, 64, 65, 128, 129, 256, 257, 520)),
                      (3000, 2048, (17, 32, 33, 64, 65, 128, 129, 256, 257, 520)),
+                     (520, 3584, (65, 200, 256, 257)),
                      (1024, 16512, (17, 32, 33, 64, 129, 257))):
         W = Packed(rng, N, K, kind)
         for T in Ts:
