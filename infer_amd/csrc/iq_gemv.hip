@@ -1944,16 +1944,19 @@ bool launch_gemvr(const float* x, const QView* W, const uint16_t* const* bias, f
 }
 
 // 17..32 rows on gemvq's two 16-row blocks instead of the GEMM's 64-row
-// tiles, for wide calls and long rows (7B, fp32 activations, int8 / int4 at
-// 17 / 32 rows: gate 18944 x 3584 43.9 -> 29.9 / 48.7 -> 34.7 us, down 3584
-// x 18944 43.3 -> 35.8 / 46.3 -> 38.1 us); narrower calls with shorter rows
-// stay on the GEMM (1.5B down 1536 x 8960 at 17 rows 22.9 against 30.1 us;
-// 7B o 18.6 against 20.2) unless the call holds several matrices, which the
-// GEMM takes one launch sequence each (7B q|k|v at 24 / 32 rows 59 / 63 us),
-// and so do 33..64 rows (ranges of 2 groups: their partial sums cost more
-// than the tiles save, 7B gate at 48 rows 50.0 -> 51.3 us).
+// tiles, for calls of >= 224 16-row tiles (N >= 3584), long rows or several
+// matrices (7B, fp32 activations, int8 / int4 at 17 / 32 rows: gate 18944 x
+// 3584 43.9 -> 29.9 / 48.7 -> 34.7 us, down 3584 x 18944 43.3 -> 35.8 / 46.3
+// -> 38.1 us, o 3584 x 3584 20.2 -> 17.3 / 21.2 -> 19.8 (int4 20.4 -> 16.5
+// / 22.1 -> 19.6), 1.5B gate 8960 x 1536 19.5 -> 16.9 / 21.4 -> 20.0, 3584
+// x 2048 15.5 -> 12.5 / 17.4 -> 14.0 us; q|k|v as one call, which the GEMM
+// takes one launch sequence per matrix, 59 / 63 -> 24 / 25 us at 24 / 32
+// rows); narrower calls with shorter rows stay on the GEMM (1.5B o 1536 x
+// 1536 at 17 rows 8.8 against 10.0, 2048 x 1536 8.4 against 9.4 us), and so
+// do 33..64 rows (ranges of 2 groups: their partial sums cost more than the
+// tiles save, 7B gate at 48 rows 50.0 -> 51.3 us).
 bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K, int n) {
-    return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 1024 || K / kGroup >= 128 || n > 1);
+    return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 224 || K / kGroup >= 128 || n > 1);
 }
 
 // gemvq on n matrices, M in 9..32, straight from x (false: M out of range;

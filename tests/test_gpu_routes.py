@@ -225,13 +225,16 @@ def test_route_boundaries(kind):
     24, 31, 32) on three shapes that fall on different sides of the width
     and K thresholds: narrow and ragged (3000 x 2048), wide (20000 x 1024,
     >= 1024 tiles) and long rows (1024 x 16512, G = 129 >= 128), with a
-    bias, against the oracle."""
+    bias, and 17..32 rows on either side of the 224-tile threshold (3568 and
+    3570 x 2048: 223 and 224 tiles), against the oracle."""
     rng = np.random.default_rng(5150 + kind)
-    for N, K in ((3000, 2048), (20000, 1024), (1024, 16512)):
+    every = (1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32)
+    for N, K, Ms in ((3000, 2048, every), (20000, 1024, every), (1024, 16512, every),
+                     (3568, 2048, (17, 32)), (3570, 2048, (17, 32))):
         W = Packed(rng, N, K, kind)
         bb = O.seeded_bf16(rng, (N,), 0.5)
         bd = torch.from_numpy(bb.view(np.int16)).cuda()
-        for M in (1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32):
+        for M in Ms:
             x = rng.standard_normal((M, K), dtype=np.float32)
             y = out_buffer(M, N)
             say("route boundaries", kind, N, K, M)
