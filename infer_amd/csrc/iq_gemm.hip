@@ -852,19 +852,6 @@ void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t s
     }
 }
 
-template <int KIND, bool LO, int NJ>
-void launch_gemmh_t(const GemmhParams& p, int bm, hipStream_t stream) {
-    const unsigned grid = unsigned(p.tiles_m * p.tiles_n * p.splits);
-    if constexpr (!LO) {
-        if (bm == 256) {
-            gemmh_kernel<KIND, LO, NJ, 256><<<grid, 2 * kThreads, 0, stream>>>(p);
-            return;
-        }
-    }
-    if (bm == 64) gemmh_kernel<KIND, LO, NJ, 64><<<grid, kThreads, 0, stream>>>(p);
-    else gemmh_kernel<KIND, LO, NJ, 128><<<grid, kThreads, 0, stream>>>(p);
-}
-
 // The fp16 operand path (K % 128 == 0, 16-byte aligned activations): one
 // preparation launch, the GEMM, and the range sums when K is split.
 hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias, int64_t T, float* y,
@@ -894,13 +881,14 @@ hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
     p.T = T; p.N = W.rows; p.K = K; p.G = W.groups;
     p.part = ws->partials;
-    // 64-row tiles for short T (the 128-row rule of gemm_kernel)
-    const bool short_t = T <= 64 || (T > 128 && T <= 256) || (T <= 128 && W.rows >= 8192);
-    const int bm = short_t ? 64 : 128;
+    // 64 x 128 tiles at every T: two workgroups per CU (one at 128 rows, whose
+    // hi + lo operand buffers fill the LDS).  7B int8 at T = 128 / 512 /
+    // 1024 against 128-row tiles: down 3584 x 18944 99 / 334 / 684 -> 66 /
+    // 212 / 433 us, gate 18944 x 3584 (64 rows already at T <= 128) 266 /
+    // 440 -> 201 / 393 us at 512 / 1024, o 3584 x 3584 at 1024 142 -> 93 us.
+    const int bm = 64;
     p.tiles_m = int((T + bm - 1) / bm);
-    const int t128 = p.tiles_m * int((p.N + 127) / 128);
-    const int nj = (t128 >= 2 * device_cu_count() || bm == 64) ? 2 : 1;
-    p.tiles_n = int((p.N + 64 * nj - 1) / (64 * nj));
+    p.tiles_n = int((p.N + 127) / 128);
     // K ranges when the tiles leave CUs without two workgroups
     p.splits = 1;
     p.kchunk = K;
@@ -918,13 +906,9 @@ hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias
             }
         }
     }
-    if (W.kind == 1) {
-        if (nj == 2) launch_gemmh_t<1, true, 2>(p, bm, stream);
-        else launch_gemmh_t<1, true, 1>(p, bm, stream);
-    } else {
-        if (nj == 2) launch_gemmh_t<0, true, 2>(p, bm, stream);
-        else launch_gemmh_t<0, true, 1>(p, bm, stream);
-    }
+    const unsigned ggrid = unsigned(p.tiles_m * p.tiles_n * p.splits);
+    if (W.kind == 1) gemmh_kernel<1, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
+    else gemmh_kernel<0, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
     if (p.splits > 1) {
         const int64_t n = p.T * p.N;
         gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
