@@ -935,14 +935,16 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
         // 24.1 -> 19.7, 7B o 23.7 -> 21.4 us; 7B gate 44.8 against 64.7) and
         // up to 256 rows on matrices of at most 2^22 (T = 96..256: 7B k 512
         // x 3584 18.0..22.4 -> 13.3..14.6 us, 1.5B o 23.2..25.1 ->
-        // 17.7..22.4)
+        // 17.7..22.4), at any T on matrices of at most 2^19 (1.5B k 256 x
+        // 1536 at T = 257 / 512 / 2048: 17.3 / 20.7 / 34.0 -> 12.7 / 12.4 /
+        // 25.9 us)
         if (x_f32) {
             hipError_t e = hipSuccess;
             if (launch_gemm_rows(x_f32, W, bias, T, y, ws, stream, &e)) return e;
         }
         const int64_t nk = W.rows * W.cols;
         const bool split_in_kernel = T <= 32 || (T <= 64 && nk <= (int64_t(1) << 24)) ||
-                                     (T <= 256 && nk <= (int64_t(1) << 22));
+                                     (T <= 256 && nk <= (int64_t(1) << 22)) || nk <= (int64_t(1) << 19);
         if (x_f32 && !split_in_kernel && W.cols % kGroup == 0 && xa % 16 == 0)
             return launch_gemmh(x_f32, W, bias, T, y, ws, stream);
     }
