@@ -561,10 +561,10 @@ __global__ __launch_bounds__(512) void gemm_xprep_kernel(const float* __restrict
 // the step after next in registers), on the prepared fp16 operands (LO: hi
 // and lo, two MFMAs per weight operand).  K % 128 == 0.
 template <int KIND, bool LO, int NJ, int BM>
-__global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, (BM == 256 || LO) ? 1 : 2) void gemmh_kernel(
+__global__ __launch_bounds__(BM >= 128 ? 2 * kThreads : kThreads, (BM == 256 || LO) ? 1 : 2) void gemmh_kernel(
     const GemmhParams p) {
     constexpr int BN = 64 * NJ;
-    constexpr int NT = BM == 256 ? 2 * kThreads : kThreads;
+    constexpr int NT = BM >= 128 ? 2 * kThreads : kThreads;
     constexpr int WR = NT / 128;
     constexpr int WROWS = BM / WR;
     constexpr int NI = WROWS / 32;
@@ -881,12 +881,18 @@ hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias
     p.q = W.q; p.scales = W.scales; p.zeros = W.zeros; p.bias = bias; p.y = y;
     p.T = T; p.N = W.rows; p.K = K; p.G = W.groups;
     p.part = ws->partials;
-    // 64 x 128 tiles at every T: two workgroups per CU (one at 128 rows, whose
-    // hi + lo operand buffers fill the LDS).  7B int8 at T = 128 / 512 /
-    // 1024 against 128-row tiles: down 3584 x 18944 99 / 334 / 684 -> 66 /
-    // 212 / 433 us, gate 18944 x 3584 (64 rows already at T <= 128) 266 /
-    // 440 -> 201 / 393 us at 512 / 1024, o 3584 x 3584 at 1024 142 -> 93 us.
-    const int bm = 64;
+    // 64 x 128 tiles on 4 waves, two workgroups per CU (a 4-wave workgroup
+    // of 128 rows, whose hi + lo operand buffers fill the LDS, runs alone
+    // on its CU: 7B int8 at T = 128 / 512 / 1024, down 3584 x 18944 99 /
+    // 334 / 684 -> 66 / 212 / 433 us, gate 18944 x 3584 266 / 440 -> 201 /
+    // 393 us at 512 / 1024, o 3584 x 3584 at 1024 142 -> 93 us).  From T =
+    // 512, int4 and rows of K >= 2048 take 128 x 128 tiles on 8 waves, each
+    // converted weight tile feeding twice the rows: 7B int4 at T = 1024 /
+    // 2048 down 426 / 936 -> 378 / 782 us, gate 389 / 801 -> 354 / 721 us,
+    // int8 gate 402 -> 381 us at 1024 (1.5B int8 gate 8960 x 1536: 110 ->
+    // 116 us, kept at 64 rows).
+    const bool wide_t = T >= 512 && (W.kind == 1 || K >= 2048);
+    const int bm = wide_t ? 128 : 64;
     p.tiles_m = int((T + bm - 1) / bm);
     p.tiles_n = int((p.N + 127) / 128);
     // K ranges when the tiles leave CUs without two workgroups
@@ -907,8 +913,13 @@ hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias
         }
     }
     const unsigned ggrid = unsigned(p.tiles_m * p.tiles_n * p.splits);
-    if (W.kind == 1) gemmh_kernel<1, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
-    else gemmh_kernel<0, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
+    if (bm == 128) {
+        if (W.kind == 1) gemmh_kernel<1, true, 2, 128><<<ggrid, 2 * kThreads, 0, stream>>>(p);
+        else gemmh_kernel<0, true, 2, 128><<<ggrid, 2 * kThreads, 0, stream>>>(p);
+    } else {
+        if (W.kind == 1) gemmh_kernel<1, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
+        else gemmh_kernel<0, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
+    }
     if (p.splits > 1) {
         const int64_t n = p.T * p.N;
         gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
