@@ -843,14 +843,22 @@ void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t s
     // workgroup then re-reads the activations for twice the columns (7B int8
     // at T = 64, fp32 activations: gate 58.5 -> 44.8, down 58.0 -> 43.7 us;
     // down at T = 256: 168 -> 119 us)
-    const int t128 = p.tiles_m * int((p.N + 127) / 128);
-    if (t128 >= 2 * device_cu_count() || bm == 64) {
+    // ... and when 128-wide tiles take at most half as many rounds of the
+    // instance's workgroup slots as 64-wide ones (bf16 activations: 7B down
+    // 3584 x 18944 at T = 1536 / 2048 int8 481 / 534 -> 397 / 419 us, int4
+    // 533 / 536 -> 412 / 422 us, at 4096 int4 1166 -> 867 us; 7B o 3584 x
+    // 3584 int8 at 2048 99 -> 78 us; 1.5B down 1536 x 8960 at 3072 / 4096
+    // 212 / 240 -> 170 / 183 us)
+    const int per_cu = XF32 || bm == 256 ? 1 : 2, slots = per_cu * device_cu_count();
+    const int t128 = p.tiles_m * int((p.N + 127) / 128), t64 = p.tiles_m * int((p.N + 63) / 64);
+    const bool nj2_rounds = 2 * ((t128 + slots - 1) / slots) <= (t64 + slots - 1) / slots;
+    if (t128 >= 2 * device_cu_count() || bm == 64 || nj2_rounds) {
         p.tiles_n = int((p.N + 127) / 128);
-        plan_splits(p, fastw && fastx, kPartialFloats, XF32 || bm == 256 ? 1 : 2);
+        plan_splits(p, fastw && fastx, kPartialFloats, per_cu);
         launch_gemm_t<KIND, XF32, 2>(p, fastw, fastx, bm, stream);
     } else {
         p.tiles_n = int((p.N + 63) / 64);
-        plan_splits(p, fastw && fastx, kPartialFloats, XF32 || bm == 256 ? 1 : 2);
+        plan_splits(p, fastw && fastx, kPartialFloats, per_cu);
         launch_gemm_t<KIND, XF32, 1>(p, fastw, fastx, bm, stream);
     }
     if (p.splits > 1) {

@@ -251,13 +251,16 @@ def test_gemm_t_boundaries(kind):
     128- and 256-row tiles, split K): 17, 32, 33, 64, 65, 128, 129, 256,
     257 and 520 rows on a wide (20000 x 1024) and a narrow ragged (3000 x
     2048) matrix, 65..257 on a small one (520 x 3584, under 2^22 weights),
-    257 and 600 on a smaller one (250 x 1536, under 2^19),
+    257 and 600 on a smaller one (250 x 1536, under 2^19), 2048 on a
+    narrow one (3000 x 1024: 128-wide tiles by the round count, on 256-row
+    tiles for int4 with bf16 activations),
     17..257 on long rows (1024 x 16512), against the oracle."""
     rng = np.random.default_rng(6160 + kind)
     for N, K, Ts in ((20000, 1024, (17, 32, 33, 64, 65, 128, 129, 256, 257, 520)),
                      (3000, 2048, (17, 32, 33, 64, 65, 128, 129, 256, 257, 520)),
                      (520, 3584, (65, 200, 256, 257)),
                      (250, 1536, (257, 600)),
+                     (3000, 1024, (2048,)),
                      (1024, 16512, (17, 32, 33, 64, 129, 257))):
         W = Packed(rng, N, K, kind)
         for T in Ts:
