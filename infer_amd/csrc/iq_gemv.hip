@@ -2274,7 +2274,12 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         if (e != hipSuccess) return e;
         if (launch_gemvs(W, bias, y, n, M, ws, stream, &e)) return e;
     }
-    if (M >= 5 && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
+    // (and from 3 / 4 rows, int8 / int4, on long rows, G >= 128, which the
+    // 1-row kernel's 4-row instance splits over K ranges: 7B down 3584 x
+    // 18944 int8 at 3 / 4 rows 27.3 / 30.6 -> 24.1 / 24.2 us, int4 at 4 rows
+    // 22.1 -> 20.8; int4 at 2 / 3 rows 17.8 / 19.9 against 20.4 / 20.5)
+    const int m_lo = G >= 128 ? (W[0].kind == 0 ? 3 : 4) : 5;
+    if (M >= m_lo && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
         hipError_t e = hipSuccess;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
         if (!ws->prep_copy) ws->invalidate_prep();
