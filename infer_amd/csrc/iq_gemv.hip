@@ -2303,6 +2303,14 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // 152064 x 3584 int8 at 16 rows: 176 -> 139 us; on the layer shapes it
     // measured no better than gemvh / gemvt: gate|up 41.7 -> 42.8, down
     // 33.6 -> 34.5 us at its best K split)
+    // ... except int4, and int8 at 9..10 rows, on gemvq straight from x (7B
+    // lm_head int4 at 9 / 12 / 16 rows 109 / 109 / 110 -> 93 / 99 / 104 us,
+    // int8 at 9 rows 153 -> 142 us; int8 at 12 / 16 rows 144 / 143 against
+    // 144 / 160)
+    if (M > 8 && M <= 16 && K % kGroup == 0 && total_tiles(W, n) >= 4096 && (W[0].kind == 1 || M <= 10)) {
+        hipError_t e = hipSuccess;
+        if (launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
+    }
     if (M > 8 && M <= 16 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
         hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream);
         if (e != hipSuccess) return e;

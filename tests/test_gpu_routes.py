@@ -129,7 +129,7 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("M", [1, 5, 9, 16])
 def test_lm_head_int8(M):
     """The int8 lm_head 152064 x 3584 (9504 tiles)."""
     rng = np.random.default_rng(152064 + M)
@@ -144,12 +144,13 @@ def test_lm_head_int8(M):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M", [5, 7, 8, 9, 13, 16])
+@pytest.mark.parametrize("M", [5, 7, 8, 9, 10, 11, 13, 16])
 def test_wide_call_5_to_16_rows(kind, M):
     """Over 4096 16-row tiles (here 65541 rows, the last tile ragged, and a
     second matrix in the same call) at 5..16 rows: the gemvr route on the
-    packed hi/lo operands (5..6 rows) and the gemvs route on 16-row operand
-    blocks (7..16)."""
+    packed hi/lo operands (5..6 rows), the gemvs route on 16-row operand
+    blocks (7..8, int8 at 11..16) and gemvq straight from x (int4 at 9..16,
+    int8 at 9..10)."""
     rng = np.random.default_rng(4096 + 10 * M + kind)
     K = 1024
     Ws = [Packed(rng, 65541, K, kind), Packed(rng, 300, K, kind)]
