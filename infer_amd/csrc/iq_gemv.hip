@@ -1959,7 +1959,7 @@ bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K, int n) {
     return M >= 17 && M <= 32 && K % kGroup == 0 && (tiles >= 224 || K / kGroup >= 128 || n > 1);
 }
 
-// gemvq on n matrices, M in 9..32, straight from x (false: M out of range;
+// gemvq on n matrices, M in 7..32, straight from x (false: M out of range;
 // partial sums beyond the workspace are avoided by looping over K ranges).
 bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                   Workspace* ws, hipStream_t stream, hipError_t* err) {
@@ -1972,7 +1972,7 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
         t32 += int((W[i].rows + 31) / 32);
     }
     const int nrb = (t32 + 7) / 8;
-    if (M < 9 || M > 32) return false;
+    if (M < 7 || M > 32) return false;
     // ranges of at most ngr groups (the weights of a range are held in
     // registers: 64 per lane at one row block; the operands of 2 blocks x 4
     // groups fill 64 KiB of LDS), and enough workgroups for two per CU
@@ -2268,6 +2268,13 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // 7..8 rows on very wide calls (the lm_head): gemvs on the 16-row
     // operand blocks (7B lm_head int8 at 7 / 8 rows: 163 -> 135 / 163 -> 138
     // us; at 5 / 6 rows gemvr stays ahead, 121 / 124 against 137 / 138)
+    // ... and before them gemvq straight from x, rows past 8 of its 16-row
+    // block reading zero (7 / 8 rows: lm_head int4 109 / 109 -> 90 / 91 us,
+    // int8 141 / 141 -> 136 / 137 us; at 5 / 6 rows gemvr stays ahead)
+    if (M >= 7 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
+        hipError_t e = hipSuccess;
+        if (launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
+    }
     if (M >= 7 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
         if (!ws->prep_copy) ws->invalidate_prep();
         hipError_t e = launch_xhprep(x, M, K, W[0].kind, ws, stream, false);
