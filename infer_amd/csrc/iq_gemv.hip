@@ -2268,10 +2268,11 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // 7..8 rows on very wide calls (the lm_head): gemvs on the 16-row
     // operand blocks (7B lm_head int8 at 7 / 8 rows: 163 -> 135 / 163 -> 138
     // us; at 5 / 6 rows gemvr stays ahead, 121 / 124 against 137 / 138)
-    // ... and before them gemvq straight from x, rows past 8 of its 16-row
-    // block reading zero (7 / 8 rows: lm_head int4 109 / 109 -> 90 / 91 us,
-    // int8 141 / 141 -> 136 / 137 us; at 5 / 6 rows gemvr stays ahead)
-    if (M >= 7 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
+    // ... and before them, for int4, gemvq straight from x, rows past 8 of
+    // its 16-row block reading zero (7 / 8 rows: lm_head int4 109 / 109 ->
+    // 90 / 91 us; at 5 / 6 rows gemvr stays ahead; int8, whose launch alone
+    // measured 141 -> 136 us, made the 7B step at 8 rows 2094 -> 2117 us)
+    if (W[0].kind == 1 && M >= 7 && M <= 8 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
         hipError_t e = hipSuccess;
         if (launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
     }
@@ -2310,11 +2311,11 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // 152064 x 3584 int8 at 16 rows: 176 -> 139 us; on the layer shapes it
     // measured no better than gemvh / gemvt: gate|up 41.7 -> 42.8, down
     // 33.6 -> 34.5 us at its best K split)
-    // ... except int4, and int8 at 9..10 rows, on gemvq straight from x (7B
-    // lm_head int4 at 9 / 12 / 16 rows 109 / 109 / 110 -> 93 / 99 / 104 us,
-    // int8 at 9 rows 153 -> 142 us; int8 at 12 / 16 rows 144 / 143 against
-    // 144 / 160)
-    if (M > 8 && M <= 16 && K % kGroup == 0 && total_tiles(W, n) >= 4096 && (W[0].kind == 1 || M <= 10)) {
+    // ... except int4, on gemvq straight from x (7B lm_head int4 at 9 / 12 /
+    // 16 rows 109 / 109 / 110 -> 93 / 99 / 104 us; int8 at 9 / 16 rows 153 /
+    // 143 against 142 / 160 for the launch alone, and no faster in the 7B
+    // step at 9 / 10 rows)
+    if (W[0].kind == 1 && M > 8 && M <= 16 && K % kGroup == 0 && total_tiles(W, n) >= 4096) {
         hipError_t e = hipSuccess;
         if (launch_gemvq(x, W, bias, y, n, M, ws, stream, &e)) return e;
     }

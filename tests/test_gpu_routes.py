@@ -149,8 +149,7 @@ def test_wide_call_5_to_16_rows(kind, M):
     """Over 4096 16-row tiles (here 65541 rows, the last tile ragged, and a
     second matrix in the same call) at 5..16 rows: the gemvr route on the
     packed hi/lo operands (5..6 rows), the gemvs route on 16-row operand
-    blocks (int8 at 11..16) and gemvq straight from x (7..8 rows, int4 at
-    9..16, int8 at 9..10)."""
+    blocks (int8 at 7..16) and gemvq straight from x (int4 at 7..16)."""
     rng = np.random.default_rng(4096 + 10 * M + kind)
     K = 1024
     Ws = [Packed(rng, 65541, K, kind), Packed(rng, 300, K, kind)]
