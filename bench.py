@@ -3,7 +3,7 @@
 MI355X.
 
 Step (the timed unit): one decode step's worth of quantised linears of
-Qwen2.5-7B at 1 activation row: 28 layers x (q 3584x3584,
+Qwen2.5-7B at 1 activation row (the headline configuration): 28 layers x (q 3584x3584,
 k/v 512x3584, o 3584x3584, gate/up 18944x3584, down 3584x18944) in int4
 (group 128, bf16 scale, u8 zero point) plus the int8 lm_head 152064x3584,
 weights seeded ~N(0, 0.02) -> bf16 -> quantised on the device (bit-exact to

@@ -5,7 +5,8 @@
 // TEST INFRASTRUCTURE ONLY: used in the build container to write the golden
 // fixtures under tests/golden/ and to cross-check oracle/iq_oracle.c.  It is
 // not part of libiq.so, never built on the GPU box (the reference tree is
-// absent there), and kept off the GPU box: .gpurunignore lists oracle/_ref.
+// absent there), and its build output (oracle/_ref) is excluded from the
+// tree copied to the GPU machines.
 #include "quant.h"
 #include "f16.h"
 

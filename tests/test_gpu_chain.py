@@ -8,7 +8,7 @@ own input vectors (every intermediate has its own buffer): the GEMV
 conditioning tolerance of tests/test_ops_gpu.cu:199-206 (5e-6 of sum |w x|),
 propagated through the SwiGLU and residual epilogues.  End to end, the
 logits are within max|err| / max|ref| <= 1e-3 of the float64 forward
-(BASELINE.json's tolerance).  Also: determinism over runs, a 7B-shaped
+(the tolerance stated for the decode path).  Also: determinism over runs, a 7B-shaped
 chain (28 layers, int4 layers, int8 head) checked stage by stage on
 sampled rows, and the host's overlap check (IQ_EALIAS)."""
 import ctypes
