@@ -691,7 +691,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 (int8 lm_head) weights x fp32 activations: exact int32 MFMA sums, fp32 accumulation",
+        "dtype": "int4 (int8 lm_head) weights x fp32 activations as per-128-column-group 31-bit fixed point (four byte limbs, rounding <= 2^-31 of the group max): exact int32 MFMA sums, fp32 accumulation",
         "data": "synthetic",
         "config": {
             "workload": "Qwen2.5-7B decode linear set, int4 group-128 (bf16 scale, u8 zero) x 28 layers "

@@ -89,7 +89,7 @@ int iq_gemv_noalloc(const float* x, const iq_view* W, const uint16_t* bias, int 
  * iq_gemv_prep takes x [B][in] (fp32) once into the device workspace: a
  * copy for B <= 4 (the GEMV kernel converts it itself), otherwise per row
  * and 128-column group a power-of-two scale 2^-k and x * 2^k as two fp16
- * terms (or as three signed byte limbs of rint(x * 2^k)), in the column
+ * terms (or as four signed byte limbs of rint(x * 2^k)), in the column
  * order that `kind`'s weight unpacking produces;
  * iq_gemv_prepped then runs the GEMV of any matrix of that kind and width on
  * the prepared block.  A prepared block belongs to the stream it was made

@@ -130,7 +130,7 @@ __device__ __forceinline__ float row16_fsum(float v) {
 // and up tiles of the same rows (each wave holds both tiles' weights of its
 // slice and multiplies both by the same activation operand).  Wave w owns
 // the K slice [w gs, w gs + gs).  NG = slice capacity in groups (a multiple
-// of 4).  Dynamic LDS: limb records [G][384] | meta [G] int4 | (RMSNorm
+// of 4).  Dynamic LDS: limb records [G][512] | meta [G] int4 | (RMSNorm
 // without producer partials) the raw input [K] fp32.
 template <int KIND, int NG, int TP, int NORM>
 __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void stage_kernel(const CStage st) {
@@ -338,15 +338,15 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
         if (ok && ln == 0) ms[g] = md;
     }
 
-    // 4. Codes x limbs: A rows 0..2 = limbs 0..2 (lanes 0..15 hold the three
-    //    sums of row ln in D[0..2]); the wave reads only its own records.
+    // 4. Codes x limbs: A rows 0..3 = limbs 0..3 (lanes 0..15 hold the four
+    //    sums of row ln in D[0..3]); the wave reads only its own records.
     //    (Fully unrolled with a wave-uniform guard: a loop the compiler does
     //    not unroll indexes the weight registers dynamically, which moves
     //    them to scratch memory.)
     float acc[TP];
 #pragma unroll
     for (int t = 0; t < TP; t++) acc[t] = 0.0f;
-    const bool alive = ln < 3;
+    const bool alive = ln < kLimbs;
 #pragma unroll
     for (int gl = 0; gl < NG; gl++) {
         if (gl >= gs) continue;  // wave-uniform
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
             const int z = KIND != 1 ? 0
                           : (G % 4 == 0 ? int((zw[t][(gl >> 2) * 2] >> (8 * (gl & 3))) & 0xFF)
                                         : int((zw[t][gl >> 1] >> (8 * (gl & 1))) & 0xFF));
-            acc[t] = combine(acc[t], D[0], D[1], D[2], z, md, sc);
+            acc[t] = combine(acc[t], D[0], D[1], D[2], D[3], z, md, sc);
         }
     }
 
@@ -416,11 +416,16 @@ template <int KIND>
 hipError_t launch_stage_k(const HostStage& h, hipStream_t stream) {
     const dim3 grid(unsigned(h.st.units)), block(unsigned(64 * h.st.ks));
     const int norm = h.st.in_op != IQ_IN_RMSNORM ? 0 : (h.st.ssq_in ? 1 : 2);
+#define IQ_STAGE1(NG_, TP_, N_)                                                             \
+    do {                                                                                    \
+        allow_big_lds<stage_kernel<KIND, NG_, TP_, N_>>();                                  \
+        stage_kernel<KIND, NG_, TP_, N_><<<grid, block, h.lds, stream>>>(h.st);             \
+    } while (0)
 #define IQ_STAGE(NG_, TP_)                                                                  \
     do {                                                                                    \
-        if (norm == 1) stage_kernel<KIND, NG_, TP_, 1><<<grid, block, h.lds, stream>>>(h.st); \
-        else if (norm == 2) stage_kernel<KIND, NG_, TP_, 2><<<grid, block, h.lds, stream>>>(h.st); \
-        else stage_kernel<KIND, NG_, TP_, 0><<<grid, block, h.lds, stream>>>(h.st);         \
+        if (norm == 1) IQ_STAGE1(NG_, TP_, 1);                                              \
+        else if (norm == 2) IQ_STAGE1(NG_, TP_, 2);                                         \
+        else IQ_STAGE1(NG_, TP_, 0);                                                        \
     } while (0)
     if (h.st.tpu == 2) {
         if (h.ng == 4) IQ_STAGE(4, 2);
@@ -436,6 +441,7 @@ hipError_t launch_stage_k(const HostStage& h, hipStream_t stream) {
         }
     }
 #undef IQ_STAGE
+#undef IQ_STAGE1
     return hipGetLastError();
 }
 

@@ -10,23 +10,28 @@
 // integers: v_mfma_i32_16x16x64_i8.  The fp32 activations are turned into
 // integers once per call (xprep):
 //   per (activation row m, 128-column group g): 2^k with
-//   max|x| * 2^k in [2^21, 2^22), X = rint(x * 2^k) (exact scaling, one
-//   rounding: |x*2^k - X| <= 1/2, i.e. 2^-22 of the group's max), and X is
-//   written as three signed byte limbs, X = 2^16 X0 + 2^8 X1 + X2.
-// The GEMV then forms, per (row tile, group), three exact int32 sums
-//   S_L = sum_k q_k * X_L,k        (L = 0, 1, 2; 6 MFMAs per 128 columns)
+//   max|x| * 2^k in [2^30, 0x7F7F7F7F], X = rint(x * 2^k) (exact scaling,
+//   one rounding: |x*2^k - X| <= 1/2, i.e. at most 2^-31 of the group's
+//   max), and X is written as four signed byte limbs,
+//   X = 2^24 X0 + 2^16 X1 + 2^8 X2 + X3.
+// The GEMV then forms, per (row tile, group), four exact int32 sums
+//   S_L = sum_k q_k * X_L,k        (L = 0..3; the four limbs of one
+//                                   activation row are four rows of the
+//                                   16-row MFMA tile)
 // and for int4 subtracts the zero point exactly in integers,
 //   T_L = S_L - z * sum_k X_L,k    (the limb sums come with the limbs),
 // so the only floating-point steps are
-//   acc += ldexp(s * (65536 T_0 + 256 T_1 + T_2), -k)       (fp32).
+//   acc += ldexp(s * (2^24 T_0 + 2^16 T_1 + 2^8 T_2 + T_3), -k)   (fp32).
 // The int8 codes go to the MFMA untouched; int4 nibbles need one AND (even
 // columns) or one shift + AND (odd columns) per 4 codes.
 //
-// Accuracy: the activation rounding is at most 2^-22 of the group's largest
+// Accuracy: the activation rounding is at most 2^-31 of the group's largest
 // |x| per element, products and sums are exact integers, and the fp32
-// combination adds a few ulps: far inside the reference's 5e-6 of the
-// conditioning sum |w*x| (tests/test_ops_gpu.cu:199-206).  Non-finite
-// activations make the affected outputs NaN.
+// combination adds a few ulps of each group's partial sum.  A group whose
+// largest value is 10^5 x its typical one (an outlier channel of an LLM's
+// residual stream) still keeps ~14 bits of its typical values, inside the
+// reference's 5e-6 of the conditioning sum |w*x| (tests/test_ops_gpu.cu:
+// 199-206).  Non-finite activations make the affected outputs NaN.
 //
 // Kernels:
 //  * gemv1 (1 row, the decode step): workgroup = W waves on one tile of 16
@@ -259,12 +264,12 @@ __device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParam
 }
 
 // Multiplies one tile's slice by the staged activation limbs.  R = 1: the A
-// operand carries the three limbs as rows 0..2 of the 16-row MFMA tile
-// (lanes l%16 = 0, 1, 2; the other lanes read a zero block), so two MFMAs per
-// 128 columns give all three exact limb sums, in D rows 0..2 of lanes 0..15.
-// R = 4: A row 4m + L = limb L of activation row m < M (rows 4m + 3 and rows
-// of m >= M zero), so the same two MFMAs give row m's limb sums in D rows
-// 4m .. 4m + 2, i.e. registers 0..2 of lanes 16m .. 16m + 15.  Returns the
+// operand carries the four limbs as rows 0..3 of the 16-row MFMA tile
+// (lanes l%16 = 0..3; the other lanes read a zero block), so two MFMAs per
+// 128 columns give all four exact limb sums, in D rows 0..3 of lanes 0..15.
+// R = 4: A row 4m + L = limb L of activation row m < M (rows of m >= M
+// zero), so the same two MFMAs give row m's limb sums in D rows
+// 4m .. 4m + 3, i.e. registers 0..3 of lanes 16m .. 16m + 15.  Returns the
 // running sum of activation row l/16 (R = 4) or row 0 (R = 1, lanes 0..15).
 template <int KIND, int NG, int R>
 __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_t* xs, const int4* ms,
@@ -274,7 +279,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
     // the first of them group glo)
     float acc = 0.0f;
     const int am = R == 1 ? 0 : ln >> 2, aL = R == 1 ? ln : ln & 3;  // A row of this lane
-    const bool alive = aL < 3 && am < M;
+    const bool alive = am < M;
     const int xoff = (am * RS - glo) * kLimbRec + aL * kGroup + kg * 16;
     const int moff = (R == 1 ? 0 : kg) * RS - glo;
     // blocks of 4 groups: an early exit over at most 8 iterations still
@@ -306,7 +311,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
             const uint32_t sw = b.s[gl / 2];
             const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
             const int z = KIND == 1 ? int((b.z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
-            const float nacc = combine(acc, D[0], D[1], D[2], z, ms[moff + g], sc);
+            const float nacc = combine(acc, D[0], D[1], D[2], D[3], z, ms[moff + g], sc);
             acc = ok ? nacc : acc;
         }
     }
@@ -324,7 +329,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // order, so the sum is deterministic and no wave waits for the others.
 template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
-    // dynamic LDS: limbs [RR][G][384], meta [R][G] int4, then (staged) the
+    // dynamic LDS: limbs [RR][G][512], meta [R][G] int4, then (staged) the
     // tile's scales [16][G] bf16 and zero points [16][G] u8.  R = 8 runs
     // two blocks of 4 rows through the same limb records (each wave reuses
     // its own groups' records; the weights stay in registers).
@@ -475,15 +480,15 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
 // Activation rows on the MFMA A operand (16 rows):
 //   ROWS4 (M <= 8): row 4*mm + L = limb L of activation row mt*4 + mm, so a
 //     tile of 4 activation rows needs 2 MFMAs per 128 columns, and lane
-//     (l%16 = n, l/16 = mm) ends with the 3 limb sums of one (row, n).
+//     (l%16 = n, l/16 = mm) ends with the 4 limb sums of one (row, n).
 //   otherwise: A row i = activation row mt*16 + i, one MFMA per limb
-//     (6 per 128 columns for 16 rows); D register r of limb L's MFMA holds
+//     (8 per 128 columns for 16 rows); D register r of limb L's MFMA holds
 //     (row mt*16 + 4*(l/16) + r, n = l%16).
 // With S > 1 slices (matrices too short to fill the GPU) each slice writes
 // fp32 partial sums and gemv_reduce adds them in slice order (deterministic).
 template <int KIND, bool ROWS4, int MT, int GC, bool VEC>
 __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
-    extern __shared__ __attribute__((aligned(16))) int8_t xsb[];  // [GC][M][384] limbs, [GC][32] meta
+    extern __shared__ __attribute__((aligned(16))) int8_t xsb[];  // [GC][M][512] limbs, [GC][32] meta
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
     constexpr int NT = 512;
     constexpr int WPG = KIND == 1 ? 1 : 2;
@@ -530,7 +535,7 @@ __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
         _Pragma("unroll") for (int i = 0; i < XPT; i++) {                                               \
             const int t = tid + i * NT < lim_ ? tid + i * NT : lim_ - 1;                                \
             const int gl = t / (xrec / 16), rem = t % (xrec / 16);                                      \
-            xr[i] = *reinterpret_cast<const int4v_t*>(p.xq + (int64_t(rem / 24) * G + g0_ + gl) * kLimbRec + (rem % 24) * 16); \
+            xr[i] = *reinterpret_cast<const int4v_t*>(p.xq + (int64_t(rem / (kLimbRec / 16)) * G + g0_ + gl) * kLimbRec + (rem % (kLimbRec / 16)) * 16); \
         }                                                                                               \
         mr = reinterpret_cast<const int4v_t*>(p.meta)[(g0_ + (tid / kMeta < ng_ ? tid / kMeta : ng_ - 1)) * kMeta + tid % kMeta]; \
     } while (0)
@@ -579,18 +584,18 @@ __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
                     int4v_t a[2];
 #pragma unroll
                     for (int st = 0; st < 2; st++) {
-                        const int8_t* pa = (L < 3 && m < M) ? xsb + (gl * M + m) * kLimbRec + L * kGroup + st * 64 + kg * 16 : xzero;
+                        const int8_t* pa = m < M ? xsb + (gl * M + m) * kLimbRec + L * kGroup + st * 64 + kg * 16 : xzero;
                         a[st] = *reinterpret_cast<const int4v_t*>(pa);
                     }
                     int4v_t D = mfma_i8(a[0], b0, int4v_t{0, 0, 0, 0});
                     D = mfma_i8(a[1], b1, D);
                     const int mo = mt * 4 + kg;  // activation row of this lane's D
-                    if (mo < M) acc[mt][0] = combine(acc[mt][0], D[0], D[1], D[2], z, msb[gl * kMeta + mo], s);
+                    if (mo < M) acc[mt][0] = combine(acc[mt][0], D[0], D[1], D[2], D[3], z, msb[gl * kMeta + mo], s);
                 } else {
                     const int m = mt * 16 + ln;
-                    int4v_t D[3];
+                    int4v_t D[kLimbs];
 #pragma unroll
-                    for (int L = 0; L < 3; L++) {
+                    for (int L = 0; L < kLimbs; L++) {
                         int4v_t a[2];
 #pragma unroll
                         for (int st = 0; st < 2; st++) {
@@ -603,7 +608,7 @@ __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int mo = mt * 16 + 4 * kg + r;
-                        if (mo < M) acc[mt][r] = combine(acc[mt][r], D[0][r], D[1][r], D[2][r], z, msb[gl * kMeta + mo], s);
+                        if (mo < M) acc[mt][r] = combine(acc[mt][r], D[0][r], D[1][r], D[2][r], D[3][r], z, msb[gl * kMeta + mo], s);
                     }
                 }
             }
@@ -652,11 +657,11 @@ __global__ __launch_bounds__(512) void gemvb_kernel(const GemvParams p) {
 // ranges: workgroup (u, s) writes its range's sums to part[s][m][16*tile + n]
 // and gemvt_reduce_kernel adds the ranges of every matrix in one launch.
 // A operand layouts: up to 12 rows, quad layout: A tile q row 4*mm + L =
-// limb L of activation row 4q + mm (rows 4*mm + 3 zero), two MFMAs per 128
-// columns give the three limb sums of four rows, lane (n = l%16, mm = l/16)
-// holding those of (row 4q + mm, output n).  13..16 rows, limb-major: A
-// tile L = limb L of the 16 rows (six MFMAs per group instead of eight),
-// lane (n, mm) holding rows 4*mm + i in D[i].
+// limb L of activation row 4q + mm, two MFMAs per 128 columns give the
+// four limb sums of four rows, lane (n = l%16, mm = l/16) holding those of
+// (row 4q + mm, output n).  13..16 rows, limb-major: A tile L = limb L of
+// the 16 rows (eight MFMAs per group), lane (n, mm) holding rows 4*mm + i
+// in D[i].
 constexpr int kGtTmax = 8;     // tiles per wave
 constexpr int kGtChunks = 16;  // staged 16-byte chunks per thread
 
@@ -665,7 +670,7 @@ __global__ __launch_bounds__(512) void gemvt_kernel(const GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) int4 gsm4[];
     constexpr int WPG = KIND == 1 ? 1 : 2;
     constexpr bool LM = MQ == 4;       // limb-major A
-    constexpr int NA = LM ? 3 : MQ;    // A tiles per 64 columns
+    constexpr int NA = LM ? kLimbs : MQ;  // A tiles per 64 columns
     constexpr int NACC = LM ? 4 : MQ;  // running sums per lane
     constexpr int NM = MQ * 4;         // meta records per group
     constexpr int CH = kGtChunks;
@@ -699,7 +704,7 @@ __global__ __launch_bounds__(512) void gemvt_kernel(const GemvParams p) {
             const int blk = c >> 6, l = c & 63;
             const int gl = blk / (NA * 2), q = (blk >> 1) % NA, st = blk & 1;
             const int m = LM ? (l & 15) : 4 * q + ((l & 15) >> 2), L = LM ? q : l & 3, kgl = l >> 4;
-            const bool ok = c < total && L < 3 && m < M;
+            const bool ok = c < total && m < M;
             const uint32_t off = uint32_t(m * G + g0 + gl) * kLimbRec + uint32_t(L * kGroup + st * 64 + kgl * 16);
             v[i] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? off : kOob, 0, 0));
         }
@@ -788,20 +793,20 @@ __global__ __launch_bounds__(512) void gemvt_kernel(const GemvParams p) {
             const int4* ag = As + cg * (NA * 2 * 64) + lane;
             const int4* mg = ms + cg * NM;
             if (LM) {
-                int4v_t Dv[3];
+                int4v_t Dv[kLimbs];
 #pragma unroll
-                for (int L = 0; L < 3; L++) {
+                for (int L = 0; L < kLimbs; L++) {
                     Dv[L] = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * L) * 64]), b0, int4v_t{0, 0, 0, 0});
                     Dv[L] = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * L + 1) * 64]), b1, Dv[L]);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[j] = combine(acc[j], Dv[0][j], Dv[1][j], Dv[2][j], z, mg[4 * kg + j], sc);
+                for (int j = 0; j < 4; j++) acc[j] = combine(acc[j], Dv[0][j], Dv[1][j], Dv[2][j], Dv[3][j], z, mg[4 * kg + j], sc);
             } else {
 #pragma unroll
                 for (int q = 0; q < MQ; q++) {
                     int4v_t Dv = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * q) * 64]), b0, int4v_t{0, 0, 0, 0});
                     Dv = mfma_i8(__builtin_bit_cast(int4v_t, ag[(2 * q + 1) * 64]), b1, Dv);
-                    acc[q] = combine(acc[q], Dv[0], Dv[1], Dv[2], z, mg[4 * q + kg], sc);
+                    acc[q] = combine(acc[q], Dv[0], Dv[1], Dv[2], Dv[3], z, mg[4 * q + kg], sc);
                 }
             }
             const bool flush = cg == RG - 1;
@@ -874,13 +879,21 @@ void launch_gemvb_t(const GemvParams& p, bool vec, unsigned grid, size_t lds, hi
     const int M = p.M;
 #define IQ_GB(R4, MT)                                                                         \
     do {                                                                                      \
-        if (vec) gemvb_kernel<KIND, R4, MT, GC, true><<<grid, 512, lds, stream>>>(p);         \
-        else gemvb_kernel<KIND, R4, MT, GC, false><<<grid, 512, lds, stream>>>(p);            \
+        if (vec) {                                                                            \
+            allow_big_lds<gemvb_kernel<KIND, R4, MT, GC, true>>();                            \
+            gemvb_kernel<KIND, R4, MT, GC, true><<<grid, 512, lds, stream>>>(p);              \
+        } else {                                                                              \
+            allow_big_lds<gemvb_kernel<KIND, R4, MT, GC, false>>();                           \
+            gemvb_kernel<KIND, R4, MT, GC, false><<<grid, 512, lds, stream>>>(p);             \
+        }                                                                                     \
     } while (0)
     if (M <= 4) IQ_GB(true, 1);
     else if (M <= 8) IQ_GB(true, 2);
-    else if (M <= 16) IQ_GB(false, 1);
-    else IQ_GB(false, 2);
+    else if constexpr (GC <= 4) {
+        // (8-group chunks of 9..32 rows would spill the staging registers)
+        if (M <= 16) IQ_GB(false, 1);
+        else IQ_GB(false, 2);
+    }
 #undef IQ_GB
 }
 
@@ -940,7 +953,8 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
         pl.kr = int((G + pl.gr - 1) / pl.gr);
         if (pl.kr > 1 && int64_t(pl.kr) * 8 * ntiles * 16 > kPartialFloats) return G1Plan{0, 0, 0, 0, 1, int(G)};
     }
-    if (gemv1_lds(pl.gr, R) > 64 * 1024) return pl;
+    // (1 row: the converted row of up to 296 groups, 7B down's 148 in 78 KiB)
+    if (gemv1_lds(pl.gr, R) > (R == 1 ? 156 : 64) * 1024) return pl;
     const int64_t GR = pl.gr;
     const int maxw = kind == 1 ? 16 : 8;
     pl.ng = kind == 1 ? 12 : 20;
@@ -964,25 +978,31 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
 
 template <int KIND, int NG, int MAXW>
 void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
+#define IQ_G1(MODE_, R_, KSPLIT_)                                                                  \
+    do {                                                                                           \
+        allow_big_lds<gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_>>();                         \
+        gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_><<<grid, 64 * ks, lds, stream>>>(p);       \
+    } while (0)
     if (p.M > 4) {
-        if constexpr (NG <= 4) gemv1_kernel<KIND, NG, 2, MAXW, 8, false><<<grid, 64 * ks, lds, stream>>>(p);
+        if constexpr (NG <= 4) IQ_G1(2, 8, false);
         return;
     }
     if (p.M > 1) {
         if constexpr (NG <= (KIND == 1 ? 4 : 8)) {
             if (mode == 2) {
-                if (p.kr > 1) gemv1_kernel<KIND, NG, 2, MAXW, 4, true><<<grid, 64 * ks, lds, stream>>>(p);
-                else gemv1_kernel<KIND, NG, 2, MAXW, 4, false><<<grid, 64 * ks, lds, stream>>>(p);
+                if (p.kr > 1) IQ_G1(2, 4, true);
+                else IQ_G1(2, 4, false);
             } else {
-                if (p.kr > 1) gemv1_kernel<KIND, NG, 1, MAXW, 4, true><<<grid, 64 * ks, lds, stream>>>(p);
-                else gemv1_kernel<KIND, NG, 1, MAXW, 4, false><<<grid, 64 * ks, lds, stream>>>(p);
+                if (p.kr > 1) IQ_G1(1, 4, true);
+                else IQ_G1(1, 4, false);
             }
         }
         return;
     }
-    if (mode == 2) gemv1_kernel<KIND, NG, 2, MAXW, 1, false><<<grid, 64 * ks, lds, stream>>>(p);
-    else if (mode == 1) gemv1_kernel<KIND, NG, 1, MAXW, 1, false><<<grid, 64 * ks, lds, stream>>>(p);
-    else gemv1_kernel<KIND, NG, 0, MAXW, 1, false><<<grid, 64 * ks, lds, stream>>>(p);
+    if (mode == 2) IQ_G1(2, 1, false);
+    else if (mode == 1) IQ_G1(1, 1, false);
+    else IQ_G1(0, 1, false);
+#undef IQ_G1
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
@@ -1076,7 +1096,7 @@ hipError_t launch_gemv_batched(const QView& W, const uint16_t* bias, int M, floa
     p.xq = ws->xq; p.meta = ws->xmeta;
     p.bias = bias; p.y = y; p.part = ws->partials;
     p.M = M;
-    const int gc = (kind == 1 && M <= 16) ? 8 : 4;  // groups per chunk (LDS: 2 * gc * M * 384 B max)
+    const int gc = (kind == 1 && M <= 8) ? 8 : 4;  // groups per chunk (LDS: gc * (M * 512 + 512) B)
     constexpr int target = 2048;  // waves per 256 CUs the slices aim for
     p.nrb = int((N + 127) / 128);
     const int64_t want_s = (int64_t(target) * device_cu_count() / 256 + int64_t(p.nrb) * 8 - 1) / (int64_t(p.nrb) * 8);
@@ -1113,7 +1133,7 @@ struct GtPlan {
 
 GtPlan gemvt_plan(int64_t G, int tiles, int M, int cus) {
     GtPlan pl;
-    const int mq = (M + 3) / 4, na = mq == 4 ? 3 : mq, nacc = mq == 4 ? 4 : mq;
+    const int mq = (M + 3) / 4, na = mq == 4 ? kLimbs : mq, nacc = mq == 4 ? 4 : mq;
     const int rmax = 96 * 1024 / (na * 2048);
     const int ks = int((G + rmax - 1) / rmax);
     const int gs = int((G + ks - 1) / ks);
@@ -1145,16 +1165,10 @@ GtPlan gemvt_plan(int64_t G, int tiles, int M, int cus) {
 template <int KIND>
 void launch_gemvt_k(const GemvParams& p, const GtPlan& pl, hipStream_t stream) {
     constexpr int D = KIND == 1 ? 16 : 10;  // ~100 VGPRs of weights in flight
-    static const bool attr = [] {
-        // up to 160 KiB of dynamic LDS
-        const void* fns[4] = {reinterpret_cast<const void*>(&gemvt_kernel<KIND, 1, D>),
-                              reinterpret_cast<const void*>(&gemvt_kernel<KIND, 2, D>),
-                              reinterpret_cast<const void*>(&gemvt_kernel<KIND, 3, D>),
-                              reinterpret_cast<const void*>(&gemvt_kernel<KIND, 4, D>)};
-        for (const void* f : fns) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        return true;
-    }();
-    (void)attr;
+    allow_big_lds<gemvt_kernel<KIND, 1, D>>();
+    allow_big_lds<gemvt_kernel<KIND, 2, D>>();
+    allow_big_lds<gemvt_kernel<KIND, 3, D>>();
+    allow_big_lds<gemvt_kernel<KIND, 4, D>>();
     switch (pl.mq) {
         case 1: gemvt_kernel<KIND, 1, D><<<pl.grid, 64 * pl.kw, pl.lds, stream>>>(p); break;
         case 2: gemvt_kernel<KIND, 2, D><<<pl.grid, 64 * pl.kw, pl.lds, stream>>>(p); break;
@@ -2106,7 +2120,7 @@ bool gemvh_applies(int64_t K, int M) {
 // Direct calls (x given with the matrices) pick per shape, from 7B and
 // 1.5B measurements at 2..16 rows: gemvh for narrow calls (< 512 tiles: 7B
 // q|k|v 13.7 against 16 us, o 10.8 against 16); gemvt, whose workgroups share
-// one LDS copy of the activations over many tiles and pack 4 rows x 3 limbs
+// one LDS copy of the activations over many tiles and pack 4 rows x 4 limbs
 // per MFMA up to 8 rows, for wider calls up to 8 rows and for 1024..4095-tile
 // calls with short K (7B gate|up: 27..38 against 47..48 us); gemvh otherwise
 // (lm_head at 12..16 rows: 173 against 184 us).

@@ -26,9 +26,9 @@ struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
     float* xf = nullptr;       // [4][kMaxKp] fp32: 1..4 activation rows copied by a prep
-    int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][3*128] limbs, or the f16 hi/lo
+    int8_t* xq = nullptr;      // [kMaxRowsGemv][kMaxKp/128][4*128] limbs, or the f16 hi/lo
                                // A operands [kMaxRowsGemv/16][kMaxKp/128][8 KiB] (gemvh)
-    int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, sum X0, 256 sum X1 + sum X2, 0}
+    int4* xmeta = nullptr;     // [kMaxKp/128][kMaxRowsGemv] {2^-k, 256 sum X0 + sum X1, 256 sum X2 + sum X3, 0}
     float* partials = nullptr; // part_floats (>= kPartialFloats)
     int64_t part_floats = 0;   // capacity of partials
     size_t xq_bytes = 0, xmeta_bytes = 0;
@@ -104,6 +104,24 @@ hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16*
 // A validated stage program on the device (iq_chain.hip).
 struct Chain;
 void chain_destroy(Chain* ch);
+
+// Lets kernel F take up to 160 KiB of LDS (gfx950's LDS per CU) in static
+// plus dynamic allocations; once per kernel instance and process.  A failed
+// attribute call is cleared from the runtime's last-error slot (a launch
+// past the default limit then reports its own error).
+template <auto F>
+inline void allow_big_lds() {
+    static const bool once = [] {
+        const void* f = reinterpret_cast<const void*>(F);
+        hipFuncAttributes a{};
+        size_t stat = 0;
+        if (hipFuncGetAttributes(&a, f) == hipSuccess) stat = a.sharedSizeBytes;
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(160 * 1024 - stat)) != hipSuccess)
+            (void)hipGetLastError();
+        return true;
+    }();
+    (void)once;
+}
 
 // Device properties used by the dispatch heuristics.
 int device_cu_count();

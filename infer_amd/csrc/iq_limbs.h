@@ -3,11 +3,12 @@
 // (DPP row reductions, buffer resources, the per-group fp32 combination).
 //
 // Per (activation row, 128-column group): 2^k with max|x| * 2^k in
-// [2^21, 2^22), X = rint(x * 2^k), written as three signed byte limbs
-// X = 2^16 X0 + 2^8 X1 + X2 (one "limb record" of 3 x 128 bytes), plus a
-// meta record {2^-k, sum X0, 256 sum X1 + sum X2}.  v_mfma_i32_16x16x64_i8
-// then forms exact int32 sums of codes times limbs, and combine() turns a
-// group's three sums into fp32 with one rounding.
+// (2^30, 0x7F7F7F7F] (k the largest power that fits; 30 or 31 significant
+// bits), X = rint(x * 2^k), written as four signed byte limbs
+// X = 2^24 X0 + 2^16 X1 + 2^8 X2 + X3 (one "limb record" of 4 x 128 bytes),
+// plus a meta record {2^-k, 256 sum X0 + sum X1, 256 sum X2 + sum X3}.
+// v_mfma_i32_16x16x64_i8 then forms exact int32 sums of codes times limbs,
+// and combine() turns a group's four sums into fp32.
 #pragma once
 
 #include "iq_internal.h"
@@ -17,7 +18,8 @@ namespace iq {
 typedef int int4v_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMeta = kMaxRowsGemv;   // meta records per group (one per row slot)
-constexpr int kLimbRec = 3 * kGroup;  // bytes of limbs per (row, group)
+constexpr int kLimbs = 4;                // byte limbs per activation value
+constexpr int kLimbRec = kLimbs * kGroup;  // bytes of limbs per (row, group)
 
 __device__ __forceinline__ int4v_t mfma_i8(int4v_t a, int4v_t b, int4v_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -82,59 +84,68 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
     return v;
 }
 
-// Three limb words (records 0, 1, 2 = X0, X1, X2) of the four values whose
-// biased integers U = X + 0x808080 are u0..u3, in that byte order: limb L of
-// a value is byte 2-L of U minus 128, i.e. that byte with its top bit flipped.
-__device__ __forceinline__ void pack_limbs(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t u3, uint32_t (&w)[3]) {
+// Four limb words (records 0..3 = X0..X3) of the four values whose biased
+// integers U = X + 0x80808080 are u0..u3, in that byte order: limb L of a
+// value is byte 3-L of U minus 128, i.e. that byte with its top bit flipped.
+__device__ __forceinline__ void pack_limbs(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t u3, uint32_t (&w)[kLimbs]) {
     const uint32_t p = __builtin_amdgcn_perm(u1, u0, 0x05010400u);   // u0.b0 u1.b0 u0.b1 u1.b1
     const uint32_t q = __builtin_amdgcn_perm(u3, u2, 0x05010400u);   // u2.b0 u3.b0 u2.b1 u3.b1
-    const uint32_t p2 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 ..
-    const uint32_t q2 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);  // u2.b2 u3.b2 ..
-    w[0] = __builtin_amdgcn_perm(q2, p2, 0x05040100u) ^ 0x80808080u;
-    w[1] = __builtin_amdgcn_perm(q, p, 0x07060302u) ^ 0x80808080u;
-    w[2] = __builtin_amdgcn_perm(q, p, 0x05040100u) ^ 0x80808080u;
+    const uint32_t p2 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 u0.b3 u1.b3
+    const uint32_t q2 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);  // u2.b2 u3.b2 u2.b3 u3.b3
+    w[0] = __builtin_amdgcn_perm(q2, p2, 0x07060302u) ^ 0x80808080u;
+    w[1] = __builtin_amdgcn_perm(q2, p2, 0x05040100u) ^ 0x80808080u;
+    w[2] = __builtin_amdgcn_perm(q, p, 0x07060302u) ^ 0x80808080u;
+    w[3] = __builtin_amdgcn_perm(q, p, 0x05040100u) ^ 0x80808080u;
 }
+
+// Largest biased magnitude four balanced byte limbs hold: 127 * 0x01010101.
+constexpr float kLimbMaxMant = 16711422.0f;  // 0x7F7F7F7F / 128, rounded down (0xFEFEFE)
 
 // Converts one (activation row, 128-column group) whose columns 8j..8j+7
 // are v[] of the lane with j = lane % 16 (the 16 lanes of a DPP row hold the
 // whole group; all 16 must call this together).  Writes this lane's limb
 // bytes into the group's record `rec` (when `store`) and returns the group's
-// meta record {2^-k as fp32 bits, sum X0, 256 sum X1 + sum X2, 0} (every lane).
+// meta record {2^-k as fp32 bits, 256 sum X0 + sum X1, 256 sum X2 + sum X3, 0}
+// (every lane).
 //
-// X = rint(x * 2^k) is formed as the bits of fma(x, 2^k, 1.5 * 2^23): with
-// |x * 2^k| <= 2^22 the sum lies in [2^23, 2^24], where the float's bits
-// minus those of 1.5 * 2^23 are X, rounded to nearest even by the fma.
-// Adding 0x808080 makes each byte of the 24-bit result its limb + 128
-// (balanced limbs in [-128, 127]).
+// amax = f 2^E with f in [0.5, 1): k = 31 - E puts amax 2^k = f 2^31 in
+// [2^30, 2^31); when f 2^31 would pass 0x7F7F7F7F (the largest value four
+// balanced limbs hold, f 2^24 > 0xFEFEFE) k is one less.  x 2^k is exact
+// and rint() rounds it once: |x 2^k - X| <= 1/2, at most 2^-30 of the
+// group's largest |x|.  Adding 0x80808080 makes each byte of X its limb +
+// 128 (balanced limbs in [-128, 127]).
 template <bool PERM>
 __device__ __forceinline__ int4 convert_group(const float (&v)[8], int j, bool store, int8_t* rec) {
-    float am = 0.0f;
+    uint32_t ab = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) am = fmaxf(am, __builtin_fabsf(v[i]));  // NaN ignored here
-    const uint32_t mb = row16_max_u32(__float_as_uint(am));
-    // amax = f * 2^E, f in [0.5, 1): k = 22 - E puts amax * 2^k in [2^21, 2^22)
-    const int k0 = mb < 0x7F800000u ? 22 - __builtin_amdgcn_frexp_expf(__uint_as_float(mb)) : 0;
+    for (int i = 0; i < 8; i++) {
+        const uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;  // NaN / inf sort above every finite value
+        ab = a > ab ? a : ab;
+    }
+    const uint32_t mb = row16_max_u32(ab);
+    const bool fin = mb < 0x7F800000u;
+    const float amax = fin ? __uint_as_float(mb) : 1.0f;
+    const int k0 = 31 - __builtin_amdgcn_frexp_expf(amax) -
+                   (__builtin_amdgcn_frexp_mantf(amax) * 16777216.0f > kLimbMaxMant ? 1 : 0);
     int k = k0;
     float xv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) xv[i] = v[i];
     if (k > 126) {
-        // amax below 2^-104: scale up exactly first so that 2^k stays a float
+        // amax below 2^-95: scale up exactly first so that 2^k stays a float
 #pragma unroll
         for (int i = 0; i < 8; i++) xv[i] = __builtin_amdgcn_ldexpf(xv[i], k - 126);
         k = 126;
     }
     const float p2k = __uint_as_float(uint32_t(k + 127) << 23);
-    uint32_t u[8], hi = 0;
+    uint32_t u[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        u[i] = __float_as_uint(__builtin_fmaf(xv[i], p2k, 12582912.0f)) + (0x808080u - 0x4B400000u);
-        hi |= u[i];
+        // (a non-finite group's integers are never used: its factor is NaN)
+        const float r = fin ? __builtin_rintf(xv[i] * p2k) : 0.0f;
+        u[i] = uint32_t(int(r)) + 0x80808080u;
     }
-    // A finite group leaves byte 3 of every U zero; NaN / inf (either from
-    // the input or, for a group whose amax is inf, from the scaling) do not.
-    const bool fin = row16_or(hi >> 24) == 0;
-    uint32_t a[3], b[3];
+    uint32_t a[kLimbs], b[kLimbs];
     if (PERM) {
         // columns 8j..8j+7: evens -> one word per limb, odds -> one word per limb
         pack_limbs(u[0], u[2], u[4], u[6], a);
@@ -143,37 +154,38 @@ __device__ __forceinline__ int4 convert_group(const float (&v)[8], int j, bool s
         pack_limbs(u[0], u[1], u[2], u[3], a);
         pack_limbs(u[4], u[5], u[6], u[7], b);
     }
-    int sl[3];
+    int sl[kLimbs];
 #pragma unroll
-    for (int L = 0; L < 3; L++)
+    for (int L = 0; L < kLimbs; L++)
         sl[L] = row16_sum(__builtin_amdgcn_sdot4(int(a[L]), 0x01010101, __builtin_amdgcn_sdot4(int(b[L]), 0x01010101, 0, false), false));
     if (store) {
         if (PERM) {
             const int pe = limb_pos(j * 8, true), po = limb_pos(j * 8 + 1, true);
 #pragma unroll
-            for (int L = 0; L < 3; L++) {
+            for (int L = 0; L < kLimbs; L++) {
                 *reinterpret_cast<uint32_t*>(rec + L * kGroup + pe) = a[L];
                 *reinterpret_cast<uint32_t*>(rec + L * kGroup + po) = b[L];
             }
         } else {
 #pragma unroll
-            for (int L = 0; L < 3; L++) *reinterpret_cast<uint2*>(rec + L * kGroup + j * 8) = make_uint2(a[L], b[L]);
+            for (int L = 0; L < kLimbs; L++) *reinterpret_cast<uint2*>(rec + L * kGroup + j * 8) = make_uint2(a[L], b[L]);
         }
     }
     // 2^-k (NaN when the group holds a non-finite value, so it propagates)
     const float fx = fin ? __builtin_amdgcn_ldexpf(1.0f, -k0) : __builtin_nanf("");
-    return make_int4(__float_as_int(fx), sl[0], (sl[1] << 8) + sl[2], 0);
+    return make_int4(__float_as_int(fx), (sl[0] << 8) + sl[1], (sl[2] << 8) + sl[3], 0);
 }
 
-// fp32 value of one group's exact integer limb sums (t_L = S_L - z * sum X_L;
-// md = {2^-k, sum X0, 256 sum X1 + sum X2}, 24-bit multiplies: |z| <= 15,
-// |256 sum X1 + sum X2| < 2^23), times the weight scale and the activation
-// factor 2^-k, added to acc.
-__device__ __forceinline__ float combine(float acc, int d0, int d1, int d2, int z, int4 md, float s) {
-    // hi = t0, lo = 256 t1 + t2 exactly in int32 (|lo| < 2^30); float(lo)
-    // rounds once, as fma(t1, 256, t2) would
-    const int hi = d0 - __mul24(z, md.y);
-    const int lo = (d1 << 8) + d2 - __mul24(z, md.z);
+// fp32 value of one group's exact integer limb sums (t_L = S_L - z sum X_L;
+// md = {2^-k, 256 sum X0 + sum X1, 256 sum X2 + sum X3}, 24-bit multiplies:
+// |z| <= 15 and both limb-sum pairs are below 2^23), times the weight scale
+// and the activation factor 2^-k, added to acc.  hi = 256 t0 + t1 and
+// lo = 256 t2 + t3 are exact in int32 (|t_L| <= 128 * 127 * 128 < 2^21):
+// the group's value 65536 hi + lo is rounded to fp32 with an error of a few
+// ulps of the group's partial sum.
+__device__ __forceinline__ float combine(float acc, int d0, int d1, int d2, int d3, int z, int4 md, float s) {
+    const int hi = (d0 << 8) + d1 - __mul24(z, md.y);
+    const int lo = (d2 << 8) + d3 - __mul24(z, md.z);
     const float v = __builtin_fmaf(float(hi), 65536.0f, float(lo));
     return __builtin_fmaf(v, s * __int_as_float(md.x), acc);
 }
