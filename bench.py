@@ -143,10 +143,24 @@ class Step:
         self.run()  # eager warm-up: workspace and code objects resident
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=capture_stream(torch)):
             self.run()
         torch.cuda.synchronize()
         return g
+
+
+_CAPTURE = None
+
+
+def capture_stream(torch):
+    """The one stream every graph here is captured on, its library
+    workspace reserved first (a capturing stream cannot allocate one)."""
+    global _CAPTURE
+    if _CAPTURE is None:
+        from infer_amd import ops as iq_ops
+        _CAPTURE = torch.cuda.Stream()
+        iq_ops.init(0, _CAPTURE)
+    return _CAPTURE
 
 
 def time_graph(torch, g, steps, warmup):
@@ -375,7 +389,7 @@ def bench_gemv_single(torch, ops, kind, N, K, M, copies, reps=200, seed=11):
     run()
     torch.cuda.synchronize()
     gr = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gr):
+    with torch.cuda.graph(gr, stream=capture_stream(torch)):
         run()
     reps_g = max(1, reps // copies)
     ms_step, _ = time_graph(torch, gr, reps_g, 2)
@@ -412,7 +426,7 @@ def bench_decode_chain(torch, ops, model, steps, warmup):
     step.step(1234)
     torch.cuda.synchronize()
     gr = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gr):
+    with torch.cuda.graph(gr, stream=capture_stream(torch)):
         step.step()
     ms, _ = time_graph(torch, gr, steps, warmup)
     wb = step.weight_bytes()

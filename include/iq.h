@@ -21,12 +21,14 @@
  * arguments are rejected on the host (nothing was enqueued), or a positive
  * hipError_t when the HIP runtime reported an error.  No exception crosses
  * this boundary.  The library keeps one workspace (activation operands,
- * split-K partial sums; about 83 MB) per (device, stream) pair, allocated on
- * the first call that needs it: calls on different streams may overlap, and
- * calls on one stream are ordered by the stream.  A stream under graph
- * capture cannot allocate: without its own workspace (iq_init_stream before
- * the capture) it uses the device's null-stream workspace (iq_init), which
- * it then shares with the null stream.
+ * split-K partial sums, the prefill GEMM's prepared operands; about 167 MB)
+ * per (device, stream) pair, allocated by iq_init / iq_init_stream or on the
+ * first call on that stream: calls on different streams may overlap, and
+ * calls on one stream are ordered by the stream.  After that no call
+ * allocates, frees or synchronises, so any call can be graph-captured the
+ * first time it is made.  A stream under graph capture cannot allocate: a
+ * call on a capturing stream that has no workspace yet (no iq_init_stream
+ * before the capture) returns an error and enqueues nothing.
  */
 #ifndef IQ_H
 #define IQ_H
@@ -196,7 +198,11 @@ typedef struct iq_stage {
 typedef struct iq_chain iq_chain;
 
 /* Validates the n stages and records their launch shapes for the current
- * device (host memory only; the run allocates nothing). */
+ * device.  When an RMSNorm stage reads the output of an earlier stage, the
+ * chain also allocates one small device array (a float per 16-row tile of
+ * each such producer) for the per-tile sums of squares passed between them,
+ * so create a chain outside graph capture, in code that may allocate;
+ * iq_chain_destroy frees it.  iq_chain_run allocates nothing. */
 int iq_chain_create(const iq_stage* stages, int n, iq_chain** out);
 /* Enqueues one run of the whole program on `stream`. */
 int iq_chain_run(const iq_chain* chain, void* stream);

@@ -29,11 +29,12 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 hipError_t create_workspace(Workspace* ws) {
     const int64_t gmax = kMaxKp / kGroup;
     const size_t xf = align256(sizeof(float) * 4 * kMaxKp);  // up to 4 rows copied by a prep
-    // limbs (3 B per value) or f16 hi + lo (4 B per value)
+    // limbs or f16 hi + lo (4 B per value)
     const size_t xq = align256(size_t(kMaxRowsGemv) * gmax * 4 * kGroup);
     const size_t meta = align256(sizeof(int4) * gmax * kMaxRowsGemv);
     const size_t part = align256(sizeof(float) * kStreamPartialFloats);
-    const size_t total = xf + xq + meta + part;
+    const size_t gx = align256(kGemmOperandBytes);
+    const size_t total = xf + xq + meta + part + gx;
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, total);
     if (e != hipSuccess) return e;
@@ -47,6 +48,8 @@ hipError_t create_workspace(Workspace* ws) {
     ws->part_floats = kStreamPartialFloats;
     ws->xq_bytes = xq;
     ws->xmeta_bytes = meta;
+    ws->gx = p + xf + xq + meta + part;
+    ws->gx_bytes = gx;
     return hipSuccess;
 }
 
@@ -99,7 +102,6 @@ hipError_t static_workspace(Workspace** out) {
         w.part_floats = kPartialFloats;
         w.xq_bytes = kStaticXq;
         w.xmeta_bytes = kStaticMeta;
-        w.can_grow = false;
         g_static_ready[dev] = true;
     }
     *out = &g_static_ws[dev];
@@ -114,16 +116,12 @@ hipError_t get_workspace(hipStream_t stream, Workspace** out) {
     std::lock_guard<std::mutex> lk(g_mu);
     const auto key = std::make_pair(dev, stream);
     if (!g_ws.count(key) && stream) {
-        // A stream under graph capture cannot allocate: it uses the device's
-        // null-stream workspace (made by iq_init) unless iq_init_stream gave
-        // it its own before the capture.
+        // A stream under graph capture cannot allocate, and sharing another
+        // stream's workspace would race with that stream's calls: it needs
+        // its own, made by iq_init_stream before the capture.
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
-            auto it = g_ws.find(std::make_pair(dev, hipStream_t(nullptr)));
-            if (it == g_ws.end() || !it->second) return hipErrorStreamCaptureUnsupported;
-            *out = it->second;
-            return hipSuccess;
-        }
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return hipErrorStreamCaptureUnsupported;
     }
     Workspace*& ws = g_ws[key];
     if (!ws) {
@@ -140,36 +138,16 @@ hipError_t get_workspace(hipStream_t stream, Workspace** out) {
     return hipSuccess;
 }
 
-hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs,
-                         hipStream_t stream) {
+int64_t gemm_operand_rows(const Workspace* ws, int64_t K) {
+    // hi + lo fp16 (4 B per value) and one fp32 row factor per row
+    const int64_t rows = int64_t(ws->gx_bytes) / (4 * K + 4 + 256);
+    return rows / 128 * 128;
+}
+
+hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs) {
     const size_t op = size_t(T) * size_t(K) * 2 * (lo ? 2 : 1);
-    const size_t rows = align256(sizeof(float) * size_t(T));
-    if (op <= ws->xq_bytes && sizeof(float) * size_t(T) <= ws->xmeta_bytes) {
-        ws->invalidate_prep();
-        *ah = reinterpret_cast<_Float16*>(ws->xq);
-        *rs = reinterpret_cast<float*>(ws->xmeta);
-        return hipSuccess;
-    }
-    const size_t need = align256(op) + rows;
-    if (need > ws->gx_bytes) {
-        if (!ws->can_grow) return hipErrorInvalidValue;
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (stream && hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return hipErrorStreamCaptureUnsupported;
-        if (ws->gx) {
-            // (earlier launches on the stream may still read the old buffer)
-            hipError_t e = hipStreamSynchronize(stream);
-            if (e != hipSuccess) return e;
-            (void)hipFree(ws->gx);
-            ws->gx = nullptr;
-            ws->gx_bytes = 0;
-        }
-        void* b = nullptr;
-        hipError_t e = hipMalloc(&b, need);
-        if (e != hipSuccess) return e;
-        ws->gx = b;
-        ws->gx_bytes = need;
-    }
+    const size_t need = align256(op) + align256(sizeof(float) * size_t(T));
+    if (!ws->gx || need > ws->gx_bytes) return hipErrorInvalidValue;
     *ah = static_cast<_Float16*>(ws->gx);
     *rs = reinterpret_cast<float*>(static_cast<char*>(ws->gx) + align256(op));
     return hipSuccess;

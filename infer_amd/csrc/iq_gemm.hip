@@ -868,14 +868,15 @@ void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t s
 }
 
 // The fp16 operand path (K % 128 == 0, 16-byte aligned activations): one
-// preparation launch, the GEMM, and the range sums when K is split.
-hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias, int64_t T, float* y,
-                        Workspace* ws, hipStream_t stream) {
+// preparation launch, the GEMM, and the range sums when K is split, for T
+// rows whose operands fit the workspace's operand area.
+hipError_t launch_gemmh_chunk(const float* x_f32, const QView& W, const uint16_t* bias, int64_t T, float* y,
+                              Workspace* ws, hipStream_t stream) {
     constexpr bool lo = true;
     const int64_t K = W.cols;
     _Float16* ah = nullptr;
     float* rs = nullptr;
-    hipError_t e = gemm_operands(ws, T, K, lo, &ah, &rs, stream);
+    hipError_t e = gemm_operands(ws, T, K, lo, &ah, &rs);
     if (e != hipSuccess) return e;
     _Float16* al = lo ? ah + T * K : nullptr;
     const bool perm = W.kind == 1;
@@ -942,6 +943,22 @@ hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias
         gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
     }
     return hipGetLastError();
+}
+
+// launch_gemmh_chunk over row chunks whose operands fit the workspace
+// (one chunk up to 1024 rows at K = 18944): the operand area is reserved
+// with the workspace, so no call allocates.  Chunks are stream-ordered, so
+// each reuses the area after the previous chunk's GEMM has read it.
+hipError_t launch_gemmh(const float* x_f32, const QView& W, const uint16_t* bias, int64_t T, float* y,
+                        Workspace* ws, hipStream_t stream) {
+    const int64_t cap = gemm_operand_rows(ws, W.cols);
+    if (cap < 128) return hipErrorInvalidValue;
+    for (int64_t t0 = 0; t0 < T; t0 += cap) {
+        const int64_t tc = T - t0 < cap ? T - t0 : cap;
+        const hipError_t e = launch_gemmh_chunk(x_f32 + t0 * W.cols, W, bias, tc, y + t0 * W.rows, ws, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace

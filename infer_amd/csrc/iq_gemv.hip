@@ -58,6 +58,7 @@
 #include <cstdlib>
 
 #include "iq_limbs.h"
+#include "iq_plan.h"
 
 namespace iq {
 
@@ -1974,7 +1975,8 @@ bool gemvq_rows_preferred(int64_t M, int tiles, int64_t K, int n) {
 }
 
 // gemvq on n matrices, M in 7..32, straight from x (false: M out of range;
-// partial sums beyond the workspace are avoided by looping over K ranges).
+// partial sums beyond the workspace are avoided by looping over K ranges,
+// gemvq_plan in iq_plan.h).
 bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                   Workspace* ws, hipStream_t stream, hipError_t* err) {
     const int64_t K = W[0].cols, G = W[0].groups;
@@ -1985,32 +1987,9 @@ bool launch_gemvq(const float* x, const QView* W, const uint16_t* const* bias, f
         tiles += int((W[i].rows + 15) / 16);
         t32 += int((W[i].rows + 31) / 32);
     }
-    const int nrb = (t32 + 7) / 8;
-    if (M < 7 || M > 32) return false;
-    // ranges of at most ngr groups (the weights of a range are held in
-    // registers: 64 per lane at one row block; the operands of 2 blocks x 4
-    // groups fill 64 KiB of LDS), and enough workgroups for two per CU
-    const int mb = M <= 16 ? 1 : 2;
-    const int ngr = mb == 2 ? 4 : (W[0].kind == 1 ? 6 : 4);
-    const int want = 2 * device_cu_count();
-    int S = int((G + ngr - 1) / ngr);
-    S = std::max<int>(S, std::min<int>((want + nrb - 1) / nrb, int(G)));
-    int gs = int((G + S - 1) / S);
-    S = int((G + gs - 1) / gs);
-    // partial sums beyond the workspace: fewer workgroups along K, each
-    // taking L consecutive ranges (one per workgroup at L = 1)
-    int L = 1;
-    int ngl = ngr;  // ranges of the looped instance
-    if (S > 1 && int64_t(S) * M * tiles * 16 > ws->part_floats) {
-        // (int8 at two row blocks loops over 2-group ranges: 110 VGPRs,
-        // two workgroups per CU, against 150 with 4)
-        if (W[0].kind == 0 && mb == 2) ngl = 2;
-        const int R = int((G + ngl - 1) / ngl);
-        gs = int((G + R - 1) / R);
-        const int64_t fit = ws->part_floats / (int64_t(M) * tiles * 16);
-        L = int((R + fit - 1) / std::max<int64_t>(fit, 1));
-        S = (R + L - 1) / L;
-    }
+    const GqPlan pl = gemvq_plan(G, M, tiles, t32, W[0].kind, device_cu_count(), ws->part_floats);
+    if (!pl.ok) return false;
+    const int S = pl.S, L = pl.L, gs = pl.gs, nrb = pl.nrb, mb = pl.mb;
     p.nmat = n;
     p.K = K;
     p.G = G;

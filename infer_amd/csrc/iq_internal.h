@@ -32,11 +32,10 @@ struct Workspace {
     float* partials = nullptr; // part_floats (>= kPartialFloats)
     int64_t part_floats = 0;   // capacity of partials
     size_t xq_bytes = 0, xmeta_bytes = 0;
-    // the prefill GEMM's prepared activations when they exceed xq (grown on
-    // demand; null in the static workspace)
+    // the prefill GEMM's prepared activations (kGemmOperandBytes, reserved
+    // with the workspace; null in the static workspace)
     void* gx = nullptr;
     size_t gx_bytes = 0;
-    bool can_grow = true;
     // Shape of the activations last prepared into xq/xmeta (host-side record).
     int prep_M = 0;
     int64_t prep_K = 0;
@@ -57,6 +56,10 @@ constexpr int kMaxRowsGemv = 32;            // GpuBatch::kMaxRows (kernels/batch
 constexpr int64_t kMaxKp = 131072;          // padded K limit of the GEMV
 constexpr int64_t kPartialFloats = int64_t(4) << 20;  // 16 MiB of split-K partials (every workspace)
 constexpr int64_t kStreamPartialFloats = int64_t(16) << 20;  // 64 MiB in a per-stream workspace
+// The fp32-activation prefill GEMM's prepared operands (fp16 hi + lo, 4 B
+// per value): 1024 rows of 7B down's 18944 columns in one pass, longer
+// prefills in row chunks (at the 131072-column limit, 128 rows a chunk).
+constexpr size_t kGemmOperandBytes = size_t(80) << 20;
 
 // Returns the workspace of (current device, stream), allocating it on first
 // use.  Every stream has its own, so calls on different streams never share
@@ -94,12 +97,12 @@ bool launch_gemm_rows(const float* x, const QView& W, const uint16_t* bias, int6
                       hipStream_t stream, hipError_t* err);
 hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& W,
                        const uint16_t* bias, int64_t T, float* y, Workspace* ws, hipStream_t stream);
-// Room for the prefill GEMM's prepared activations: T x K fp16 (x 2 with
-// lo) and T row factors.  Reuses xq / xmeta when they are large enough
-// (the preparation of iq_gemv_prep is then forgotten), else a buffer the
-// workspace grows (not while the stream is being captured).
-hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs,
-                         hipStream_t stream);
+// The prefill GEMM's prepared activations for T rows of K columns: fp16
+// hi (and lo) [T][K] and T row factors, in the workspace's operand area
+// (hipErrorInvalidValue when they do not fit: callers split T into chunks
+// of at most gemm_operand_rows(ws, K) rows, a multiple of 128).
+hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs);
+int64_t gemm_operand_rows(const Workspace* ws, int64_t K);
 
 // A validated stage program on the device (iq_chain.hip).
 struct Chain;

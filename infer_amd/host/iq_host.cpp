@@ -582,9 +582,20 @@ void QuantFile::open(const std::string& path) {
         QTensor t;
         t.kind = kind_of_dtype(e.at("dtype").as_str(), name);
         const JVal& shape = e.at("shape");
-        if (shape.type != JVal::kArr || shape.arr.empty()) throw bad(name + ": shape must be a non-empty array");
+        // the reference's writer emits [n] (bf16 vectors) or [rows, cols];
+        // every dimension positive, the element count checked against
+        // overflow before any payload size is derived from it
+        if (shape.type != JVal::kArr || shape.arr.empty() || shape.arr.size() > 2)
+            throw bad(name + ": shape must be [n] or [rows, cols]");
+        if (t.kind != QKind::kBf16 && shape.arr.size() != 2) throw bad(name + ": a quantised tensor needs [rows, cols]");
+        constexpr int64_t kMaxDim = int64_t(1) << 40;
         int64_t count = 1;
-        for (const JVal& d : shape.arr) count *= d.as_int();
+        for (const JVal& d : shape.arr) {
+            const int64_t v = d.as_int();
+            if (v <= 0 || v > kMaxDim) throw bad(name + ": shape dimension out of range");
+            if (count > (int64_t(1) << 62) / v) throw bad(name + ": shape too large");
+            count *= v;
+        }
         t.rows = shape.arr[0].as_int();
         t.cols = shape.arr.size() > 1 ? shape.arr[1].as_int() : 1;
         if (t.kind == QKind::kBf16) {

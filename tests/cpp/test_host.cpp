@@ -183,6 +183,17 @@ int cmd_errors(const std::string& dir) {
     CHECK(throws(p), "int4 without zeros accepted");
     put(with_header("{\"m\":{\"data\":[0,64],\"dtype\":\"int8\",\"group\":128,\"scales\":[64,66],\"shape\":[1,64]", 66));
     CHECK(throws(p), "truncated JSON accepted");
+    put(with_header("{\"m\":{\"data\":[0,64],\"dtype\":\"int8\",\"group\":128,\"scales\":[64,66],\"shape\":[-1,-64]}}", 66));
+    CHECK(throws(p), "negative dimensions accepted");
+    put(with_header("{\"m\":{\"data\":[0,0],\"dtype\":\"bf16\",\"shape\":[0]}}", 0));
+    CHECK(throws(p), "zero dimension accepted");
+    put(with_header("{\"m\":{\"data\":[0,64],\"dtype\":\"int8\",\"group\":128,\"scales\":[64,66],\"shape\":[1,64,1]}}", 66));
+    CHECK(throws(p), "three dimensions accepted");
+    put(with_header("{\"m\":{\"data\":[0,64],\"dtype\":\"int8\",\"group\":128,\"scales\":[64,66],\"shape\":[64]}}", 66));
+    CHECK(throws(p), "one-dimensional quantised tensor accepted");
+    // 2^32 x 2^32 elements: the count wraps to 0 in 64-bit arithmetic
+    put(with_header("{\"m\":{\"data\":[0,0],\"dtype\":\"bf16\",\"shape\":[4294967296,4294967296]}}", 0));
+    CHECK(throws(p), "overflowing shape accepted");
     put(with_header("{\"m\":{\"data\":[0,64],\"dtype\":\"int8\",\"group\":128,\"scales\":[64,66],\"shape\":[1,64]}}", 66));
     CHECK(!throws(p), "valid minimal container rejected");
     llm::QuantModel m;

@@ -11,7 +11,8 @@ seeded sample of output features, with every row of the activation block.
 Routes covered (dispatch in infer_amd/csrc/iq_gemm.hip / iq_gemv.hip):
   * prefill GEMM at T = 1024 on 18944 x 3584: 8 row tiles x 148 column
     tiles >= 2 x CUs, i.e. the 128 x 128 tile instance (NJ = 2, BM = 128),
-    bf16 and fp32 activations, int8 and int4;
+    and on 3584 x 18944 (config 5's down, K = 18944), bf16 and fp32
+    activations, int8 and int4;
   * gate|up (2 x 18944 x 3584) in one iq_gemv_multi call at 9, 12 and 16
     rows (int4 on gemvq: 32-row tiles on the 32 x 32 matrix instruction,
     both terms of all 16 rows in one operand; int8 on gemvr) and at 1 row;
@@ -111,6 +112,28 @@ def test_prefill_gemm_t1024_wide(kind, xtype):
         ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
     torch.cuda.synchronize()
     check_sampled(y, x, W, T, rng, f"gemm T=1024 {xtype} kind={kind}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("xtype", ["bf16", "fp32"])
+def test_prefill_gemm_t1024_down(kind, xtype):
+    """Config 5's down shape at its own size: X[1024, 18944] times the
+    3584 x 18944 matrix (148 groups per row), the instance the benchmark's
+    down figure is measured on."""
+    rng = np.random.default_rng(2048 + kind + (10 if xtype == "fp32" else 0))
+    T, N, K = 1024, 3584, 18944
+    W = Packed(rng, N, K, kind)
+    y = out_buffer(T, N)
+    say("gemm T=1024 down", kind, xtype)
+    if xtype == "bf16":
+        xb = O.seeded_bf16(rng, (T, K), 1.0)
+        x = O.bf16_to_f32(xb)
+        ops.launch_gemm_bf16x(torch.from_numpy(xb.view(np.int16)).cuda(), W.view, None, T, K, N, y)
+    else:
+        x = rng.standard_normal((T, K), dtype=np.float32)
+        ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x, W, T, rng, f"gemm T=1024 down {xtype} kind={kind}")
 
 
 @pytest.mark.parametrize("kind", [0, 1])

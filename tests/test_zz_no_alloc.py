@@ -43,3 +43,29 @@ def test_noalloc_rejects_oversize():
         ops.gemv_noalloc(x, W.view, None, 1, 32896, 16, y)
     torch.cuda.synchronize()
     assert torch.all(y == CANARY)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [28, 32])
+def test_noalloc_lm_head_wide_rows(kind, M):
+    """The 7B lm_head (152064 x 3584) at 28..32 rows through the static
+    scratch: the widest call whose K-range partial sums cannot fit the
+    scratch (the plan then keeps every range in one workgroup per row
+    block), checked against the oracle on sampled rows, then a smaller
+    call on the same scratch."""
+    from tests.test_gpu_routes import Packed, check_sampled
+    rng = np.random.default_rng(152064 + 2 * M + kind)
+    N, K = 152064, 3584
+    W = Packed(rng, N, K, kind)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    y = out_buffer(M, N)
+    say("noalloc lm_head", kind, M)
+    ops.gemv_noalloc(torch.from_numpy(x).cuda(), W.view, None, M, K, N, y)
+    torch.cuda.synchronize()
+    check_sampled(y, x, W, M, rng, f"noalloc lm_head kind={kind} M={M}")
+    W2 = Packed(rng, 1536, K, kind)
+    x2 = rng.standard_normal((9, K), dtype=np.float32)
+    y2 = out_buffer(9, 1536)
+    ops.gemv_noalloc(torch.from_numpy(x2).cuda(), W2.view, None, 9, K, 1536, y2)
+    torch.cuda.synchronize()
+    check_sampled(y2, x2, W2, 9, rng, f"noalloc 1536x3584 kind={kind} M=9")
