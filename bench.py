@@ -400,7 +400,7 @@ def bench_gemv_single(torch, ops, kind, N, K, M, copies, reps=200, seed=11):
     return per_ms * 1e3, nb / (per_ms * 1e-3) / 1e9
 
 
-def bench_decode_chain(torch, ops, model, steps, warmup):
+def bench_decode_chain(torch, ops, model, steps, warmup, rows=1):
     """The quantised decode step as the reference's engine chains it
     (kernels/batch_gpu.cu:186-215), one token at position 0: embedding
     gather, then per layer RMSNorm -> q|k|v, single-key attention -> o +
@@ -422,8 +422,8 @@ def bench_decode_chain(torch, ops, model, steps, warmup):
         d["q_b"], d["k_b"], d["v_b"] = nb(NH7 * 128), nb(KV7 * 128), nb(KV7 * 128)
         layers.append(d)
     spec = dict(cfg=cfg, layers=layers, embed=model.head, head=model.head, final_norm=nb(H7))
-    step = C.DecodeStep(spec)
-    step.step(1234)
+    step = C.DecodeStep(spec, rows=rows)
+    step.step([1234 + 7 * b for b in range(rows)])
     torch.cuda.synchronize()
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr, stream=capture_stream(torch)):
@@ -432,12 +432,15 @@ def bench_decode_chain(torch, ops, model, steps, warmup):
     wb = step.weight_bytes()
     out = {"us_per_step": round(ms * 1e3, 1), "GBps": round(wb / (ms * 1e-3) / 1e9, 1),
            "frac_hbm_peak": round(wb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-           "launches": len(step.chain.stages) + 1, "weight_bytes": int(wb),
+           "rows": rows,
+           "launches": (len(step.chain.stages) if rows == 1 else 2 * len(step.chain.stages)) + 1,
+           "weight_bytes": int(wb),
            # the quantised linears of one decode step per second (attention
            # over a KV cache, sampling and the host are not in it; the
            # reference's 7B int4 end to end: 126 tok/s on an RTX 5070 Ti,
            # README.md:57)
            "steps_per_s_linears_only": round(1e3 / ms, 1),
+           "tokens_per_s_linears_only": round(rows * 1e3 / ms, 1),
            "logits_finite": bool(torch.isfinite(step.logits).all().item())}
     del gr, step
     return out
@@ -595,6 +598,12 @@ def main():
             del gm, stm
         detail["7b_int4_rows_sweep"] = sweep
         detail["7b_int4_decode_chain_m1"] = bench_decode_chain(torch, ops, m4, args.steps, args.warmup)
+        # the chained step at B sequences (B-row stages), beside the bare
+        # linear set at the same widths
+        for B in (4, 16, 32):
+            dc = bench_decode_chain(torch, ops, m4, args.steps, args.warmup, rows=B)
+            dc["ratio_vs_chain_m1"] = round(dc["us_per_step"] / detail["7b_int4_decode_chain_m1"]["us_per_step"], 3)
+            detail[f"7b_int4_decode_chain_m{B}"] = dc
         cpu_gbs, cpu_sample = cpu_baseline(torch, m4, args.cpu_seconds)
         cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": "oracle iqo_linear_q_f32 (src/forward.cpp:35-47 over dequant(), scalar fp32, "

@@ -154,18 +154,23 @@ int iq_quantize(const uint16_t* w_bf16, int64_t rows, int64_t cols, int kind, ui
                 uint16_t* scales, uint8_t* zeros, void* stream);
 
 /* ---------------------------------------------------------------- chains
- * A chain is a program of dependent 1-row GEMV stages: the quantised
- * linears of a decode step in the order of GpuBatch::Impl::launch_sequence
- * (kernels/batch_gpu.cu:186-215), each stage reading what earlier stages
- * wrote, with the elementwise work between them fused into the stages.
- * A run is one launch per stage on one stream (capturable into a HIP
- * graph).  No reference counterpart as an entry point: the reference
+ * A chain is a program of dependent GEMV stages of 1..32 activation rows:
+ * the quantised linears of a (batched) decode step in the order of
+ * GpuBatch::Impl::launch_sequence (kernels/batch_gpu.cu:186-215), each
+ * stage reading what earlier stages wrote, with the elementwise work
+ * between them fused into the stages.  A run is one launch per 1-row stage
+ * and two per B-row stage (the GEMV with the input transform, then the
+ * K-range sums with the output transform), on one stream, capturable into
+ * a HIP graph.  No reference counterpart as an entry point: the reference
  * issues launch_gemv_batched_q, launch_rmsnorm, launch_swiglu and
  * launch_residual_add separately.
  *
  * Stage = y_i = f_out( dequant(W_i) . f_in(x) + bias_i ), i < n <= 3, all W_i
- * of one kind and width K (K % 256 == 0; int4 K <= 24576, int8 K <= 20480,
- * halved for IQ_OUT_SWIGLU), x 16-byte aligned:
+ * of one kind and width K (K % 256 == 0; 1 row: int4 K <= 24576, int8
+ * K <= 20480, halved for IQ_OUT_SWIGLU), x 16-byte aligned, for each of
+ * the stage's `rows` activation rows B (1..32; 0 means 1): x is [B][K]
+ * ([B][K / group] for IQ_IN_GQA), residual and every y_i [B][W_i->rows],
+ * row-major, each row transformed on its own (RMSNorm per row):
  *   f_in   IQ_IN_PLAIN    x[k]
  *          IQ_IN_RMSNORM  x[k] / sqrt(mean(x^2) + eps) * norm[k], norm bf16
  *                         (src/forward.cpp:21-31); K <= 16384
@@ -193,6 +198,7 @@ typedef struct iq_stage {
     iq_view W[3];
     const uint16_t* bias[3];          /* bf16 or NULL */
     float* y[3];                      /* IQ_OUT_SWIGLU: y[0] only */
+    int32_t rows;                     /* activation rows B, 1..32 (0: 1) */
 } iq_stage;
 
 typedef struct iq_chain iq_chain;

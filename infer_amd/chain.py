@@ -2,9 +2,10 @@
 the decode step built from them.
 
 DecodeStep is the quantised part of the reference's decode step,
-GpuBatch::Impl::launch_sequence (kernels/batch_gpu.cu:186-215), for one
-sequence of one token (position 0): the quantised embedding gather
-(launch_embedding_q), then per layer
+GpuBatch::Impl::launch_sequence (kernels/batch_gpu.cu:186-215), for B
+sequences (B = 1..32, GpuBatch::kMaxRows, kernels/batch_gpu.h:80) of one
+token each at position 0: the quantised embedding gather of the B tokens
+(launch_embedding_q), then per layer, for each of the B rows
 
     q|k|v  = rmsnorm(h, input_ln) . W_qkv^T + b_qkv          (one stage)
     h'     = h + attn . W_o^T                                  (one stage)
@@ -43,8 +44,9 @@ class Stage:
     """One stage: y_i = out_op(dequant(Ws[i]) . in_op(x) + biases[i])."""
 
     def __init__(self, Ws, x, ys, in_op=IN_PLAIN, out_op=OUT_STORE, biases=None, norm=None, eps=0.0,
-                 residual=None, gqa=(0, 0)):
+                 residual=None, gqa=(0, 0), rows=1):
         self.Ws, self.x, self.ys = list(Ws), x, list(ys)
+        self.rows = rows
         self.in_op, self.out_op = in_op, out_op
         self.biases = list(biases) if biases is not None else [None] * len(self.Ws)
         self.norm, self.eps, self.residual, self.gqa = norm, eps, residual, gqa
@@ -54,6 +56,7 @@ class Stage:
         s.in_op, s.out_op, s.n = self.in_op, self.out_op, len(self.Ws)
         s.gqa_head_dim, s.gqa_group = self.gqa
         s.eps = self.eps
+        s.rows = self.rows
         s.x, s.norm, s.residual = _p(self.x), _p(self.norm), _p(self.residual)
         for i, W in enumerate(self.Ws):
             s.W[i] = W._c
@@ -108,21 +111,23 @@ class DecodeStep:
     docstring).  `model` has: cfg dict (hidden, inter, heads, kv_heads,
     head_dim, vocab, layers, eps), embed / head (QuantView), final_norm
     (bf16 int16 tensor), layers: list of dicts with QuantViews q, k, v, o,
-    gate, up, down, bf16 tensors input_ln, post_ln and optional q_b, k_b, v_b."""
+    gate, up, down, bf16 tensors input_ln, post_ln and optional q_b, k_b, v_b.
+    rows: B sequences; every vector below is [B][n] row-major."""
 
-    def __init__(self, model, device="cuda"):
+    def __init__(self, model, device="cuda", rows=1):
         c = model["cfg"]
         H, I, V = c["hidden"], c["inter"], c["vocab"]
         nh, nkv, hd, L = c["heads"], c["kv_heads"], c["head_dim"], c["layers"]
         qo, kvo = nh * hd, nkv * hd
+        B = self.rows = int(rows)
         sizes = [H]
         for _ in range(L):
             sizes += [qo, kvo, kvo, H, I, H]
         sizes += [V]
-        self.arena = Arena(sizes, device)
+        self.arena = Arena([B * n for n in sizes], device)
         vs = iter(self.arena.views)
         self.h0 = next(vs)
-        self.ids = torch.zeros(1, dtype=torch.int64, device=device)
+        self.ids = torch.zeros(B, dtype=torch.int64, device=device)
         self.model = model
         self.per_layer = []
         stages = []
@@ -132,30 +137,34 @@ class DecodeStep:
             q, k, v, h1, act, h2 = (next(vs) for _ in range(6))
             stages.append(Stage([Lw["q"], Lw["k"], Lw["v"]], h, [q, k, v], IN_RMSNORM, OUT_STORE,
                                 biases=[Lw.get("q_b"), Lw.get("k_b"), Lw.get("v_b")], norm=Lw["input_ln"],
-                                eps=c["eps"]))
-            stages.append(Stage([Lw["o"]], v, [h1], IN_GQA, OUT_RESIDUAL, residual=h, gqa=(hd, nh // nkv)))
+                                eps=c["eps"], rows=B))
+            stages.append(Stage([Lw["o"]], v, [h1], IN_GQA, OUT_RESIDUAL, residual=h, gqa=(hd, nh // nkv), rows=B))
             stages.append(Stage([Lw["gate"], Lw["up"]], h1, [act], IN_RMSNORM, OUT_SWIGLU, norm=Lw["post_ln"],
-                                eps=c["eps"]))
-            stages.append(Stage([Lw["down"]], act, [h2], IN_PLAIN, OUT_RESIDUAL, residual=h1))
+                                eps=c["eps"], rows=B))
+            stages.append(Stage([Lw["down"]], act, [h2], IN_PLAIN, OUT_RESIDUAL, residual=h1, rows=B))
             self.per_layer.append(dict(h=h, q=q, k=k, v=v, h1=h1, act=act, h2=h2))
             h = h2
         self.logits = next(vs)
         stages.append(Stage([model["head"]], h, [self.logits], IN_RMSNORM, OUT_STORE, norm=model["final_norm"],
-                            eps=c["eps"]))
+                            eps=c["eps"], rows=B))
         self.h_last = h
         self.chain = Chain(stages)
 
     def step(self, token_id=None, stream=None):
-        """Embedding gather of `token_id` (or of the id already in self.ids),
+        """Embedding gather of the B token ids `token_id` (an int for every
+        row, or a sequence of B ints; None: the ids already in self.ids),
         then the chain.  Asynchronous on the stream."""
         if token_id is not None:
-            self.ids.fill_(int(token_id))
+            if isinstance(token_id, int):
+                self.ids.fill_(int(token_id))
+            else:
+                self.ids.copy_(torch.tensor([int(t) for t in token_id], dtype=torch.int64))
         H = self.model["cfg"]["hidden"]
-        ops.launch_embedding_q(self.model["embed"], self.ids, 1, H, self.h0, stream)
+        ops.launch_embedding_q(self.model["embed"], self.ids, self.rows, H, self.h0, stream)
         self.chain.run(stream)
 
     def weight_bytes(self):
-        n = self.model["embed"].nbytes() // self.model["embed"].rows  # one gathered row
+        n = self.rows * (self.model["embed"].nbytes() // self.model["embed"].rows)  # the gathered rows
         for Lw in self.model["layers"]:
             n += sum(Lw[k].nbytes() for k in ("q", "k", "v", "o", "gate", "up", "down"))
         return n + self.model["head"].nbytes()

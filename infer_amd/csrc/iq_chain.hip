@@ -88,12 +88,41 @@ struct CStage {
     float* ssq_out;
 };
 
+// Output side of a B-row stage (epi_kernel): the K-range sums of the rows
+// GEMV, bias, then store / residual add / SwiGLU, and (when a later
+// RMSNorm stage reads the output) the sums of squares of each row's
+// 256-column blocks.
+struct CEpi {
+    float* y[kMaxStageMats];
+    const uint16_t* bias[kMaxStageMats];
+    int32_t N[kMaxStageMats];
+    int32_t tile0[kMaxStageMats];
+    int32_t nmat;
+    const float* part;
+    int32_t S, M;
+    int64_t ld;        // partial-sum row length: 16 x tiles of all matrices
+    int32_t swiglu;
+    const float* res;
+    float* ssq_out;    // [M][ssq_n] or null
+    int32_t ssq_n;
+    int32_t ncols;     // columns of the grid: N_0 (SwiGLU) or ld
+};
+
 // Host record of a stage: the kernel argument and its launch shape.
 struct HostStage {
     CStage st;
     int kind;
     int ng;  // slice capacity of the kernel instance
     size_t lds;
+    // B-row stages (rows > 1)
+    int rows = 1;
+    QView W[kMaxStageMats];
+    RowsIn in{};
+    CEpi epi{};
+    // RMSNorm input no earlier stage of the chain produces: its sums of
+    // squares come from ssq_kernel before the GEMV
+    bool own_ssq = false;
+    float* ssq = nullptr;  // [rows][ssq_n] (own or the producer's)
 };
 
 __device__ __forceinline__ CMat stage_mat(const CStage& st, int m) {
@@ -412,6 +441,79 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     }
 }
 
+// Sum over the 256 threads of a block, in a fixed order (shuffle tree per
+// wave, then the four wave sums in order); the result in thread 0.
+__device__ __forceinline__ float block256_sum(float v, float* red4) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red4[0] + red4[1]) + red4[2]) + red4[3];
+}
+
+// Output side of a B-row stage: thread (column c, row m = blockIdx.y).
+__global__ __launch_bounds__(256) void epi_kernel(const CEpi e) {
+    __shared__ float red4[4];
+    const int m = blockIdx.y;
+    const int c = int(blockIdx.x) * 256 + int(threadIdx.x);
+    const int64_t stride = int64_t(e.M) * e.ld, base = int64_t(m) * e.ld;
+    float v = 0.0f;
+    bool valid = false;
+    if (c < e.ncols) {
+        if (e.swiglu) {
+            // silu(g) * u  (kernels/ops/elementwise.cu:6-11)
+            const float g = sum_slices(e.part, e.S, stride, base + c) + (e.bias[0] ? bf16_to_f32(e.bias[0][c]) : 0.0f);
+            const float u = sum_slices(e.part, e.S, stride, base + int64_t(e.tile0[1]) * 16 + c) +
+                            (e.bias[1] ? bf16_to_f32(e.bias[1][c]) : 0.0f);
+            v = g / (1.0f + expf(-g)) * u;
+            e.y[0][int64_t(m) * e.N[0] + c] = v;
+            valid = true;
+        } else {
+            int i = 0;
+            for (int k = 1; k < e.nmat; k++)
+                if (c >= e.tile0[k] * 16) i = k;
+            const int col = c - e.tile0[i] * 16;
+            if (col < e.N[i]) {
+                v = sum_slices(e.part, e.S, stride, base + c) + (e.bias[i] ? bf16_to_f32(e.bias[i][col]) : 0.0f);
+                if (e.res) v = e.res[int64_t(m) * e.N[0] + col] + v;
+                e.y[i][int64_t(m) * e.N[i] + col] = v;
+                valid = true;
+            }
+        }
+    }
+    if (e.ssq_out) {
+        const float sq = block256_sum(valid ? v * v : 0.0f, red4);
+        if (threadIdx.x == 0) e.ssq_out[int64_t(m) * e.ssq_n + blockIdx.x] = sq;
+    }
+}
+
+// Sums of squares of the 256-column blocks of each row of x [M][K] (row
+// stride K), for an RMSNorm input that no earlier stage produced.
+__global__ __launch_bounds__(256) void ssq_kernel(const float* __restrict__ x, int K, int ssq_n,
+                                                  float* __restrict__ ssq) {
+    __shared__ float red4[4];
+    const int m = blockIdx.y;
+    const int c = int(blockIdx.x) * 256 + int(threadIdx.x);
+    const float v = c < K ? x[int64_t(m) * K + c] : 0.0f;
+    const float sq = block256_sum(v * v, red4);
+    if (threadIdx.x == 0) ssq[int64_t(m) * ssq_n + blockIdx.x] = sq;
+}
+
+hipError_t run_rows_stage(const HostStage& h, float* part, int64_t part_floats, hipStream_t stream) {
+    if (h.own_ssq) {
+        const int K = int(h.W[0].cols);
+        ssq_kernel<<<dim3(unsigned(h.in.ssq_n), unsigned(h.rows)), 256, 0, stream>>>(h.in.x, K, h.in.ssq_n, h.ssq);
+    }
+    int S = 0;
+    hipError_t e = launch_chain_rows(h.W, h.st.nmat, h.rows, h.in, part, part_floats, &S, stream);
+    if (e != hipSuccess) return e;
+    CEpi ep = h.epi;
+    ep.part = part;
+    ep.S = S;
+    epi_kernel<<<dim3(unsigned((ep.ncols + 255) / 256), unsigned(h.rows)), 256, 0, stream>>>(ep);
+    return hipGetLastError();
+}
+
 template <int KIND>
 hipError_t launch_stage_k(const HostStage& h, hipStream_t stream) {
     const dim3 grid(unsigned(h.st.units)), block(unsigned(64 * h.st.ks));
@@ -457,6 +559,11 @@ struct Chain {
     int device = 0;
     std::vector<HostStage> stages;
     float* partials = nullptr;  // per-tile sums of squares passed between stages
+    // B-row stages: K-range sums (one buffer, the stages run in order) and
+    // the per-row block sums of squares
+    float* rpart = nullptr;
+    int64_t rpart_floats = 0;
+    float* rssq = nullptr;
 };
 
 int chain_create(const iq_stage* stages, int n, Chain** out) {
@@ -470,6 +577,9 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         CStage& c = hs.st;
         std::memset(&c, 0, sizeof(c));
         if (a.n < 1 || a.n > kMaxStageMats) return IQ_ESHAPE;
+        const int rows = a.rows == 0 ? 1 : a.rows;
+        if (rows < 1 || rows > kMaxRowsGemv) return IQ_ESHAPE;
+        hs.rows = rows;
         if (a.in_op < IQ_IN_PLAIN || a.in_op > IQ_IN_GQA) return IQ_ESHAPE;
         if (a.out_op < IQ_OUT_STORE || a.out_op > IQ_OUT_SWIGLU) return IQ_ESHAPE;
         const iq_view& W0 = a.W[0];
@@ -496,7 +606,8 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         const int nout = pair ? 1 : a.n;
         for (int i = 0; i < nout; i++) {
             if (!a.y[i]) return IQ_ENULL;
-            writes.push_back({reinterpret_cast<uintptr_t>(a.y[i]), reinterpret_cast<uintptr_t>(a.y[i] + a.W[i].rows)});
+            writes.push_back({reinterpret_cast<uintptr_t>(a.y[i]),
+                              reinterpret_cast<uintptr_t>(a.y[i] + int64_t(rows) * a.W[i].rows)});
         }
         if (!a.x) return IQ_ENULL;
         if (reinterpret_cast<uintptr_t>(a.x) % 16) return IQ_ESHAPE;
@@ -508,7 +619,7 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
             c.gqa_span = int32_t(hd * grp);
             xlen = K / grp;
         }
-        reads.push_back({reinterpret_cast<uintptr_t>(a.x), reinterpret_cast<uintptr_t>(a.x + xlen)});
+        reads.push_back({reinterpret_cast<uintptr_t>(a.x), reinterpret_cast<uintptr_t>(a.x + int64_t(rows) * xlen)});
         if (a.in_op == IQ_IN_RMSNORM) {
             if (!a.norm) return IQ_ENULL;
             if (reinterpret_cast<uintptr_t>(a.norm) % 16) return IQ_ESHAPE;
@@ -518,7 +629,7 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         if (a.out_op == IQ_OUT_RESIDUAL) {
             if (!a.residual) return IQ_ENULL;
             reads.push_back({reinterpret_cast<uintptr_t>(a.residual),
-                             reinterpret_cast<uintptr_t>(a.residual + W0.rows)});
+                             reinterpret_cast<uintptr_t>(a.residual + int64_t(rows) * W0.rows)});
         }
         // a stage's workgroups read its inputs while others store: no output
         // may overlap an input or another output of the same stage
@@ -539,6 +650,37 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         c.G = int32_t(G);
         c.tpu = pair ? 2 : 1;
         c.units = pair ? int((W0.rows + 15) / 16) : tiles;
+        hs.kind = W0.kind;
+        if (rows > 1) {
+            // B rows: the rows GEMV (gemvr / gemvq with the input transform)
+            // and epi_kernel
+            for (int i = 0; i < a.n; i++) {
+                const iq_view& Wi = a.W[i];
+                hs.W[i] = QView{Wi.kind, Wi.rows, Wi.cols, Wi.groups, Wi.q, Wi.scales,
+                                Wi.kind == IQ_INT4 ? Wi.zeros : nullptr};
+            }
+            if (chain_rows_partials(hs.W, a.n, rows, kStreamPartialFloats) < 0) return IQ_ETOOLARGE;
+            hs.in.x = a.x;
+            hs.in.xstride = xlen;
+            hs.in.gqa_hd = a.in_op == IQ_IN_GQA ? a.gqa_head_dim : 0;
+            hs.in.gqa_span = a.in_op == IQ_IN_GQA ? a.gqa_head_dim * a.gqa_group : 0;
+            hs.in.norm = a.in_op == IQ_IN_RMSNORM ? a.norm : nullptr;
+            hs.in.eps = a.eps;
+            CEpi& ep = hs.epi;
+            for (int i = 0; i < a.n; i++) {
+                ep.y[i] = a.y[i];
+                ep.bias[i] = a.bias[i];
+                ep.N[i] = int32_t(a.W[i].rows);
+                ep.tile0[i] = c.mat[i].tile0;
+            }
+            ep.nmat = a.n;
+            ep.M = rows;
+            ep.ld = int64_t(tiles) * 16;
+            ep.swiglu = pair ? 1 : 0;
+            ep.res = a.out_op == IQ_OUT_RESIDUAL ? a.residual : nullptr;
+            ep.ncols = pair ? int32_t(W0.rows) : int32_t(ep.ld);
+            continue;
+        }
         // slices of whole 4-group blocks (measured: fewer, fatter waves beat
         // more waves with 2 groups each), at most 16 waves of <= 12 groups
         // (int4) or 8 waves of <= 20 groups (int8: twice the weight
@@ -550,7 +692,6 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         if (gs > (pair ? 8 : (i4 ? 12 : 20))) return IQ_ETOOLARGE;
         c.gs = gs;
         c.ks = int((G + gs - 1) / gs);
-        hs.kind = W0.kind;
         hs.ng = gs;
         // RMSNorm from the whole input: at most four 16-byte chunks per thread
         if (a.in_op == IQ_IN_RMSNORM && K > 16 * 64 * int64_t(c.ks)) return IQ_ETOOLARGE;
@@ -563,18 +704,23 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
     // also writes per-tile sums of squares, so the consumer's workgroups
     // need not read the whole vector (unless a stage in between rewrites it)
     std::vector<std::pair<int, int>> links;  // (producer, consumer)
+    auto rows_of = [&](int i) { return stages[i].rows == 0 ? 1 : stages[i].rows; };
     for (int s = 0; s < n; s++) {
         if (stages[s].in_op != IQ_IN_RMSNORM) continue;
         const float* x = stages[s].x;
         const int64_t K = stages[s].W[0].cols;
+        const int B = rows_of(s);
         for (int e = s - 1; e >= 0; e--) {
             const iq_stage& a = stages[e];
             const int nout = a.out_op == IQ_OUT_SWIGLU ? 1 : a.n;
+            const int Be = rows_of(e);
             bool hit = false, clash = false;
             for (int i = 0; i < nout; i++) {
-                const Range w{reinterpret_cast<uintptr_t>(a.y[i]), reinterpret_cast<uintptr_t>(a.y[i] + a.W[i].rows)};
-                if (a.y[i] == x && a.W[i].rows == K && nout == 1 && K <= 4096) hit = true;
-                else if (overlaps(w, Range{reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(x + K)})) clash = true;
+                const Range w{reinterpret_cast<uintptr_t>(a.y[i]),
+                              reinterpret_cast<uintptr_t>(a.y[i] + int64_t(Be) * a.W[i].rows)};
+                if (a.y[i] == x && a.W[i].rows == K && nout == 1 && Be == B && (B > 1 || K <= 4096)) hit = true;
+                else if (overlaps(w, Range{reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(x + int64_t(B) * K)}))
+                    clash = true;
             }
             if (hit) links.emplace_back(e, s);
             if (hit || clash) break;
@@ -585,25 +731,77 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         delete ch;
         return IQ_EDEVICE;
     }
-    if (!links.empty()) {
-        // one partial-sum array per producer
+    auto fail = [&](hipError_t e) {
+        chain_destroy(ch);
+        return e == hipErrorOutOfMemory ? IQ_ENOMEM : int(e);
+    };
+    // 1 row: one per-tile partial-sum array per producer
+    {
         std::vector<size_t> off(static_cast<size_t>(n), size_t(-1));
         size_t total = 0;
         for (const auto& l : links)
-            if (off[size_t(l.first)] == size_t(-1)) {
+            if (rows_of(l.first) == 1 && off[size_t(l.first)] == size_t(-1)) {
                 off[size_t(l.first)] = total;
                 total += size_t((prog[size_t(l.first)].st.mat[0].N + 15) / 16 + 63) / 64 * 64;
             }
-        const hipError_t e = hipMalloc(reinterpret_cast<void**>(&ch->partials), total * sizeof(float));
-        if (e != hipSuccess) {
-            delete ch;
-            return e == hipErrorOutOfMemory ? IQ_ENOMEM : int(e);
+        if (total) {
+            const hipError_t e = hipMalloc(reinterpret_cast<void**>(&ch->partials), total * sizeof(float));
+            if (e != hipSuccess) return fail(e);
+            for (const auto& l : links) {
+                if (rows_of(l.first) != 1) continue;
+                float* p = ch->partials + off[size_t(l.first)];
+                prog[size_t(l.first)].st.ssq_out = p;
+                prog[size_t(l.second)].st.ssq_in = p;
+                prog[size_t(l.second)].st.ssq_n = (prog[size_t(l.first)].st.mat[0].N + 15) / 16;
+            }
         }
-        for (const auto& l : links) {
-            float* p = ch->partials + off[size_t(l.first)];
-            prog[size_t(l.first)].st.ssq_out = p;
-            prog[size_t(l.second)].st.ssq_in = p;
-            prog[size_t(l.second)].st.ssq_n = (prog[size_t(l.first)].st.mat[0].N + 15) / 16;
+    }
+    // B rows: per-row sums of squares of 256-column blocks, written by the
+    // producer's epi_kernel or by ssq_kernel (RMSNorm inputs no stage of
+    // the chain produces); one K-range partial-sum buffer for all stages
+    {
+        std::vector<size_t> off(static_cast<size_t>(n), size_t(-1));  // by producer / own consumer
+        std::vector<int> producer(static_cast<size_t>(n), -1);
+        for (const auto& l : links)
+            if (rows_of(l.second) > 1) producer[size_t(l.second)] = l.first;
+        size_t total = 0;
+        int64_t part = 0;
+        for (int s = 0; s < n; s++) {
+            HostStage& h = prog[size_t(s)];
+            if (h.rows == 1) continue;
+            part = std::max<int64_t>(part, chain_rows_partials(h.W, h.st.nmat, h.rows, kStreamPartialFloats));
+            if (stages[s].in_op != IQ_IN_RMSNORM) continue;
+            const int pe = producer[size_t(s)];
+            const int key = pe >= 0 ? pe : s;
+            const int64_t K = h.W[0].cols;
+            const int ssq_n = pe >= 0 ? int((prog[size_t(pe)].epi.ncols + 255) / 256) : int((K + 255) / 256);
+            if (off[size_t(key)] == size_t(-1)) {
+                off[size_t(key)] = total;
+                total += size_t(h.rows) * size_t(ssq_n);
+            }
+            h.in.ssq_n = ssq_n;
+            h.own_ssq = pe < 0;
+        }
+        if (total) {
+            const hipError_t e = hipMalloc(reinterpret_cast<void**>(&ch->rssq), total * sizeof(float));
+            if (e != hipSuccess) return fail(e);
+            for (int s = 0; s < n; s++) {
+                HostStage& h = prog[size_t(s)];
+                if (h.rows == 1 || stages[s].in_op != IQ_IN_RMSNORM) continue;
+                const int pe = producer[size_t(s)];
+                float* p = ch->rssq + off[size_t(pe >= 0 ? pe : s)];
+                h.ssq = p;
+                h.in.ssq = p;
+                if (pe >= 0) {
+                    prog[size_t(pe)].epi.ssq_out = p;
+                    prog[size_t(pe)].epi.ssq_n = h.in.ssq_n;
+                }
+            }
+        }
+        if (part > 0) {
+            const hipError_t e = hipMalloc(reinterpret_cast<void**>(&ch->rpart), size_t(part) * sizeof(float));
+            if (e != hipSuccess) return fail(e);
+            ch->rpart_floats = part;
         }
     }
     ch->stages = std::move(prog);
@@ -613,7 +811,8 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
 
 hipError_t chain_run(const Chain* ch, hipStream_t stream) {
     for (const HostStage& h : ch->stages) {
-        const hipError_t e = h.kind == IQ_INT4 ? launch_stage_k<1>(h, stream) : launch_stage_k<0>(h, stream);
+        const hipError_t e = h.rows > 1 ? run_rows_stage(h, ch->rpart, ch->rpart_floats, stream)
+                                        : (h.kind == IQ_INT4 ? launch_stage_k<1>(h, stream) : launch_stage_k<0>(h, stream));
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -622,6 +821,8 @@ hipError_t chain_run(const Chain* ch, hipStream_t stream) {
 void chain_destroy(Chain* ch) {
     if (!ch) return;
     if (ch->partials) (void)hipFree(ch->partials);
+    if (ch->rpart) (void)hipFree(ch->rpart);
+    if (ch->rssq) (void)hipFree(ch->rssq);
     delete ch;
 }
 

@@ -131,7 +131,71 @@ struct GemvParams {
     int ntiles;  // 1-row kernel: 16-row tiles over all matrices
     int kr, gr;  // 1-row kernel: K ranges (workgroups per tile) and groups per range;
                  // gemvq: kr consecutive K ranges per workgroup
+    // Chain prologue (gemvr / gemvq instances with PRO): activation row m,
+    // column c is x[m * xstride + c], or with gqa_span > 0 the value row of
+    // c's key/value head, x[m * xstride + (c / gqa_span) * gqa_hd + c % gqa_hd];
+    // with norm, RMSNorm'd: (x * r_m) * norm[c], r_m = 1 / sqrt(sum_b
+    // ssq[m][b] / K + eps) over the ssq_n partial sums of squares of row m.
+    // to_part: K-range partial sums are written even when S == 1.
+    int64_t xstride;
+    int gqa_hd, gqa_span;
+    const uint16_t* norm;
+    const float* ssq;
+    int ssq_n;
+    float eps;
+    int to_part;
 };
+
+// ------------------------------------------------------------------ chain prologue
+// Byte offset of activation row m, columns [c, c + 8) (PRO instances).
+__device__ __forceinline__ uint32_t pro_x_offset(const GemvParams& p, int m, int64_t c) {
+    const int64_t src = p.gqa_span ? (c / p.gqa_span) * p.gqa_hd + c % p.gqa_hd : c;
+    return uint32_t((int64_t(m) * p.xstride + src) * 4);
+}
+
+// The RMSNorm row factors r_m of a PRO launch into rsc[0 .. M): step 1
+// requests this thread's partial sums of squares (thread t: row t / 8,
+// partials t % 8, t % 8 + 8, ...; issued before anything else), step 2
+// adds them in a fixed order (double) once they land.
+struct ProScale {
+    float sq[8];
+    __device__ __forceinline__ void request(const GemvParams& p, int tid) {
+        const rsrc_t r = make_rsrc(p.ssq, p.norm ? int64_t(p.M) * p.ssq_n * 4 : 0);
+        const int m = tid >> 3, j = tid & 7;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int b = j + 8 * k;
+            sq[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  r, (m < p.M && b < p.ssq_n) ? uint32_t(m * p.ssq_n + b) * 4 : kOob, 0, 0));
+        }
+    }
+    // every thread of the workgroup calls this (two barriers)
+    __device__ __forceinline__ void finish(const GemvParams& p, int tid, double (*part)[8], float* rsc) {
+        double v = 0.0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) v += double(sq[k]);
+        if (tid < 256) part[tid >> 3][tid & 7] = v;
+        __syncthreads();
+        if (tid < p.M) {
+            double ss = 0.0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss += part[tid][j];
+            rsc[tid] = 1.0f / __builtin_sqrtf(float(ss / double(p.K)) + p.eps);
+        }
+        __syncthreads();
+    }
+};
+
+// bf16 norm weights of columns [c, c + 8) applied to v (PRO with norm).
+__device__ __forceinline__ void pro_norm8(float (&v)[8], uint4 nw, float r) {
+    const uint32_t w4[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t h = w4[i >> 1];
+        const float wn = __uint_as_float((i & 1) ? (h & 0xFFFF0000u) : (h << 16));
+        v[i] = (v[i] * r) * wn;
+    }
+}
 
 // 16 bytes of a row at byte offset `off`, zero past `row_bytes` (unaligned
 // rows / ragged tails; test shapes only).
@@ -1586,7 +1650,7 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
 // (xh_split8; PK: the packed form), one barrier, and every wave multiplies
 // its weights by the range's operands group by group as they land.  S > 1
 // ranges write fp32 partial sums (gemvt_reduce_kernel).
-template <int KIND, bool PK, int NG>
+template <int KIND, bool PK, int NG, bool PRO = false>
 __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvParams p) {
     constexpr int WPG = KIND == 1 ? 1 : 2;
     constexpr int GB = PK ? kHGroupBytes / 2 : kHGroupBytes;  // operand bytes per group
@@ -1617,17 +1681,23 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     constexpr int NX = (PK ? 8 : 16) * NG * 16 / 512;
     static_assert(NX * 512 == (PK ? 8 : 16) * NG * 16, "whole DPP rows per task set");
     float xv[NX][8];
+    uint4 nwv[PRO ? NX : 1];
+    ProScale psc;
+    if constexpr (PRO) psc.request(p, tid);
     {
-        const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
+        const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * (PRO ? p.xstride : p.K) * 4);
+        const rsrc_t rn = make_rsrc(PRO ? p.norm : nullptr, PRO && p.norm ? p.K * 2 : 0);
 #pragma unroll
         for (int u = 0; u < NX; u++) {
             const int t = tid + 512 * u, j16 = t & 15, pr = t >> 4;
             const int m = PK ? pr & 7 : pr & 15, i = PK ? pr >> 3 : pr >> 4;
-            const uint32_t o = (i < gs && m < p.M)
-                                   ? uint32_t((int64_t(m) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
-                                   : kOob;
+            const int64_t c = int64_t(g0 + i) * kGroup + j16 * 8;
+            const bool ok = i < gs && m < p.M;
+            const uint32_t o = !ok ? kOob : (PRO ? pro_x_offset(p, m, c) : uint32_t((int64_t(m) * p.K + c) * 4));
             const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
             const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
+            if constexpr (PRO)
+                nwv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rn, ok ? uint32_t(c) * 2 : kOob, 0, 0));
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 xv[u][e] = a[e];
@@ -1654,11 +1724,19 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     }
     // 2. the operands and factors of the range (all 16 lanes of each
     //    (row, group) together), then one barrier
+    __shared__ double rsp[PRO ? kMaxRowsGemv : 1][8];
+    __shared__ float rsc[PRO ? kMaxRowsGemv : 1];
+    if constexpr (PRO) {
+        if (p.norm) psc.finish(p, tid, rsp, rsc);  // workgroup-uniform
+    }
 #pragma unroll
     for (int u = 0; u < NX; u++) {
         const int t = tid + 512 * u, j16 = t & 15, pr = t >> 4;
         const int m = PK ? pr & 7 : pr & 15, i = PK ? pr >> 3 : pr >> 4;
         const int qq = j16 >> 2, jj = j16 & 3;
+        if constexpr (PRO) {
+            if (p.norm) pro_norm8(xv[u], nwv[u], rsc[m < p.M ? m : 0]);
+        }
         half8_t ho, lo;
         float fac;
         xh_split8<KIND == 1>(xv[u], ho, lo, fac);
@@ -1727,7 +1805,7 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     for (int r = 0; r < 4; r++) {
         const int m = 4 * q + r;
         if (m >= p.M || ln >= rows) continue;
-        if (p.S == 1) {
+        if (p.S == 1 && !(PRO && p.to_part)) {
             const int64_t row = ts.row0 + ln;
             ts.m.y[int64_t(m) * ts.m.N + row] = acc[r] + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
         } else {
@@ -1752,7 +1830,7 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
 // MB blocks of 16 activation rows, each group's dequantised weights (one
 // chunk at a time) multiplied by every block's operand before the next
 // chunk, so the weights are read and converted once for all the rows.
-template <int KIND, int NG, int MB, bool LOOP>
+template <int KIND, int NG, int MB, bool LOOP, bool PRO = false>
 __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     constexpr int NW = KIND == 1 ? 2 : 4;  // 16-byte weight loads per lane and group
     __shared__ __attribute__((aligned(16))) half8_t Aq[MB][NG][8][64];  // [block][group][chunk][lane]
@@ -1786,6 +1864,8 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     const uint32_t vq = uint32_t(l32 * row_bytes + h * NW * 16);
     const uint32_t vs = uint32_t(l32 * G) * 2, vz = uint32_t(l32 * G);
 
+    __shared__ double rsp[PRO ? kMaxRowsGemv : 1][8];
+    __shared__ float rsc[PRO ? kMaxRowsGemv : 1];
     float acc[MB][8];
 #pragma unroll
     for (int b = 0; b < MB; b++)
@@ -1806,17 +1886,25 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
         constexpr int NX = MB * 16 * NG * 16 / 512;
         static_assert(NX * 512 == MB * 16 * NG * 16, "whole DPP rows per task set");
         float xv[NX][8];
+        uint4 nwv[PRO ? NX : 1];
+        ProScale psc;
+        if constexpr (PRO) {
+            if (it == 0) psc.request(p, tid);
+        }
         {
-            const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * p.K * 4);
+            const rsrc_t rxx = make_rsrc(p.x, int64_t(p.M) * (PRO ? p.xstride : p.K) * 4);
+            const rsrc_t rn = make_rsrc(PRO ? p.norm : nullptr, PRO && p.norm ? p.K * 2 : 0);
 #pragma unroll
             for (int u = 0; u < NX; u++) {
                 const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG;
                 const int row = 16 * ((t >> 8) / NG) + m;
-                const uint32_t o = (i < gs && row < p.M)
-                                       ? uint32_t((int64_t(row) * p.K + int64_t(g0 + i) * kGroup + j16 * 8) * 4)
-                                       : kOob;
+                const int64_t c = int64_t(g0 + i) * kGroup + j16 * 8;
+                const bool ok = i < gs && row < p.M;
+                const uint32_t o = !ok ? kOob : (PRO ? pro_x_offset(p, row, c) : uint32_t((int64_t(row) * p.K + c) * 4));
                 const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 0, 0));
                 const float4_t b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rxx, o, 16, 0));
+                if constexpr (PRO)
+                    nwv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rn, ok ? uint32_t(c) * 2 : kOob, 0, 0));
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     xv[u][e] = a[e];
@@ -1845,9 +1933,16 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
         // 2. the range's operands and factors (16 lanes per (row, group)):
         //    octet j16 = 8 h' + c of row m goes to chunk c, lanes m + 32 h'
         //    (hi) and m + 16 + 32 h' (lo); then one barrier
+        if constexpr (PRO) {
+            if (it == 0 && p.norm) psc.finish(p, tid, rsp, rsc);  // workgroup-uniform
+        }
 #pragma unroll
         for (int u = 0; u < NX; u++) {
             const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG, b = (t >> 8) / NG;
+            if constexpr (PRO) {
+                const int row = 16 * b + m;
+                if (p.norm) pro_norm8(xv[u], nwv[u], rsc[row < p.M ? row : 0]);
+            }
             half8_t ho, lo;
             float fac;
             xh_split8<KIND == 1>(xv[u], ho, lo, fac);
@@ -1902,7 +1997,7 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
         for (int r = 0; r < 8; r++) {
             const int m = 16 * b + 8 * (r >> 2) + 4 * h + (r & 3);
             if (m >= p.M) continue;
-            if (p.S == 1)
+            if (p.S == 1 && !(PRO && p.to_part))
                 mr.y[int64_t(m) * mr.N + row] = acc[b][r] + (mr.bias ? bf16_to_f32(mr.bias[row]) : 0.0f);
             else
                 p.part[(int64_t(range) * p.M + m) * ld + int64_t(mr.tile0) * 16 + row] = acc[b][r];
@@ -2355,6 +2450,120 @@ bool launch_gemm_rows(const float* x, const QView& W, const uint16_t* bias, int6
 hipError_t launch_gemv(const float* x, const QView& W, const uint16_t* bias, int M, float* y,
                        Workspace* ws, hipStream_t stream) {
     return launch_gemv_multi(x, &W, &bias, &y, 1, M, ws, stream);
+}
+
+// ------------------------------------------------------------------ B-row chain stages
+namespace {
+
+// The kernel and K ranges of a B-row chain stage (the rows GEMV of
+// launch_gemv_multi: gemvr, or gemvq from 17 rows and for wide int4 calls
+// from 9), every range's sums written to part [S][M][tiles * 16].
+struct RowsSetup {
+    GemvParams p{};
+    bool q = false;  // gemvq (else gemvr)
+    int S = 0;
+    unsigned grid = 0;
+    bool ok = false;
+};
+
+RowsSetup rows_setup(const QView* W, int n, int M, int64_t part_floats) {
+    RowsSetup r;
+    const int64_t K = W[0].cols, G = W[0].groups;
+    int tiles = 0, t32 = 0;
+    for (int i = 0; i < n; i++) {
+        r.p.mat[i] = MatRef{W[i].q, W[i].scales, W[i].zeros, nullptr, nullptr, W[i].rows, tiles};
+        tiles += int((W[i].rows + 15) / 16);
+        t32 += int((W[i].rows + 31) / 32);
+    }
+    if (M < 1 || M > kMaxRowsGemv || K % kGroup) return r;
+    r.p.nmat = n;
+    r.p.K = K;
+    r.p.G = G;
+    r.p.M = M;
+    r.p.ntiles = tiles;
+    r.p.to_part = 1;
+    const int cus = device_cu_count();
+    const bool use_q = M >= 17 || (M >= 9 && W[0].kind == 1 && tiles >= 1024);
+    if (!use_q) {
+        // launch_gemvr's ranges
+        const int nrb = (tiles + 7) / 8;
+        constexpr int ngr = 8;
+        int S = int((G + ngr - 1) / ngr);
+        S = std::max<int>(S, std::min<int>((2 * cus + nrb - 1) / nrb, int(G)));
+        const int gs = int((G + S - 1) / S);
+        S = int((G + gs - 1) / gs);
+        if (int64_t(S) * M * tiles * 16 <= part_floats) {
+            r.p.gs = gs;
+            r.p.S = S;
+            r.S = S;
+            r.grid = unsigned(nrb * S);
+            r.ok = true;
+            return r;
+        }
+        if (M < 7) return r;
+    }
+    const GqPlan pl = gemvq_plan(G, M, tiles, t32, W[0].kind, cus, part_floats);
+    if (!pl.ok) return r;
+    r.q = true;
+    r.p.gs = pl.gs;
+    r.p.S = pl.S;
+    r.p.kr = pl.L;
+    r.p.nrb = pl.nrb;
+    r.S = pl.S;
+    r.grid = unsigned(pl.nrb * pl.S);
+    r.ok = true;
+    return r;
+}
+
+}  // namespace
+
+int64_t chain_rows_partials(const QView* W, int n, int M, int64_t cap) {
+    const RowsSetup r = rows_setup(W, n, M, cap);
+    return r.ok ? int64_t(r.S) * M * r.p.ntiles * 16 : -1;
+}
+
+hipError_t launch_chain_rows(const QView* W, int n, int M, const RowsIn& in, float* part, int64_t part_floats,
+                             int* S, hipStream_t stream) {
+    RowsSetup r = rows_setup(W, n, M, part_floats);
+    if (!r.ok) return hipErrorInvalidValue;
+    GemvParams& p = r.p;
+    p.x = in.x;
+    p.xstride = in.xstride;
+    p.gqa_hd = in.gqa_hd;
+    p.gqa_span = in.gqa_span;
+    p.norm = in.norm;
+    p.ssq = in.ssq;
+    p.ssq_n = in.ssq_n;
+    p.eps = in.eps;
+    p.part = part;
+    *S = r.S;
+    const int kind = W[0].kind;
+    if (!r.q) {
+        if (M <= 8) {
+            if (kind == 1) gemvr_kernel<1, true, 8, true><<<r.grid, 512, 0, stream>>>(p);
+            else gemvr_kernel<0, true, 8, true><<<r.grid, 512, 0, stream>>>(p);
+        } else {
+            if (kind == 1) gemvr_kernel<1, false, 8, true><<<r.grid, 512, 0, stream>>>(p);
+            else gemvr_kernel<0, false, 8, true><<<r.grid, 512, 0, stream>>>(p);
+        }
+    } else if (M <= 16) {
+        if (kind == 1) {
+            if (p.kr > 1) gemvq_kernel<1, 6, 1, true, true><<<r.grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<1, 6, 1, false, true><<<r.grid, 512, 0, stream>>>(p);
+        } else {
+            if (p.kr > 1) gemvq_kernel<0, 4, 1, true, true><<<r.grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<0, 4, 1, false, true><<<r.grid, 512, 0, stream>>>(p);
+        }
+    } else {
+        if (kind == 1) {
+            if (p.kr > 1) gemvq_kernel<1, 4, 2, true, true><<<r.grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<1, 4, 2, false, true><<<r.grid, 512, 0, stream>>>(p);
+        } else {
+            if (p.kr > 1) gemvq_kernel<0, 2, 2, true, true><<<r.grid, 512, 0, stream>>>(p);
+            else gemvq_kernel<0, 4, 2, false, true><<<r.grid, 512, 0, stream>>>(p);
+        }
+    }
+    return hipGetLastError();
 }
 
 }  // namespace iq

@@ -104,6 +104,27 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
 hipError_t gemm_operands(Workspace* ws, int64_t T, int64_t K, bool lo, _Float16** ah, float** rs);
 int64_t gemm_operand_rows(const Workspace* ws, int64_t K);
 
+// Activations of a B-row chain stage: row m, column c is x[m xstride + c]
+// (gqa_span > 0: the value row of c's key/value head, x[m xstride +
+// (c / gqa_span) gqa_hd + c % gqa_hd]), RMSNorm'd when norm is set, with
+// row m's factor from the ssq_n partial sums of squares ssq[m][0 .. ssq_n).
+struct RowsIn {
+    const float* x;
+    int64_t xstride;
+    int gqa_hd, gqa_span;
+    const uint16_t* norm;
+    const float* ssq;
+    int ssq_n;
+    float eps;
+};
+// The rows GEMV of a chain stage on n <= 4 matrices sharing K and kind
+// (M in 1..32): every K range's sums into part [S][M][tiles * 16] (16-row
+// tiles of the matrices in order), S returned.  chain_rows_partials gives
+// the floats that needs for a capacity `cap` (-1: shape not covered).
+int64_t chain_rows_partials(const QView* W, int n, int M, int64_t cap);
+hipError_t launch_chain_rows(const QView* W, int n, int M, const RowsIn& in, float* part, int64_t part_floats,
+                             int* S, hipStream_t stream);
+
 // A validated stage program on the device (iq_chain.hip).
 struct Chain;
 void chain_destroy(Chain* ch);

@@ -57,6 +57,7 @@ class IqStage(ctypes.Structure):
         ("W", IqView * 3),
         ("bias", ctypes.c_void_p * 3),
         ("y", ctypes.c_void_p * 3),
+        ("rows", ctypes.c_int32),
     ]
 
 

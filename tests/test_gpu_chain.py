@@ -215,3 +215,87 @@ def test_chain_rejects_in_place_stages():
     with pytest.raises(RuntimeError, match="overlaps"):
         C.Chain([C.Stage([W.view], x, [y], out_op=C.OUT_RESIDUAL, residual=y)])
     C.Chain([C.Stage([W.view], x, [y]), C.Stage([W.view], y, [x])]).close()
+
+
+class RowView:
+    """Row b of a B-row DecodeStep, shaped like a 1-row step for check_step."""
+
+    def __init__(self, step, b):
+        B = step.rows
+        row = lambda t: t.view(B, -1)[b]
+        self.per_layer = [{k: row(v) for k, v in d.items()} for d in step.per_layer]
+        self.h_last = row(step.h_last)
+        self.logits = row(step.logits)
+
+
+@pytest.mark.parametrize("B", [2, 4, 16, 32])
+@pytest.mark.parametrize("kind,head_kind", [(1, 0), (0, 0)])
+def test_chain_rows_small_model_matches_forward(B, kind, head_kind):
+    """B sequences of one token each through the B-row stages: every stage of
+    every row against the oracle on the chain's own inputs, and every row's
+    logits against the float64 forward of its token."""
+    rng = np.random.default_rng(100 + B + 3 * kind + head_kind)
+    host, dev = make_model(rng, H=512, I=1536, nh=4, nkv=2, hd=128, V=1000, L=3, kind=kind, head_kind=head_kind)
+    tokens = [int(t) for t in rng.integers(0, 1000, B)]
+    say("chain rows small", B, kind, head_kind)
+    step = C.DecodeStep(dev, rows=B)
+    step.step(tokens)
+    torch.cuda.synchronize()
+    om = oracle_model(host)
+    worst = 0.0
+    for b in range(B):
+        check_step(RowView(step, b), host)
+        ref = O.decode_first_token_f64(om, tokens[b])
+        got = f64(RowView(step, b).logits)
+        worst = max(worst, float(np.abs(got - ref["logits"]).max() / np.abs(ref["logits"]).max()))
+    say(f"  end-to-end logits max rel {worst:.3g} over {B} rows")
+    assert worst <= 1e-3
+    first = step.logits.clone()
+    step.step(tokens)
+    torch.cuda.synchronize()
+    assert torch.equal(first, step.logits)
+
+
+@pytest.mark.parametrize("B", [16, 32])
+def test_chain_rows_7b_shapes_sampled(B):
+    """The 7B program (28 int4 layers, int8 lm_head) at B rows: gate|up on
+    the 32-row tile kernel, stage by stage on sampled output rows of a few
+    layers and sequences."""
+    rng = np.random.default_rng(70 + B)
+    host, dev = make_model(rng, H=3584, I=18944, nh=28, nkv=4, hd=128, V=152064, L=28, kind=1, head_kind=0,
+                           quantize=False)
+    tokens = [int(t) for t in rng.integers(0, 152064, B)]
+    say("chain rows 7B", B)
+    step = C.DecodeStep(dev, rows=B)
+    step.step(tokens)
+    torch.cuda.synchronize()
+    assert np.all(np.isfinite(f64(step.logits)))
+    pick = np.random.default_rng(2)
+    for b in (0, B // 2, B - 1):
+        check_step(RowView(step, b), host, idx_of=lambda n: np.unique(np.r_[0, n - 1, pick.choice(n, 32)]),
+                   layers=[0, 27])
+
+
+def test_chain_rows_embedding_input_norm():
+    """A B-row RMSNorm stage whose input no stage of the chain writes (its
+    row sums of squares come from the chain's own pass) and a mixed program:
+    a 1-row stage after B-row ones."""
+    rng = np.random.default_rng(12)
+    B, K, N = 5, 1024, 768
+    W = Mat(rng, N, K, 1)
+    W1 = Mat(rng, 256, N, 0)
+    x = rng.standard_normal((B, K)).astype(np.float32) * 3.0
+    nb = O.f32_to_bf16(rng.uniform(0.5, 1.5, K).astype(np.float32))
+    xd = torch.from_numpy(x).cuda()
+    y = torch.zeros(B * N, device="cuda")
+    y1 = torch.zeros(256, device="cuda")
+    ch = C.Chain([C.Stage([W.view], xd, [y], C.IN_RMSNORM, C.OUT_STORE, norm=bf16_dev(nb), eps=1e-5, rows=B),
+                  C.Stage([W1.view], y, [y1], rows=1)])
+    ch.run()
+    torch.cuda.synchronize()
+    yh = f64(y).reshape(B, N)
+    for b in range(B):
+        n = O.rmsnorm_f64(x[b], nb, 1e-5)
+        check_gemv(yh[b], W, n, np.arange(N), f"row {b}")
+    check_gemv(f64(y1), W1, yh[0], np.arange(256), "1-row stage after B-row stages")
+    ch.close()
