@@ -106,14 +106,14 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
     struct Regs {
         uint4 xr[XCH];
         uint4 wr[WCH];
-        uint32_t zr;
+        uint32_t zr[WCH];  // int4: the zero point of each weight chunk's row
     };
     Regs r0, r1;
 
     // Per-thread source rows, fixed for the whole K loop (a step adds its
     // column offset): the fast paths need no per-step bounds arithmetic.
     const uint8_t* wrow[WCH];
-    const uint8_t* zrow = nullptr;
+    const uint8_t* zrow[WCH];
     bool wok[WCH];
     int wcol[WCH];
 #pragma unroll
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
         wok[i] = row < BN && n < p.N;
         wrow[i] = p.q + (wok[i] ? n : 0) * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg);
         wcol[i] = KIND == 1 ? (c & 1) * 16 : (c & 3) * 16;  // byte offset inside the step
-        if (KIND == 1) zrow = p.zeros + (wok[i] ? n : 0) * p.G + gbeg;
+        zrow[i] = KIND == 1 ? p.zeros + (wok[i] ? n : 0) * p.G + gbeg : nullptr;
     }
     const void* xrow[XCH];
     bool xok[XCH];
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
     const rsrc_t rw = make_rsrc(p.q + n0 * row_bytes, nrows * row_bytes);
     const rsrc_t rsc = make_rsrc(p.scales + n0 * p.G, nrows * p.G * 2);
     const rsrc_t rzp = make_rsrc(KIND == 1 ? p.zeros + n0 * p.G : nullptr, KIND == 1 ? nrows * p.G : 0);
-    uint32_t xoff[XCH], woff[WCH], zoff = kOob;
+    uint32_t xoff[XCH], woff[WCH], zoff[WCH];
 #pragma unroll
     for (int i = 0; i < XCH; i++) {
         const int c = tid + NT * i;
@@ -165,13 +165,13 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
         const int c = tid + NT * i;
         const int row = KIND == 1 ? c >> 1 : c >> 2;
         woff[i] = wok[i] ? uint32_t(row * row_bytes + (KIND == 1 ? kbeg / 2 : kbeg) + wcol[i]) : kOob;
-        if (KIND == 1 && i == 0) zoff = wok[0] ? uint32_t(row * p.G + gbeg) : kOob;
+        zoff[i] = (KIND == 1 && wok[i]) ? uint32_t(row * p.G + gbeg) : kOob;
     }
 
     auto load_step = [&](Regs& rg, int kt) {
         uint4* xr = rg.xr;
         uint4* wr = rg.wr;
-        uint32_t& zr = rg.zr;
+        uint32_t* zr = rg.zr;
         const int64_t k0 = int64_t(kt) * BK;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
@@ -209,14 +209,17 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
                 wr[i] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
-        if (KIND == 1 && FASTW) zr = __builtin_amdgcn_raw_buffer_load_b8(rzp, zoff + uint32_t(k0 / kGroup), 0, 0);
-        else zr = (KIND == 1 && wok[0]) ? zrow[k0 / kGroup] : 0u;
+#pragma unroll
+        for (int i = 0; i < WCH; i++) {
+            if (KIND == 1 && FASTW) zr[i] = __builtin_amdgcn_raw_buffer_load_b8(rzp, zoff[i] + uint32_t(k0 / kGroup), 0, 0);
+            else zr[i] = (KIND == 1 && wok[i]) ? zrow[i][k0 / kGroup] : 0u;
+        }
     };
 
     auto store_step = [&](const Regs& rg, int buf) {
         const uint4* xr = rg.xr;
         const uint4* wr = rg.wr;
-        const uint32_t zr = rg.zr;
+        const uint32_t* zr = rg.zr;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const int c = tid + NT * i;
@@ -258,7 +261,7 @@ __global__ __launch_bounds__(BM == 256 ? 2 * kThreads : kThreads, BM == 256 ? 1 
                 if ((KIND == 1 ? c >> 1 : c >> 2) >= BN) continue;
             if (KIND == 1) {
                 const int row = c >> 1, kc = c & 1;
-                const int z = int(zr);
+                const int z = int(zr[i]);
                 uint32_t o[16];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
