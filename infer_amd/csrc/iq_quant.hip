@@ -295,12 +295,56 @@ __device__ __forceinline__ float oct_minf(float v) {
     return __builtin_fminf(v, dpp_f<0xB1>(v));
 }
 
+// Max over the 8 lanes of a half DPP row of non-negative values compared
+// as unsigned integers (bf16 / fp32 magnitude bits: the order of the
+// values).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ uint32_t oct_maxu(uint32_t v) {
+    v = max(v, dpp_u<0x141>(v));
+    v = max(v, dpp_u<0x4E>(v));
+    return max(v, dpp_u<0xB1>(v));
+}
+
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// Largest magnitude among a lane's 16 bf16 values (8 words), as bf16 bits:
+// magnitudes compare as unsigned integers; a result above 0x7F80 means the
+// lane holds a NaN.
+__device__ __forceinline__ uint32_t absmax16_bits(const uint32_t (&wd)[8]) {
+    u16x2_t m[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        m[i] = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, wd[2 * i] & 0x7FFF7FFFu),
+                                         __builtin_bit_cast(u16x2_t, wd[2 * i + 1] & 0x7FFF7FFFu));
+    m[0] = __builtin_elementwise_max(m[0], m[1]);
+    m[2] = __builtin_elementwise_max(m[2], m[3]);
+    m[0] = __builtin_elementwise_max(m[0], m[2]);
+    return max(uint32_t(m[0][0]), uint32_t(m[0][1]));
+}
+
+// Bytes 0 of c0..c3 in one word (two's complement int8 codes).
+__device__ __forceinline__ uint32_t pack4_b0(int c0, int c1, int c2, int c3) {
+    const uint32_t lo = __builtin_amdgcn_perm(uint32_t(c1), uint32_t(c0), 0x0C0C0400u);  // c0.b0 c1.b0 0 0
+    const uint32_t hi = __builtin_amdgcn_perm(uint32_t(c3), uint32_t(c2), 0x0C0C0400u);  // c2.b0 c3.b0 0 0
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 // quantize for cols % 128 == 0: the arithmetic of quantize_kernel with 8
 // lanes per group and 16 columns per lane (two 16-byte loads), so the
 // per-group work (reductions, the scale's two divisions and its bf16
 // rounding, addresses) is spread over twice the values.  Items are (row,
 // 8 groups); rows whose group count is not a multiple of 8 leave the
-// surplus lanes of their last item idle.
+// surplus lanes of their last item idle.  A wave walks its items in grid
+// strides with three register sets: the values of the next two items are
+// in flight while one is converted (each set is refilled right after its
+// item is converted, so no wait covers a newer request), and the item
+// cursor is wave-uniform (scalar arithmetic).  Group statistics: the
+// magnitudes of groups without NaN are compared as unsigned bf16 bits
+// (packed 16-bit maxima), the int4 range with fp32 min / max; a wave
+// holding a NaN takes the reference's comparison loop.
 template <int KIND>
 __global__ __launch_bounds__(kQThreads) void quantize8_kernel(const uint16_t* __restrict__ w, int64_t rows,
                                                               int64_t cols, int64_t G, int64_t octs,
@@ -309,7 +353,9 @@ __global__ __launch_bounds__(kQThreads) void quantize8_kernel(const uint16_t* __
     const int lane = threadIdx.x & 63, sub = lane & 7;
     const int64_t items = rows * octs;
     const int64_t stride = int64_t(gridDim.x) * (kQThreads / 64);
-    const int64_t first = int64_t(blockIdx.x) * (kQThreads / 64) + (threadIdx.x >> 6);
+    const int64_t first0 = int64_t(blockIdx.x) * (kQThreads / 64) + (threadIdx.x >> 6);
+    const int64_t first = (int64_t(__builtin_amdgcn_readfirstlane(uint32_t(first0 >> 32))) << 32) |
+                          int64_t(__builtin_amdgcn_readfirstlane(uint32_t(first0)));
     if (first >= items) return;
     const int64_t sr = stride / octs, so = stride % octs;
     struct Cursor {
@@ -327,10 +373,8 @@ __global__ __launch_bounds__(kQThreads) void quantize8_kernel(const uint16_t* __
         uint4 a, b;
     };
     auto fetch = [&](const Cursor& c) {
-        const int64_t r = (int64_t(__builtin_amdgcn_readfirstlane(uint32_t(c.r >> 32))) << 32) |
-                          int64_t(__builtin_amdgcn_readfirstlane(uint32_t(c.r)));
-        const bool rok = r < rows;
-        const rsrc_t rw = make_rsrc(w + (rok ? r : 0) * cols, rok ? cols * 2 : 0);
+        const bool rok = c.r < rows;
+        const rsrc_t rw = make_rsrc(w + (rok ? c.r : 0) * cols, rok ? cols * 2 : 0);
         const int64_t g = c.o * 8 + (lane >> 3);
         const uint32_t off = g < G ? uint32_t((g * kGroup + sub * 16) * 2) : kOob;
         Raw x;
@@ -338,66 +382,86 @@ __global__ __launch_bounds__(kQThreads) void quantize8_kernel(const uint16_t* __
         x.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 16, 0));
         return x;
     };
-    Cursor cc{first / octs, first % octs}, fc = cc;
-    Raw r0 = fetch(fc);
-    advance(fc);
-    Raw r1 = fetch(fc);
-    advance(fc);
-    for (; cc.r < rows; advance(cc)) {
-        const Raw cur = r0;
-        r0 = r1;
-        r1 = fetch(fc);
-        advance(fc);
+    auto process = [&](const Cursor& cc, const Raw& cur) {
         const int64_t r = cc.r;
         const int64_t g = cc.o * 8 + (lane >> 3);
         const bool gvalid = g < G;
+        const uint32_t wd[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
         float v[16];
-        {
-            const uint32_t wd[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                v[2 * i] = __uint_as_float(wd[i] << 16);
-                v[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
-            }
+        for (int i = 0; i < 8; i++) {
+            v[2 * i] = __uint_as_float(wd[i] << 16);
+            v[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
         }
         const int64_t c0 = g * kGroup + sub * 16;
+        const uint32_t mb = absmax16_bits(wd);
+        const bool nan = __builtin_amdgcn_ballot_w64(mb > 0x7F80u) != 0;  // wave-uniform
         if (KIND == 0) {
-            // amax = std::max(amax, fabs(v)): comparisons skip NaN (quiet or
-            // signalling; a maxNum would turn a signalling NaN into NaN)
-            float amax = 0.0f;
+            // amax = std::max(amax, fabs(v)) over the group: without NaN the
+            // largest magnitude (exact); with one, the reference's loop
+            // (comparisons skip NaN, quiet or signalling)
+            float amax;
+            if (!nan) {
+                amax = __uint_as_float(oct_maxu(mb) << 16);
+            } else {
+                amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float a = __builtin_fabsf(v[i]);
-                amax = amax < a ? a : amax;
+                for (int i = 0; i < 16; i++) {
+                    const float a = __builtin_fabsf(v[i]);
+                    amax = amax < a ? a : amax;
+                }
+                amax = oct_maxf(amax);
             }
-            amax = oct_maxf(amax);
             const uint16_t sb = f32_to_bf16(amax > 0.0f ? amax / 127.0f : 1.0f);
             const QScale qs = qscale(bf16_to_f32(sb));
-            uint32_t d[4] = {0, 0, 0, 0};
+            uint32_t d[4];
             const bool plain = qs.up == 1.0f && qs.s < 3.0e38f;
             if (__builtin_amdgcn_ballot_w64(!plain) == 0) {
                 const float rf = __builtin_amdgcn_rcpf(qs.s);
+                int c[16];
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int c = clampi(qdiv_fast(v[i], qs.s, rf), -127, 127);
-                    d[i / 4] |= uint32_t(uint8_t(int8_t(c))) << (8 * (i % 4));
-                }
+                for (int i = 0; i < 16; i++) c[i] = clampi(qdiv_fast(v[i], qs.s, rf), -127, 127);
+#pragma unroll
+                for (int j = 0; j < 4; j++) d[j] = pack4_b0(c[4 * j], c[4 * j + 1], c[4 * j + 2], c[4 * j + 3]);
             } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) d[j] = 0;
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int c = clampi(qdiv(v[i] * qs.up, qs.s, qs.r()), -127, 127);
                     d[i / 4] |= uint32_t(uint8_t(int8_t(c))) << (8 * (i % 4));
                 }
             }
-            if (!gvalid) continue;
+            if (!gvalid) return;
             if (sub == 0) scales[r * G + g] = sb;
             *reinterpret_cast<uint4*>(q + r * cols + c0) = make_uint4(d[0], d[1], d[2], d[3]);
         } else {
+            // lo = min(0, min w), hi = max(0, max w) over the group, NaN
+            // skipped: without NaN fp32 min / max in any order (the zero's
+            // sign, which maxNum may pick either way, reaches no output)
             float mn = 0.0f, mx = 0.0f;
+            if (!nan) {
+                float a[8], b[8];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                mn = v[i] < mn ? v[i] : mn;
-                mx = mx < v[i] ? v[i] : mx;
+                for (int i = 0; i < 8; i++) {
+                    a[i] = __builtin_fminf(v[2 * i], v[2 * i + 1]);
+                    b[i] = __builtin_fmaxf(v[2 * i], v[2 * i + 1]);
+                }
+#pragma unroll
+                for (int s2 = 4; s2 >= 1; s2 >>= 1)
+#pragma unroll
+                    for (int i = 0; i < s2; i++) {
+                        a[i] = __builtin_fminf(a[i], a[i + s2]);
+                        b[i] = __builtin_fmaxf(b[i], b[i + s2]);
+                    }
+                mn = __builtin_fminf(a[0], 0.0f);
+                mx = __builtin_fmaxf(b[0], 0.0f);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    mn = v[i] < mn ? v[i] : mn;
+                    mx = mx < v[i] ? v[i] : mx;
+                }
             }
             mn = oct_minf(mn);
             mx = oct_maxf(mx);
@@ -422,13 +486,38 @@ __global__ __launch_bounds__(kQThreads) void quantize8_kernel(const uint16_t* __
                     d[i / 8] |= uint32_t(c) << (4 * (i % 8));
                 }
             }
-            if (!gvalid) continue;
+            if (!gvalid) return;
             if (sub == 0) {
                 scales[r * G + g] = sb;
                 zeros[r * G + g] = uint8_t(z);
             }
             *reinterpret_cast<uint2*>(q + (r * cols + c0) / 2) = make_uint2(d[0], d[1]);
         }
+    };
+    Cursor c0{first / octs, first % octs}, c1 = c0, c2;
+    advance(c1);
+    c2 = c1;
+    advance(c2);
+    Raw ra = fetch(c0), rb = fetch(c1), rc;
+    // three items per iteration: sets a, b, c hold items c0, c1, c2
+    for (;;) {
+        rc = fetch(c2);
+        process(c0, ra);
+        Cursor n = c2;
+        advance(n);  // c0 + 3 strides
+        if (c1.r >= rows) break;
+        ra = fetch(n);
+        process(c1, rb);
+        if (c2.r >= rows) break;
+        Cursor n1 = n;
+        advance(n1);
+        rb = fetch(n1);
+        process(c2, rc);
+        if (n.r >= rows) break;
+        c0 = n;
+        c1 = n1;
+        c2 = n1;
+        advance(c2);
     }
 }
 
