@@ -346,7 +346,7 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
     const int am = R == 1 ? 0 : ln >> 2, aL = R == 1 ? ln : ln & 3;  // A row of this lane
     const bool alive = am < M;
     const int xoff = (am * RS - glo) * kLimbRec + aL * kGroup + kg * 16;
-    const int moff = (R == 1 ? 0 : kg) * RS - glo;
+    const int moff = (R == 1 ? 0 : (kg < R ? kg : 0)) * RS - glo;  // (lane groups past R: row 0, never stored)
     // blocks of 4 groups: an early exit over at most 8 iterations still
     // unrolls fully (so the slice stays in registers)
 #pragma unroll
@@ -970,8 +970,12 @@ int gemv1_mode(int64_t K, int64_t G, const float* x) {
 }
 
 // Rows of the 1-row kernel instance for M activation rows, and its dynamic
-// LDS (limbs of up to 4 rows, meta records of all).
-int gemv1_rows(int M) { return M > 4 ? 8 : (M > 1 ? 4 : 1); }
+// LDS (limbs of up to 4 rows, meta records of all).  2 rows have their own
+// instance (A rows 0..7; 63-66 VGPRs against 79-82 for 4 rows, so 7-8
+// waves per SIMD and half the limb LDS): 7B int4 step at 2 rows 1681 ->
+// 1505 us (gate|up 25.5 -> 20.5, down 19.9 -> 18.0, lm_head int8 107.5 ->
+// 94.7 us).
+int gemv1_rows(int M) { return M > 4 ? 8 : (M > 2 ? 4 : M); }
 size_t gemv1_lds(int64_t G, int R) { return size_t(G) * ((R < 4 ? R : 4) * kLimbRec + R * 16); }
 
 // 1..4 rows always; 5..8 rows (two blocks of 4, the second converted after
@@ -1010,7 +1014,7 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
     // tile) whose records fit 64 KiB, multiples of 4 groups (7B down at 2
     // rows: int4 27.0 -> 18.0, int8 30.2 -> 23.8 us); 1 row, and 5..8 rows
     // (measured slower split: down 27 -> 32 us at 8 rows): one range
-    if (R == 4) {
+    if (R == 2 || R == 4) {
         while (gemv1_lds(pl.gr, R) > 64 * 1024 && pl.kr < 8) {
             pl.kr++;
             pl.gr = int((G + pl.kr - 1) / pl.kr + 3) / 4 * 4;
@@ -1050,6 +1054,18 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
     } while (0)
     if (p.M > 4) {
         if constexpr (NG <= 4) IQ_G1(2, 8, false);
+        return;
+    }
+    if (p.M == 2) {
+        if constexpr (NG <= (KIND == 1 ? 4 : 8)) {
+            if (mode == 2) {
+                if (p.kr > 1) IQ_G1(2, 2, true);
+                else IQ_G1(2, 2, false);
+            } else {
+                if (p.kr > 1) IQ_G1(1, 2, true);
+                else IQ_G1(1, 2, false);
+            }
+        }
         return;
     }
     if (p.M > 1) {
