@@ -879,19 +879,22 @@ iq_view to_iq(const QuantView& v) {
 }
 }  // namespace
 
-DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
+DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg, int rows) : m_(m) {
     const int64_t H = cfg.hidden_size, I = cfg.intermediate_size, V = cfg.vocab_size;
     const int64_t hd = cfg.head_dim, nh = cfg.num_attention_heads, nkv = cfg.num_key_value_heads;
     const int64_t qo = nh * hd, kvo = nkv * hd, L = cfg.num_hidden_layers;
     H_ = H;
     V_ = V;
+    if (rows < 1 || rows > 32) throw std::runtime_error("DecodeStep: rows must be 1..32");
+    B_ = rows;
     if (int64_t(m.layers.size()) != L) throw std::runtime_error("DecodeStep: model and config disagree on layers");
-    // arena: h0, per layer q, k, v, h1, act, h2, then logits; each vector on
-    // its own 1 KiB boundary
-    auto pad = [](int64_t n) { return (n + 255) / 256 * 256; };
+    // arena: h0, per layer q, k, v, h1, act, h2, then logits, each [B][n];
+    // each block on its own 1 KiB boundary
+    const int64_t B = rows;
+    auto pad = [B](int64_t n) { return (B * n + 255) / 256 * 256; };
     int64_t total = pad(H) + L * (pad(qo) + 2 * pad(kvo) + 2 * pad(H) + pad(I)) + pad(V);
     hip_check(hipMalloc(reinterpret_cast<void**>(&arena_), size_t(total) * 4), "DecodeStep: hipMalloc");
-    if (hipMalloc(reinterpret_cast<void**>(&ids_), 8) != hipSuccess) {
+    if (hipMalloc(reinterpret_cast<void**>(&ids_), size_t(8 * B)) != hipSuccess) {
         (void)hipFree(arena_);
         throw std::runtime_error("DecodeStep: hipMalloc");
     }
@@ -909,6 +912,7 @@ DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
         const DevLayer& D = m.layers[size_t(l)];
         float *q = take(qo), *k = take(kvo), *v = take(kvo), *h1 = take(H), *act = take(I), *h2 = take(H);
         iq_stage a{};
+        a.rows = rows;
         a.in_op = IQ_IN_RMSNORM;
         a.out_op = IQ_OUT_STORE;
         a.n = 3;
@@ -926,6 +930,7 @@ DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
         a.y[2] = v;
         st.push_back(a);
         iq_stage o{};
+        o.rows = rows;
         o.in_op = IQ_IN_GQA;
         o.out_op = IQ_OUT_RESIDUAL;
         o.n = 1;
@@ -937,6 +942,7 @@ DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
         o.y[0] = h1;
         st.push_back(o);
         iq_stage g{};
+        g.rows = rows;
         g.in_op = IQ_IN_RMSNORM;
         g.out_op = IQ_OUT_SWIGLU;
         g.n = 2;
@@ -948,6 +954,7 @@ DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
         g.y[0] = act;
         st.push_back(g);
         iq_stage d{};
+        d.rows = rows;
         d.in_op = IQ_IN_PLAIN;
         d.out_op = IQ_OUT_RESIDUAL;
         d.n = 1;
@@ -961,6 +968,7 @@ DecodeStep::DecodeStep(const DevQuantModel& m, const ModelConfig& cfg) : m_(m) {
     }
     logits_ = take(V);
     iq_stage f{};
+    f.rows = rows;
     f.in_op = IQ_IN_RMSNORM;
     f.out_op = IQ_OUT_STORE;
     f.n = 1;
@@ -985,13 +993,22 @@ DecodeStep::~DecodeStep() {
 }
 
 void DecodeStep::step(int64_t token, hipStream_t stream) {
-    if (token < 0 || token >= V_) throw std::runtime_error("DecodeStep: token id out of range");
-    hip_check(hipMemcpyAsync(ids_, &token, 8, hipMemcpyHostToDevice, stream), "DecodeStep: id upload");
+    const std::vector<int64_t> t(size_t(B_), token);
+    step(t.data(), B_, stream);
+}
+
+void DecodeStep::step(const int64_t* tokens, int n, hipStream_t stream) {
+    if (n != B_) throw std::runtime_error("DecodeStep: one token per row expected");
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= V_) throw std::runtime_error("DecodeStep: token id out of range");
+    hip_check(hipMemcpyAsync(ids_, tokens, size_t(8 * n), hipMemcpyHostToDevice, stream), "DecodeStep: id upload");
+    // (the copy has read the caller's array when this returns)
+    hip_check(hipStreamSynchronize(stream), "DecodeStep: id upload");
     run(stream);
 }
 
 void DecodeStep::run(hipStream_t stream) {
-    iq_check(iq_embedding(reinterpret_cast<const iq_view*>(&m_.embed_tokens.view()), ids_, 1, H_, h_[0], stream),
+    iq_check(iq_embedding(reinterpret_cast<const iq_view*>(&m_.embed_tokens.view()), ids_, B_, H_, h_[0], stream),
              "DecodeStep: embedding");
     iq_check(iq_chain_run(chain_, stream), "DecodeStep: chain");
 }

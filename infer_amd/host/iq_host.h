@@ -247,26 +247,33 @@ struct DevQuantModel {
 // q|k|v (+ biases), single-key attention (each query head takes its kv
 // head's value row: the softmax over one key is 1) -> o + residual,
 // RMSNorm -> gate|up with the SwiGLU epilogue, down + residual, and the
-// final RMSNorm -> LM head.  Every intermediate vector has its own device
-// buffer.  The model's widths must be multiples of 256 (the chain's stage
-// rule).  Runs are asynchronous on `stream`; run(stream) issues only device
-// work (capturable into a HIP graph) after the token id is in ids().
+// final RMSNorm -> LM head.  `rows` sequences (1..32, GpuBatch::kMaxRows,
+// kernels/batch_gpu.h:80) of one token each run together, as GpuBatch::step
+// runs its batch (kernels/batch_gpu.cu:186-215): every vector is [rows][n].
+// Every intermediate vector has its own device buffer.  The model's widths
+// must be multiples of 256 (the chain's stage rule).  run(stream) issues
+// only device work (capturable into a HIP graph) after the token ids are in
+// ids().
 class DecodeStep {
 public:
-    DecodeStep(const DevQuantModel& m, const ModelConfig& cfg);
+    DecodeStep(const DevQuantModel& m, const ModelConfig& cfg, int rows = 1);
     ~DecodeStep();
     DecodeStep(const DecodeStep&) = delete;
     DecodeStep& operator=(const DecodeStep&) = delete;
-    // copies `token` to ids() (host to device, on `stream`), then run()
+    // copies the token ids to ids() (host to device, on `stream`; `token`
+    // for every row), then run()
     void step(int64_t token, hipStream_t stream = nullptr);
+    void step(const int64_t* tokens, int n, hipStream_t stream = nullptr);  // n == rows()
     void run(hipStream_t stream = nullptr);
-    int64_t* ids() const { return ids_; }            // device, 1 id
-    const float* logits() const { return logits_; }  // device, vocab_size
-    const float* hidden(int layer) const;            // residual stream entering `layer` (layers: the last)
+    int rows() const { return B_; }
+    int64_t* ids() const { return ids_; }            // device, rows() ids
+    const float* logits() const { return logits_; }  // device, [rows()][vocab_size]
+    const float* hidden(int layer) const;            // residual stream entering `layer` (layers: the last), [rows()][H]
 
 private:
     const DevQuantModel& m_;
     int64_t H_ = 0, V_ = 0;
+    int B_ = 1;
     float* arena_ = nullptr;
     int64_t* ids_ = nullptr;
     float* logits_ = nullptr;

@@ -404,9 +404,14 @@ int cmd_chain(const std::string& bin, const std::string& dir, const std::string&
     llm::QuantModel qm;
     qm.load(dir, kind_of(kind));
     llm::gpu::DevQuantModel dm(qm);
-    llm::gpu::DecodeStep step(dm, qm.cfg);
-    step.step(token);
-    std::vector<float> logits(size_t(cfg.vocab_size));
+    // rows > 1 (env IQ_TEST_ROWS): row b takes token + 7 b
+    const char* re = std::getenv("IQ_TEST_ROWS");
+    const int rows = re ? std::atoi(re) : 1;
+    llm::gpu::DecodeStep step(dm, qm.cfg, rows);
+    std::vector<int64_t> toks(static_cast<size_t>(rows));
+    for (int b = 0; b < rows; b++) toks[size_t(b)] = (token + 7 * b) % cfg.vocab_size;
+    step.step(toks.data(), rows);
+    std::vector<float> logits(size_t(cfg.vocab_size) * size_t(rows));
     hip_ok(hipMemcpy(logits.data(), step.logits(), logits.size() * 4, hipMemcpyDeviceToHost), "logits");
     std::ofstream f(out, std::ios::binary);
     f.write(reinterpret_cast<const char*>(logits.data()), std::streamsize(logits.size() * 4));

@@ -132,12 +132,13 @@ def test_quantize_model_on_gpu_writes_the_reference_file(kind, fname, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["int8", "int4"])
-def test_decode_step_through_the_host_layer(kind, tmp_path):
+@pytest.mark.parametrize("kind,rows", [("int8", 1), ("int4", 1), ("int4", 3), ("int8", 12)])
+def test_decode_step_through_the_host_layer(kind, rows, tmp_path):
     """The C++ host path end to end: quantize_model (GPU) writes a .llmq,
     QuantModel::load reads it, DevQuantModel uploads it, gpu::DecodeStep
-    runs the chained decode step of one token; its logits match the
-    oracle's float64 forward of src/forward.cpp on the dequantised weights
+    runs the chained decode step of one token per sequence for `rows`
+    sequences (row b: token + 7 b); every row's logits match the oracle's
+    float64 forward of src/forward.cpp on the dequantised weights
     (max |err| / max |ref| <= 1e-3)."""
     import numpy as np
     from oracle import oracle as O
@@ -162,8 +163,12 @@ def test_decode_step_through_the_host_layer(kind, tmp_path):
     _write_tensors(str(tmp_path / "tensors.bin"), ents)
     token = 123
     out = str(tmp_path / "logits.bin")
-    print("host chain", kind, flush=True)
-    rc, o, e = run("chain", str(tmp_path / "tensors.bin"), str(tmp_path), kind, str(token), out, timeout=110)
+    print("host chain", kind, rows, flush=True)
+    os.environ["IQ_TEST_ROWS"] = str(rows)
+    try:
+        rc, o, e = run("chain", str(tmp_path / "tensors.bin"), str(tmp_path), kind, str(token), out, timeout=110)
+    finally:
+        del os.environ["IQ_TEST_ROWS"]
     assert rc == 0, o + e
     got = np.fromfile(out, dtype=np.float32).astype(np.float64)
     k = 1 if kind == "int4" else 0
@@ -186,7 +191,9 @@ def test_decode_step_through_the_host_layer(kind, tmp_path):
             "down": dq(p + "mlp.down_proj.weight"), "input_ln": t[p + "input_layernorm.weight"],
             "post_ln": t[p + "post_attention_layernorm.weight"], "q_b": t[p + "self_attn.q_proj.bias"],
             "k_b": t[p + "self_attn.k_proj.bias"], "v_b": t[p + "self_attn.v_proj.bias"]})
-    ref = O.decode_first_token_f64(model, token)["logits"]
-    rel = float(np.abs(got - ref).max() / np.abs(ref).max())
-    print(f"  logits max rel {rel:.3g}", flush=True)
-    assert rel <= 1e-3
+    got = got.reshape(rows, V)
+    for b in range(rows):
+        ref = O.decode_first_token_f64(model, (token + 7 * b) % V)["logits"]
+        rel = float(np.abs(got[b] - ref).max() / np.abs(ref).max())
+        print(f"  row {b} logits max rel {rel:.3g}", flush=True)
+        assert rel <= 1e-3
