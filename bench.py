@@ -600,7 +600,7 @@ def main():
         detail["7b_int4_decode_chain_m1"] = bench_decode_chain(torch, ops, m4, args.steps, args.warmup)
         # the chained step at B sequences (B-row stages), beside the bare
         # linear set at the same widths
-        for B in (4, 16, 32):
+        for B in (2, 4, 16, 32):
             dc = bench_decode_chain(torch, ops, m4, args.steps, args.warmup, rows=B)
             dc["ratio_vs_chain_m1"] = round(dc["us_per_step"] / detail["7b_int4_decode_chain_m1"]["us_per_step"], 3)
             detail[f"7b_int4_decode_chain_m{B}"] = dc

@@ -86,6 +86,10 @@ struct CStage {
     int32_t ssq_n;
     // per-tile sums of squares of this stage's output (for a later RMSNorm), or null
     float* ssq_out;
+    // activation rows (R-row instances: 1..R; row m of x at m * xlen, of
+    // residual and y at m * N); per-row sums of squares: ssq_in [rows][ssq_n]
+    // and ssq_out [rows][tiles]
+    int32_t rows;
 };
 
 // Output side of a B-row stage (epi_kernel): the K-range sums of the rows
@@ -116,6 +120,7 @@ struct HostStage {
     size_t lds;
     // B-row stages (rows > 1)
     int rows = 1;
+    int fused_r = 1;  // > 1: one stage_kernel launch of the R-row instance (rows <= R)
     QView W[kMaxStageMats];
     RowsIn in{};
     CEpi epi{};
@@ -161,10 +166,16 @@ __device__ __forceinline__ float row16_fsum(float v) {
 // the K slice [w gs, w gs + gs).  NG = slice capacity in groups (a multiple
 // of 4).  Dynamic LDS: limb records [G][512] | meta [G] int4 | (RMSNorm
 // without producer partials) the raw input [K] fp32.
-template <int KIND, int NG, int TP, int NORM>
+// R = 2 or 4: up to R activation rows per launch (st.rows), the limb records
+// [R][G][512] and meta [R][G]; A row 4m + L = limb L of activation row m (as
+// in the 1-row GEMV's 4-row instance), lane group m of D holding row m's
+// sums; RMSNorm only from per-row partial sums of squares (NORM 1: st.ssq_n
+// <= 256 per row), slices of at most 4 groups.
+template <int KIND, int NG, int TP, int NORM, int R>
 __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void stage_kernel(const CStage st) {
+    static_assert(R == 1 || (NG == 4 && NORM != 2), "R-row stages: 4-group slices, producer sums of squares");
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
-    __shared__ float red[kMaxWaves][TP][16];
+    __shared__ float red[kMaxWaves][TP][16 * R];
     __shared__ double ssq[kMaxWaves];
     __shared__ int arrived;
     constexpr int WPG = KIND == 1 ? 1 : 2;  // 16-byte weight loads per group
@@ -175,7 +186,8 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     const int G = st.G, K = st.K;
     const int g0 = wave * st.gs < G ? wave * st.gs : G;
     const int gs = (g0 + st.gs < G ? g0 + st.gs : G) - g0;
-    int4* ms = reinterpret_cast<int4*>(lds + G * kLimbRec);
+    const int M = R == 1 ? 1 : st.rows;
+    int4* ms = reinterpret_cast<int4*>(lds + R * G * kLimbRec);
     float* xraw = reinterpret_cast<float*>(lds + G * (kLimbRec + 16));
 
     // the unit's tiles and their matrices
@@ -203,8 +215,8 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     constexpr bool full = NORM == 2;
     constexpr int kMaxChunks = NORM == 2 ? 4 : 1;  // 16-byte chunks per thread
     const int xlen = st.in_op == IQ_IN_GQA ? K / (st.gqa_span / st.gqa_hd) : K;
-    const rsrc_t rx = make_rsrc(st.x, int64_t(xlen) * 4);
-    u32x4_t xc[kMaxChunks], xw[XP][2], nwv[norm ? XP : 1];
+    const rsrc_t rx = make_rsrc(st.x, int64_t(M) * xlen * 4);
+    u32x4_t xc[R == 1 ? kMaxChunks : R], xw[R][XP][2], nwv[norm ? XP : 1];
     if constexpr (full) {
         const int nchunk = K / 4, nthr = nw * 64;
 #pragma unroll
@@ -214,18 +226,27 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
         }
     } else {
         if constexpr (norm) {
-            // the producer's per-tile sums of squares, 4 per lane
-            const rsrc_t rp = make_rsrc(st.ssq_in, int64_t(st.ssq_n) * 4);
-            xc[0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, uint32_t(lane) * 16, 0, 0));
+            // the producer's sums of squares, 4 per lane (row m: ssq_n of
+            // them at m * ssq_n)
+            const rsrc_t rp = make_rsrc(st.ssq_in, int64_t(M) * st.ssq_n * 4);
+#pragma unroll
+            for (int m = 0; m < (R == 1 ? 1 : R); m++) {
+                const uint32_t o = (m < M && 4 * lane < st.ssq_n) ? uint32_t(m * st.ssq_n + 4 * lane) * 4 : kOob;
+                xc[m] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        rp, R == 1 ? uint32_t(lane) * 16 : o, 0, 0));
+            }
         }
 #pragma unroll
-        for (int t = 0; t < XP; t++) {
-            const int g = g0 + 4 * t + kg;
-            int k0 = g * kGroup + ln * 8;
-            if (st.in_op == IQ_IN_GQA) k0 = (k0 / st.gqa_span) * st.gqa_hd + (k0 % st.gqa_hd);
-            const uint32_t off = 4 * t + kg < gs ? uint32_t(k0) * 4 : kOob;
-            xw[t][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
-            xw[t][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 16, 0));
+        for (int m = 0; m < R; m++) {
+#pragma unroll
+            for (int t = 0; t < XP; t++) {
+                const int g = g0 + 4 * t + kg;
+                int k0 = g * kGroup + ln * 8;
+                if (st.in_op == IQ_IN_GQA) k0 = (k0 / st.gqa_span) * st.gqa_hd + (k0 % st.gqa_hd);
+                const uint32_t off = (4 * t + kg < gs && m < M) ? uint32_t(m * xlen + k0) * 4 : kOob;
+                xw[m][t][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+                xw[m][t][1] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 16, 0));
+            }
         }
     }
     if constexpr (norm) {
@@ -237,19 +258,21 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
                                                      rn, 4 * t + kg < gs ? uint32_t(g * kGroup + ln * 8) * 2 : kOob, 0, 0));
         }
     }
-    // bias (and residual) of the rows this lane may store (lanes 0..15 of
-    // every wave: the last wave to finish stores); rows past N read zero
+    // bias (and residual) of the rows this lane may store (lane group m <
+    // M of every wave, activation row m: the last wave to finish stores);
+    // rows past N read zero
     uint32_t addb[TP], resb = 0;
     {
-        const uint32_t ro = lane < 16 ? uint32_t(row0 + ln) : 0x20000000u;
+        const bool st_lane = lane < 16 * M;
+        const uint32_t ro = st_lane ? uint32_t(row0 + ln) : 0x20000000u;
 #pragma unroll
         for (int t = 0; t < TP; t++) {
             const rsrc_t rb = make_rsrc(Ms[t].bias, Ms[t].bias ? N * 2 : 0);
             addb[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, ro * 2, 0, 0);
         }
         if (TP == 1 && st.out_op == IQ_OUT_RESIDUAL) {
-            const rsrc_t rr = make_rsrc(st.res, N * 4);
-            resb = __builtin_amdgcn_raw_buffer_load_b32(rr, ro * 4, 0, 0);
+            const rsrc_t rr = make_rsrc(st.res, int64_t(M) * N * 4);
+            resb = __builtin_amdgcn_raw_buffer_load_b32(rr, st_lane ? uint32_t(kg * N + row0 + ln) * 4 : kOob, 0, 0);
         }
     }
     if (tid == 0) arrived = 0;
@@ -304,8 +327,10 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     //    fixed order: from the producer's per-tile sums (every wave adds
     //    them itself), or from the whole input (reduced through LDS, the raw
     //    input kept in LDS for the slices).
-    float xv[XP][8];
-    float scale = 1.0f;
+    float xv[R][XP][8];
+    float scale[R];
+#pragma unroll
+    for (int m = 0; m < R; m++) scale[m] = 1.0f;
     if constexpr (full) {
         double part = 0.0;
 #pragma unroll
@@ -326,45 +351,55 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
         __syncthreads();
         double ss = 0.0;
         for (int i = 0; i < nw; i++) ss += ssq[i];
-        scale = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
+        scale[0] = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
 #pragma unroll
         for (int t = 0; t < XP; t++) {
             if (4 * t >= gs) continue;
             const int g = 4 * t + kg < gs ? g0 + 4 * t + kg : g0;
             const u32x4_t a = reinterpret_cast<const u32x4_t*>(xraw + g * kGroup + ln * 8)[0];
             const u32x4_t c = reinterpret_cast<const u32x4_t*>(xraw + g * kGroup + ln * 8)[1];
-            xw[t][0] = a;
-            xw[t][1] = c;
+            xw[0][t][0] = a;
+            xw[0][t][1] = c;
         }
     } else if constexpr (norm) {
-        double part = 0.0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) part += double(__uint_as_float(xc[0][j]));
-        const double ss = wave_sum(part);
-        scale = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
+        for (int m = 0; m < R; m++) {
+            double part = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                part += (R == 1 || 4 * lane + j < st.ssq_n) ? double(__uint_as_float(xc[m][j])) : 0.0;
+            const double ss = wave_sum(part);
+            scale[m] = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
+        }
     }
 #pragma unroll
-    for (int t = 0; t < XP; t++)
+    for (int m = 0; m < R; m++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float r = __uint_as_float(xw[t][i >> 2][i & 3]);
-            if constexpr (norm) {
-                const uint32_t nv = nwv[t][i >> 1];
-                const float wn = __uint_as_float((i & 1) ? (nv & 0xFFFF0000u) : (nv << 16));
-                xv[t][i] = (r * scale) * wn;
-            } else {
-                xv[t][i] = r;
+        for (int t = 0; t < XP; t++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float r = __uint_as_float(xw[m][t][i >> 2][i & 3]);
+                if constexpr (norm) {
+                    const uint32_t nv = nwv[t][i >> 1];
+                    const float wn = __uint_as_float((i & 1) ? (nv & 0xFFFF0000u) : (nv << 16));
+                    xv[m][t][i] = (r * scale[m]) * wn;
+                } else {
+                    xv[m][t][i] = r;
+                }
             }
-        }
 
-    // 3. This wave's slice into limb records.
+    // 3. This wave's slice into limb records (row m: records m * G + g).
 #pragma unroll
-    for (int t = 0; t < XP; t++) {
-        if (4 * t >= gs) continue;  // wave-uniform
-        const int g = g0 + 4 * t + kg;
-        const bool ok = 4 * t + kg < gs;
-        const int4 md = convert_group<KIND == 1>(xv[t], ln, ok, lds + (ok ? g : g0) * kLimbRec);
-        if (ok && ln == 0) ms[g] = md;
+    for (int m = 0; m < R; m++) {
+        if (m >= M) break;  // uniform
+#pragma unroll
+        for (int t = 0; t < XP; t++) {
+            if (4 * t >= gs) continue;  // wave-uniform
+            const int g = g0 + 4 * t + kg;
+            const bool ok = 4 * t + kg < gs;
+            const int4 md = convert_group<KIND == 1>(xv[m][t], ln, ok, lds + (m * G + (ok ? g : g0)) * kLimbRec);
+            if (ok && ln == 0) ms[m * G + g] = md;
+        }
     }
 
     // 4. Codes x limbs: A rows 0..3 = limbs 0..3 (lanes 0..15 hold the four
@@ -375,18 +410,22 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     float acc[TP];
 #pragma unroll
     for (int t = 0; t < TP; t++) acc[t] = 0.0f;
-    const bool alive = ln < kLimbs;
+    // A row of this lane: limb ln (R = 1) or limb ln % 4 of activation row
+    // ln / 4 (R > 1); D lane group kg holds activation row kg's sums (R > 1)
+    const int am = R == 1 ? 0 : ln >> 2, aL = R == 1 ? ln : ln & 3;
+    const bool alive = R == 1 ? ln < kLimbs : am < M;
+    const int mrow = R == 1 ? 0 : (kg < M ? kg : 0);
 #pragma unroll
     for (int gl = 0; gl < NG; gl++) {
         if (gl >= gs) continue;  // wave-uniform
         const int g = g0 + gl;
         int4v_t a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
         if (alive) {
-            const int8_t* pa = lds + g * kLimbRec + ln * kGroup + kg * 16;
+            const int8_t* pa = lds + (am * G + g) * kLimbRec + aL * kGroup + kg * 16;
             a0 = *reinterpret_cast<const int4v_t*>(pa);
             a1 = *reinterpret_cast<const int4v_t*>(pa + 64);
         }
-        const int4 md = ms[g];
+        const int4 md = ms[mrow * G + g];
 #pragma unroll
         for (int t = 0; t < TP; t++) {
             int4v_t b0, b1;
@@ -411,19 +450,20 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     // 5. Partials through LDS; the last wave adds them in wave order and
     //    applies the epilogue (and the per-tile sum of squares of the output
     //    for a consumer's RMSNorm).
-    if (lane < 16) {
+    //    (R > 1: lane group m = activation row m.)
+    if (lane < 16 * R) {
 #pragma unroll
-        for (int t = 0; t < TP; t++) red[wave][t][ln] = acc[t];
+        for (int t = 0; t < TP; t++) red[wave][t][lane] = acc[t];
     }
     int prior = 0;
     if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
     prior = __builtin_amdgcn_readfirstlane(prior);
-    if (prior != nw - 1 || lane >= 16) return;
+    if (prior != nw - 1 || lane >= 16 * M) return;
     float sum[TP];
 #pragma unroll
     for (int t = 0; t < TP; t++) {
         sum[t] = 0.0f;
-        for (int i = 0; i < nw; i++) sum[t] += red[i][t][ln];
+        for (int i = 0; i < nw; i++) sum[t] += red[i][t][lane];
     }
     const int64_t row = row0 + ln;
     float v = sum[0] + __uint_as_float(addb[0] << 16);
@@ -434,10 +474,11 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
     } else if (st.out_op == IQ_OUT_RESIDUAL) {
         v = __uint_as_float(resb) + v;
     }
-    if (row < N) Ms[0].y[row] = v;
+    if (row < N) Ms[0].y[int64_t(kg) * N + row] = v;
     if (st.ssq_out) {
+        // (the 16 lanes of row kg together: M is a whole number of groups)
         const float sq = row16_fsum(row < N ? v * v : 0.0f);
-        if (ln == 0) st.ssq_out[tile] = sq;
+        if (ln == 0) st.ssq_out[R == 1 ? tile : kg * ((N + 15) / 16) + tile] = sq;
     }
 }
 
@@ -518,18 +559,33 @@ template <int KIND>
 hipError_t launch_stage_k(const HostStage& h, hipStream_t stream) {
     const dim3 grid(unsigned(h.st.units)), block(unsigned(64 * h.st.ks));
     const int norm = h.st.in_op != IQ_IN_RMSNORM ? 0 : (h.st.ssq_in ? 1 : 2);
-#define IQ_STAGE1(NG_, TP_, N_)                                                             \
+#define IQ_STAGE1(NG_, TP_, N_, R_)                                                         \
     do {                                                                                    \
-        allow_big_lds<stage_kernel<KIND, NG_, TP_, N_>>();                                  \
-        stage_kernel<KIND, NG_, TP_, N_><<<grid, block, h.lds, stream>>>(h.st);             \
+        allow_big_lds<stage_kernel<KIND, NG_, TP_, N_, R_>>();                              \
+        stage_kernel<KIND, NG_, TP_, N_, R_><<<grid, block, h.lds, stream>>>(h.st);         \
     } while (0)
 #define IQ_STAGE(NG_, TP_)                                                                  \
     do {                                                                                    \
-        if (norm == 1) IQ_STAGE1(NG_, TP_, 1);                                              \
-        else if (norm == 2) IQ_STAGE1(NG_, TP_, 2);                                         \
-        else IQ_STAGE1(NG_, TP_, 0);                                                        \
+        if (norm == 1) IQ_STAGE1(NG_, TP_, 1, 1);                                           \
+        else if (norm == 2) IQ_STAGE1(NG_, TP_, 2, 1);                                      \
+        else IQ_STAGE1(NG_, TP_, 0, 1);                                                     \
     } while (0)
-    if (h.st.tpu == 2) {
+#define IQ_STAGER(TP_, R_)                                                                  \
+    do {                                                                                    \
+        if (norm == 1) IQ_STAGE1(4, TP_, 1, R_);                                            \
+        else IQ_STAGE1(4, TP_, 0, R_);                                                      \
+    } while (0)
+    if (h.fused_r > 1) {
+        // (norm == 2 never reaches an R-row stage: chain_create gives its
+        // input per-row sums of squares)
+        if (h.fused_r == 2) {
+            if (h.st.tpu == 2) IQ_STAGER(2, 2);
+            else IQ_STAGER(1, 2);
+        } else {
+            if (h.st.tpu == 2) IQ_STAGER(2, 4);
+            else IQ_STAGER(1, 4);
+        }
+    } else if (h.st.tpu == 2) {
         if (h.ng == 4) IQ_STAGE(4, 2);
         else IQ_STAGE(8, 2);
     } else {
@@ -544,6 +600,7 @@ hipError_t launch_stage_k(const HostStage& h, hipStream_t stream) {
     }
 #undef IQ_STAGE
 #undef IQ_STAGE1
+#undef IQ_STAGER
     return hipGetLastError();
 }
 
@@ -651,6 +708,24 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         c.tpu = pair ? 2 : 1;
         c.units = pair ? int((W0.rows + 15) / 16) : tiles;
         hs.kind = W0.kind;
+        const bool i4 = W0.kind == IQ_INT4;
+        const int maxw = i4 ? kMaxWaves : kMaxWaves / 2;
+        if (rows > 1 && rows <= 4 && G <= int64_t(4) * maxw &&
+            size_t(rows <= 2 ? 2 : 4) * size_t(G) * (kLimbRec + 16) <= 160 * 1024) {
+            // 2..4 rows on short rows: one fused launch (the R-row
+            // stage_kernel: 4-group slices, the limbs of every row in LDS)
+            hs.fused_r = rows <= 2 ? 2 : 4;
+            hs.rows = rows;
+            c.rows = rows;
+            c.gs = 4;
+            c.ks = int((G + 3) / 4);
+            hs.ng = 4;
+            hs.lds = size_t(hs.fused_r) * size_t(G) * (kLimbRec + 16);
+            hs.in.x = a.x;
+            hs.in.xstride = xlen;
+            hs.W[0] = QView{W0.kind, W0.rows, W0.cols, W0.groups, W0.q, W0.scales, nullptr};
+            continue;
+        }
         if (rows > 1) {
             // B rows: the rows GEMV (gemvr / gemvq with the input transform)
             // and epi_kernel
@@ -685,8 +760,6 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         // more waves with 2 groups each), at most 16 waves of <= 12 groups
         // (int4) or 8 waves of <= 20 groups (int8: twice the weight
         // registers per group); a SwiGLU pair holds two tiles per wave
-        const bool i4 = W0.kind == IQ_INT4;
-        const int maxw = i4 ? kMaxWaves : kMaxWaves / 2;
         int gs = int((G + maxw - 1) / maxw);
         gs = (gs + 3) & ~3;
         if (gs > (pair ? 8 : (i4 ? 12 : 20))) return IQ_ETOOLARGE;
@@ -756,25 +829,32 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
             }
         }
     }
-    // B rows: per-row sums of squares of 256-column blocks, written by the
-    // producer's epi_kernel or by ssq_kernel (RMSNorm inputs no stage of
-    // the chain produces); one K-range partial-sum buffer for all stages
+    // B rows: per-row sums of squares of an RMSNorm input, written by the
+    // stage that produced it (a B-row epi_kernel: one per 256-column block;
+    // an R-row stage_kernel: one per 16-row output tile) or by ssq_kernel
+    // (inputs no stage of the chain produces: one per 256-column block), at
+    // most 256 per row; one K-range partial-sum buffer for all B-row GEMVs
     {
         std::vector<size_t> off(static_cast<size_t>(n), size_t(-1));  // by producer / own consumer
         std::vector<int> producer(static_cast<size_t>(n), -1);
+        auto ssq_count = [&](int e) {
+            const HostStage& hp = prog[size_t(e)];
+            return hp.fused_r > 1 ? int((hp.st.mat[0].N + 15) / 16) : int((hp.epi.ncols + 255) / 256);
+        };
         for (const auto& l : links)
-            if (rows_of(l.second) > 1) producer[size_t(l.second)] = l.first;
+            if (rows_of(l.second) > 1 && ssq_count(l.first) <= 256) producer[size_t(l.second)] = l.first;
         size_t total = 0;
         int64_t part = 0;
         for (int s = 0; s < n; s++) {
             HostStage& h = prog[size_t(s)];
             if (h.rows == 1) continue;
-            part = std::max<int64_t>(part, chain_rows_partials(h.W, h.st.nmat, h.rows, kStreamPartialFloats));
+            if (h.fused_r == 1)
+                part = std::max<int64_t>(part, chain_rows_partials(h.W, h.st.nmat, h.rows, kStreamPartialFloats));
             if (stages[s].in_op != IQ_IN_RMSNORM) continue;
             const int pe = producer[size_t(s)];
             const int key = pe >= 0 ? pe : s;
             const int64_t K = h.W[0].cols;
-            const int ssq_n = pe >= 0 ? int((prog[size_t(pe)].epi.ncols + 255) / 256) : int((K + 255) / 256);
+            const int ssq_n = pe >= 0 ? ssq_count(pe) : int((K + 255) / 256);
             if (off[size_t(key)] == size_t(-1)) {
                 off[size_t(key)] = total;
                 total += size_t(h.rows) * size_t(ssq_n);
@@ -792,9 +872,18 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
                 float* p = ch->rssq + off[size_t(pe >= 0 ? pe : s)];
                 h.ssq = p;
                 h.in.ssq = p;
+                if (h.fused_r > 1) {
+                    h.st.ssq_in = p;
+                    h.st.ssq_n = h.in.ssq_n;
+                }
                 if (pe >= 0) {
-                    prog[size_t(pe)].epi.ssq_out = p;
-                    prog[size_t(pe)].epi.ssq_n = h.in.ssq_n;
+                    HostStage& hp = prog[size_t(pe)];
+                    if (hp.fused_r > 1) {
+                        hp.st.ssq_out = p;
+                    } else {
+                        hp.epi.ssq_out = p;
+                        hp.epi.ssq_n = h.in.ssq_n;
+                    }
                 }
             }
         }
@@ -811,8 +900,17 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
 
 hipError_t chain_run(const Chain* ch, hipStream_t stream) {
     for (const HostStage& h : ch->stages) {
-        const hipError_t e = h.rows > 1 ? run_rows_stage(h, ch->rpart, ch->rpart_floats, stream)
-                                        : (h.kind == IQ_INT4 ? launch_stage_k<1>(h, stream) : launch_stage_k<0>(h, stream));
+        hipError_t e;
+        if (h.rows > 1 && h.fused_r == 1) {
+            e = run_rows_stage(h, ch->rpart, ch->rpart_floats, stream);
+        } else {
+            if (h.own_ssq) {
+                // (an R-row stage whose RMSNorm input no stage produced)
+                ssq_kernel<<<dim3(unsigned(h.in.ssq_n), unsigned(h.rows)), 256, 0, stream>>>(
+                    h.in.x, int(h.W[0].cols), h.in.ssq_n, h.ssq);
+            }
+            e = h.kind == IQ_INT4 ? launch_stage_k<1>(h, stream) : launch_stage_k<0>(h, stream);
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

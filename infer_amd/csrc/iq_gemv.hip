@@ -154,32 +154,32 @@ __device__ __forceinline__ uint32_t pro_x_offset(const GemvParams& p, int m, int
 }
 
 // The RMSNorm row factors r_m of a PRO launch into rsc[0 .. M): step 1
-// requests this thread's partial sums of squares (thread t: row t / 8,
-// partials t % 8, t % 8 + 8, ...; issued before anything else), step 2
-// adds them in a fixed order (double) once they land.
+// requests this thread's partial sums of squares (thread t: row t / 16,
+// partials t % 16, t % 16 + 16, ... of at most 256; issued before anything
+// else), step 2 adds them in a fixed order (double) once they land.
 struct ProScale {
-    float sq[8];
+    float sq[16];
     __device__ __forceinline__ void request(const GemvParams& p, int tid) {
         const rsrc_t r = make_rsrc(p.ssq, p.norm ? int64_t(p.M) * p.ssq_n * 4 : 0);
-        const int m = tid >> 3, j = tid & 7;
+        const int m = tid >> 4, j = tid & 15;
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int b = j + 8 * k;
+        for (int k = 0; k < 16; k++) {
+            const int b = j + 16 * k;
             sq[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                   r, (m < p.M && b < p.ssq_n) ? uint32_t(m * p.ssq_n + b) * 4 : kOob, 0, 0));
         }
     }
     // every thread of the workgroup calls this (two barriers)
-    __device__ __forceinline__ void finish(const GemvParams& p, int tid, double (*part)[8], float* rsc) {
+    __device__ __forceinline__ void finish(const GemvParams& p, int tid, double (*part)[16], float* rsc) {
         double v = 0.0;
 #pragma unroll
-        for (int k = 0; k < 8; k++) v += double(sq[k]);
-        if (tid < 256) part[tid >> 3][tid & 7] = v;
+        for (int k = 0; k < 16; k++) v += double(sq[k]);
+        part[tid >> 4][tid & 15] = v;
         __syncthreads();
         if (tid < p.M) {
             double ss = 0.0;
 #pragma unroll
-            for (int j = 0; j < 8; j++) ss += part[tid][j];
+            for (int j = 0; j < 16; j++) ss += part[tid][j];
             rsc[tid] = 1.0f / __builtin_sqrtf(float(ss / double(p.K)) + p.eps);
         }
         __syncthreads();
@@ -1740,7 +1740,7 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
     }
     // 2. the operands and factors of the range (all 16 lanes of each
     //    (row, group) together), then one barrier
-    __shared__ double rsp[PRO ? kMaxRowsGemv : 1][8];
+    __shared__ double rsp[PRO ? kMaxRowsGemv : 1][16];
     __shared__ float rsc[PRO ? kMaxRowsGemv : 1];
     if constexpr (PRO) {
         if (p.norm) psc.finish(p, tid, rsp, rsc);  // workgroup-uniform
@@ -1880,7 +1880,7 @@ __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     const uint32_t vq = uint32_t(l32 * row_bytes + h * NW * 16);
     const uint32_t vs = uint32_t(l32 * G) * 2, vz = uint32_t(l32 * G);
 
-    __shared__ double rsp[PRO ? kMaxRowsGemv : 1][8];
+    __shared__ double rsp[PRO ? kMaxRowsGemv : 1][16];
     __shared__ float rsc[PRO ? kMaxRowsGemv : 1];
     float acc[MB][8];
 #pragma unroll

@@ -228,12 +228,13 @@ class RowView:
         self.logits = row(step.logits)
 
 
-@pytest.mark.parametrize("B", [2, 4, 16, 32])
+@pytest.mark.parametrize("B", [2, 3, 4, 16, 32])
 @pytest.mark.parametrize("kind,head_kind", [(1, 0), (0, 0)])
 def test_chain_rows_small_model_matches_forward(B, kind, head_kind):
-    """B sequences of one token each through the B-row stages: every stage of
-    every row against the oracle on the chain's own inputs, and every row's
-    logits against the float64 forward of its token."""
+    """B sequences of one token each: 2..4 rows on the fused R-row stages
+    (one launch per stage), more on the B-row stages (rows GEMV + epilogue);
+    every stage of every row against the oracle on the chain's own inputs,
+    and every row's logits against the float64 forward of its token."""
     rng = np.random.default_rng(100 + B + 3 * kind + head_kind)
     host, dev = make_model(rng, H=512, I=1536, nh=4, nkv=2, hd=128, V=1000, L=3, kind=kind, head_kind=head_kind)
     tokens = [int(t) for t in rng.integers(0, 1000, B)]
@@ -256,11 +257,12 @@ def test_chain_rows_small_model_matches_forward(B, kind, head_kind):
     assert torch.equal(first, step.logits)
 
 
-@pytest.mark.parametrize("B", [16, 32])
+@pytest.mark.parametrize("B", [3, 4, 16, 32])
 def test_chain_rows_7b_shapes_sampled(B):
-    """The 7B program (28 int4 layers, int8 lm_head) at B rows: gate|up on
-    the 32-row tile kernel, stage by stage on sampled output rows of a few
-    layers and sequences."""
+    """The 7B program (28 int4 layers, int8 lm_head) at B rows: at 3 / 4 rows
+    q|k|v, o, gate|up and the head on fused R-row stages and down (K = 18944)
+    on the B-row stages; at 16 / 32 gate|up on the 32-row tile kernel; stage
+    by stage on sampled output rows of a few layers and sequences."""
     rng = np.random.default_rng(70 + B)
     host, dev = make_model(rng, H=3584, I=18944, nh=28, nkv=4, hd=128, V=152064, L=28, kind=1, head_kind=0,
                            quantize=False)
