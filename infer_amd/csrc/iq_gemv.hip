@@ -267,8 +267,12 @@ __device__ __forceinline__ void load_meta(Slice<KIND, NG>& b, const GemvParams& 
     const rsrc_t rs = make_rsrc(mr.scales, mr.N * G * 2);
     const rsrc_t rz = make_rsrc(mr.zeros, KIND == 1 ? mr.N * G : 0);
     const int64_t rcs = MODE == 0 ? (row < mr.N ? row : mr.N - 1) : row;
-    const uint32_t vs = uint32_t((rcs * G + gbeg) * 2);
-    const uint32_t vz = uint32_t(rcs * G + gbeg);
+    // (a 24-bit multiply, rows and G < 2^24: the compiler's 64-bit
+    // multiply-add for a 32-bit product read an undefined high half from a
+    // register that a pending load writes, and so waited for every earlier
+    // load before these requests)
+    const uint32_t vz = __umul24(uint32_t(rcs), uint32_t(G)) + uint32_t(gbeg);
+    const uint32_t vs = vz * 2u;
     if (MODE == 2) {
 #pragma unroll
         for (int q4 = 0; q4 < NG / 4; q4++) {
@@ -452,14 +456,17 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     //    (32 G bytes) and of its zero-point block (16 G bytes; rows past N
     //    read zero); otherwise each wave its own slice's.  Then every wave's
     //    weights, and the conversion while they stream in.
+    //    The staged loads are unconditional (not staged, or threads past
+    //    the block: an empty range, reading zero): under a branch the
+    //    compiler waited for every earlier load before the weights went out.
     int4v_t mv_s = {0, 0, 0, 0}, mv_z = {0, 0, 0, 0};
     const int64_t trows = ts.m.N - ts.row0 < 16 ? ts.m.N - ts.row0 : 16;
-    if (staged && wave * 64 < 2 * G) {
-        const rsrc_t rs = make_rsrc(ts.m.scales + ts.row0 * G, trows * G * 2);
+    if constexpr (MODE == 2) {
+        const rsrc_t rs = make_rsrc(ts.m.scales + ts.row0 * G, staged ? trows * G * 2 : 0);
         mv_s = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                rs, tid < 2 * G ? uint32_t(tid) * 16 : kOob, 0, 0));
-        if (KIND == 1 && wave * 64 < G) {
-            const rsrc_t rz = make_rsrc(ts.m.zeros + ts.row0 * G, trows * G);
+        if (KIND == 1) {
+            const rsrc_t rz = make_rsrc(ts.m.zeros + ts.row0 * G, staged ? trows * G : 0);
             mv_z = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                    rz, tid < G ? uint32_t(tid) * 16 : kOob, 0, 0));
         }
