@@ -67,10 +67,13 @@ __device__ __forceinline__ void dq_int4_x8(uint32_t v, uint32_t zb, uint32_t zc,
                                            uint32_t& o1, uint32_t& o2, uint32_t& o3) {
     const half2_t sixteenth = as_h2(0x2C002C00u);  // 1/16, 1/16
     const uint32_t v8 = v >> 8;
-    const uint32_t a0 = (v & 0x000F000Fu) | 0x64006400u;   // 1024+n0, 1024+n4
-    const uint32_t a1 = (v & 0x00F000F0u) | 0x64006400u;   // 1024+16n1, 1024+16n5
-    const uint32_t a2 = (v8 & 0x000F000Fu) | 0x64006400u;  // 1024+n2, 1024+n6
-    const uint32_t a3 = (v8 & 0x00F000F0u) | 0x64006400u;  // 1024+16n3, 1024+16n7
+    // (m & mask) | 0x6400 in each half: one v_bitop3_b32 each (truth table
+    // 0xEA = (src0 & src1) | src2); written as & then | the compiler emits
+    // two instructions, since one instruction takes at most one literal
+    const uint32_t a0 = __builtin_amdgcn_bitop3_b32(v, 0x000F000Fu, 0x64006400u, 0xEA);   // 1024+n0, 1024+n4
+    const uint32_t a1 = __builtin_amdgcn_bitop3_b32(v, 0x00F000F0u, 0x64006400u, 0xEA);   // 1024+16n1, 1024+16n5
+    const uint32_t a2 = __builtin_amdgcn_bitop3_b32(v8, 0x000F000Fu, 0x64006400u, 0xEA);  // 1024+n2, 1024+n6
+    const uint32_t a3 = __builtin_amdgcn_bitop3_b32(v8, 0x00F000F0u, 0x64006400u, 0xEA);  // 1024+16n3, 1024+16n7
     o0 = h2_bits(as_h2(a0) + as_h2(zb));
     o1 = h2_bits(__builtin_elementwise_fma(as_h2(a1), sixteenth, as_h2(zc)));
     o2 = h2_bits(as_h2(a2) + as_h2(zb));

@@ -1335,25 +1335,42 @@ constexpr int kHGroupBytes = 4 * 2 * 64 * 16;  // prepared bytes per (block, gro
 // weights); fac: 2^-k, or NaN when the group holds a non-finite value.
 template <bool PERM>
 __device__ __forceinline__ void xh_split8(const float (&v)[8], half8_t& ho, half8_t& lo, float& fac) {
-    uint32_t am = 0, nf = 0;
+    // largest |x| bits over the 16 lanes; a NaN or an infinity has larger
+    // bits (>= 0x7F800000) than any finite value, so one test of the
+    // maximum finds any of them
+    uint32_t am = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const uint32_t a = __float_as_uint(v[i]) & 0x7FFFFFFFu;
-        nf |= a >= 0x7F800000u ? 1u : 0u;
         am = a > am ? a : am;
     }
-    am = row16_max_u32(nf ? 0u : am);
-    const bool fin = row16_or(nf) == 0;
+    am = row16_max_u32(am);
+    const bool fin = am < 0x7F800000u;
     // amax = f 2^E, f in [0.5, 1): k = 15 - E puts amax 2^k in [2^14, 2^15)
     const int k = (am > 0 && fin) ? 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(am)) : 0;
+    // operand dword j: values (j, j + 4) with PERM, else (2j, 2j + 1).
+    // (A group with a non-finite value keeps its values: fac is NaN, so its
+    // row's outputs are NaN whatever the operand holds, and an MFMA output
+    // row reads only its own operand row.)
+    u32x4_t hw, lw;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float s = fin ? __builtin_amdgcn_ldexpf(v[e], k) : 0.0f;
-        const _Float16 h = _Float16(s);
-        const int slot = PERM ? 2 * (e & 3) + (e >> 2) : e;
-        ho[slot] = h;
-        lo[slot] = _Float16(s - float(h));
+    for (int j = 0; j < 4; j++) {
+        const int e0 = PERM ? j : 2 * j, e1 = PERM ? j + 4 : 2 * j + 1;
+        const float s0 = __builtin_amdgcn_ldexpf(v[e0], k);
+        const float s1 = __builtin_amdgcn_ldexpf(v[e1], k);
+        half2_t h, l;
+        h[0] = _Float16(s0);
+        h[1] = _Float16(s1);
+        const uint32_t hb = h2_bits(h);
+        const float b0 = float(__builtin_bit_cast(_Float16, uint16_t(hb)));
+        const float b1 = float(__builtin_bit_cast(_Float16, uint16_t(hb >> 16)));
+        l[0] = _Float16(s0 - b0);
+        l[1] = _Float16(s1 - b1);
+        hw[j] = hb;
+        lw[j] = h2_bits(l);
     }
+    ho = __builtin_bit_cast(half8_t, hw);
+    lo = __builtin_bit_cast(half8_t, lw);
     fac = fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
 }
 
@@ -2397,7 +2414,16 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // 1-row kernel's 4-row instance splits over K ranges: 7B down 3584 x
     // 18944 int8 at 3 / 4 rows 27.3 / 30.6 -> 24.1 / 24.2 us, int4 at 4 rows
     // 22.1 -> 20.8; int4 at 2 / 3 rows 17.8 / 19.9 against 20.4 / 20.5)
-    const int m_lo = G >= 128 ? (W[0].kind == 0 ? 3 : 4) : 5;
+    // ... and, since the cheaper int4 dequantisation and activation split,
+    // from 4 rows on wide int4 calls and very wide calls of either kind
+    // (7B at 4 rows: int4 gate|up 32.5 -> 27.3, lm_head int4 137 -> 118,
+    // int8 138 -> 127 us; int4 step 1922 -> 1825 us; the 4-row instance's
+    // limb records of 4 rows hold a CU to two workgroups); at 3 rows the
+    // step measured the same either way, at 2 the 4-row instance is far
+    // ahead
+    const int tiles_all = total_tiles(W, n);
+    int m_lo = G >= 128 ? (W[0].kind == 0 ? 3 : 4) : 5;
+    if (tiles_all >= 4096 || (W[0].kind == 1 && tiles_all >= 1024)) m_lo = m_lo < 4 ? m_lo : 4;
     if (M >= m_lo && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
         hipError_t e = hipSuccess;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;
