@@ -396,17 +396,19 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // instead of every wave fetching the same lines for its slice.  The slice partials are added
 // through LDS by whichever wave finishes last (an LDS counter), in slice
 // order, so the sum is deterministic and no wave waits for the others.
-template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT>
+template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT, bool HALF = false>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // dynamic LDS: limbs [RR][G][512], meta [R][G] int4, then (staged) the
-    // tile's scales [16][G] bf16 and zero points [16][G] u8.  R = 8 runs
-    // two blocks of 4 rows through the same limb records (each wave reuses
-    // its own groups' records; the weights stay in registers).
-    constexpr int RR = R < 4 ? R : 4;  // rows per block
-    constexpr int RB = R / RR;         // blocks
+    // tile's scales [16][G] bf16 and zero points [16][G] u8.  R = 8, and R =
+    // 4 with HALF, run two blocks of R / 2 rows through the same limb
+    // records (each wave reuses its own groups' records; the weights stay
+    // in registers): half the LDS of one block of R rows.
+    static_assert(!HALF || (R == 4 && !KSPLIT), "two 2-row blocks: the 4-row instance, one K range");
+    constexpr int RR = HALF ? R / 2 : (R < 4 ? R : 4);  // rows per block
+    constexpr int RB = R / RR;                          // blocks
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
-    __shared__ float red[MAXW][16 * R];
+    __shared__ float red[MAXW][RB][16 * RR];
     __shared__ int arrived;
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
     const int KS = int(blockDim.x) >> 6;
@@ -512,14 +514,16 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
 
     // 3. The slice as it lands; partials through LDS, the last wave to
     //    arrive adds them in slice order (rows k >= KS were never written).
-    float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, RS, glo, M, gbeg, gs, ln, kg);
-    if (lane < 16 * RR) red[wave][lane] = acc;
+    float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, RS, glo, M < RR ? M : RR, gbeg, gs, ln, kg);
+    if (lane < 16 * RR) red[wave][0][lane] = acc;
     if constexpr (RB == 2) {
-        // rows 4..7: the wave overwrites its own records (its reads of them
-        // above come first in program order)
-        convert_rows(4);
-        acc = slice_dot<KIND, NG, RR>(b, xs1, ms1 + 4 * RS, xzero, RS, glo, M - 4, gbeg, gs, ln, kg);
-        red[wave][64 + lane] = acc;
+        // rows RR..2 RR - 1: the wave overwrites its own records (its reads
+        // of them above come first in program order)
+        if (M > RR) {  // uniform
+            convert_rows(RR);
+            acc = slice_dot<KIND, NG, RR>(b, xs1, ms1 + RR * RS, xzero, RS, glo, M - RR, gbeg, gs, ln, kg);
+            if (lane < 16 * RR) red[wave][1][lane] = acc;
+        }
     }
     int prior = 0;
     if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -527,12 +531,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     if (prior != KS - 1) return;
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-        const int m = 4 * rb + kg;  // lane group kg of block rb: row m
-        if (m >= M) break;
-        float sum = red[0][64 * rb + lane];
+        const int m = RR * rb + kg;  // lane group kg < RR of block rb: row m
+        if (kg >= RR || m >= M) break;
+        float sum = red[0][rb][lane];
 #pragma unroll
         for (int k = 1; k < MAXW; k++) {
-            const float v = red[k][64 * rb + lane];
+            const float v = red[k][rb][lane];
             sum += k < KS ? v : 0.0f;
         }
         if (ts.row0 + ln >= ts.m.N) continue;
@@ -983,7 +987,10 @@ int gemv1_mode(int64_t K, int64_t G, const float* x) {
 // 1505 us (gate|up 25.5 -> 20.5, down 19.9 -> 18.0, lm_head int8 107.5 ->
 // 94.7 us).
 int gemv1_rows(int M) { return M > 4 ? 8 : (M > 2 ? 4 : M); }
-size_t gemv1_lds(int64_t G, int R) { return size_t(G) * ((R < 4 ? R : 4) * kLimbRec + R * 16); }
+// (half: the 4-row instance's two blocks of 2 rows)
+size_t gemv1_lds(int64_t G, int R, bool half = false) {
+    return size_t(G) * ((half ? R / 2 : (R < 4 ? R : 4)) * kLimbRec + R * 16);
+}
 
 // 1..4 rows always; 5..8 rows (two blocks of 4, the second converted after
 // the first is multiplied) only on narrow launches, measured at 7B: o (224
@@ -1053,12 +1060,14 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
 }
 
 template <int KIND, int NG, int MAXW>
-void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream) {
-#define IQ_G1(MODE_, R_, KSPLIT_)                                                                  \
+void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream,
+                    bool half = false) {
+#define IQ_G1H(MODE_, R_, KSPLIT_, HALF_)                                                          \
     do {                                                                                           \
-        allow_big_lds<gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_>>();                         \
-        gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_><<<grid, 64 * ks, lds, stream>>>(p);       \
+        allow_big_lds<gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_, HALF_>>();                  \
+        gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_, HALF_><<<grid, 64 * ks, lds, stream>>>(p); \
     } while (0)
+#define IQ_G1(MODE_, R_, KSPLIT_) IQ_G1H(MODE_, R_, KSPLIT_, false)
     if (p.M > 4) {
         if constexpr (NG <= 4) IQ_G1(2, 8, false);
         return;
@@ -1077,7 +1086,12 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
     }
     if (p.M > 1) {
         if constexpr (NG <= (KIND == 1 ? 4 : 8)) {
-            if (mode == 2) {
+            if (KIND == 0 && half) {
+                if constexpr (KIND == 0) {  // (int8 only)
+                    if (mode == 2) IQ_G1H(2, 4, false, true);
+                    else IQ_G1H(1, 4, false, true);
+                }
+            } else if (mode == 2) {
                 if (p.kr > 1) IQ_G1(2, 4, true);
                 else IQ_G1(2, 4, false);
             } else {
@@ -1091,6 +1105,7 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
     else if (mode == 1) IQ_G1(1, 1, false);
     else IQ_G1(0, 1, false);
 #undef IQ_G1
+#undef IQ_G1H
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
@@ -1114,7 +1129,14 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     p.kr = pl.kr;
     p.gr = pl.gr;
     p.part = part;
-    size_t lds = gemv1_lds(pl.gr, gemv1_rows(M));
+    // int8, 3..4 rows on wide launches (at least 4 workgroups per CU), one
+    // K range: two blocks of 2 rows through the limb records of 2 rows (7B
+    // int8 at 3 rows: gate|up 33.2 -> 32.2, lm_head 130 -> 124.5 us, step
+    // 2091 -> 2060 us; at 4 rows 2192 -> 2175 us).  Not int4 (gate|up at
+    // 3 rows 28.0 -> 32.5 us): the instance's 82 VGPRs hold a CU to two
+    // workgroups either way, and the second block's pass is then extra.
+    const bool half = W[0].kind == 0 && gemv1_rows(M) == 4 && pl.kr == 1 && tiles >= 4 * device_cu_count();
+    size_t lds = gemv1_lds(pl.gr, gemv1_rows(M), half);
     // Staged scales / zero points on wide launches (7B int4 gate|up 16.9 ->
     // 15.9 us); narrow ones (under 4 workgroups per CU) lose more to the
     // extra barrier than they save (o 4.8 -> 5.1 us).  Not where the 48 G
@@ -1130,14 +1152,14 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
     }
     const unsigned grid = unsigned(pl.grid);
     if (W[0].kind == 1) {
-        if (pl.ng == 4) launch_gemv1_m<1, 4, 16>(p, mode, pl.ks, grid, lds, stream);
-        else if (pl.ng == 8) launch_gemv1_m<1, 8, 16>(p, mode, pl.ks, grid, lds, stream);
-        else launch_gemv1_m<1, 12, 16>(p, mode, pl.ks, grid, lds, stream);
+        if (pl.ng == 4) launch_gemv1_m<1, 4, 16>(p, mode, pl.ks, grid, lds, stream, half);
+        else if (pl.ng == 8) launch_gemv1_m<1, 8, 16>(p, mode, pl.ks, grid, lds, stream, half);
+        else launch_gemv1_m<1, 12, 16>(p, mode, pl.ks, grid, lds, stream, half);
     } else {
-        if (pl.ng == 4) launch_gemv1_m<0, 4, 8>(p, mode, pl.ks, grid, lds, stream);
-        else if (pl.ng == 8) launch_gemv1_m<0, 8, 8>(p, mode, pl.ks, grid, lds, stream);
-        else if (pl.ng == 12) launch_gemv1_m<0, 12, 8>(p, mode, pl.ks, grid, lds, stream);
-        else launch_gemv1_m<0, 20, 8>(p, mode, pl.ks, grid, lds, stream);
+        if (pl.ng == 4) launch_gemv1_m<0, 4, 8>(p, mode, pl.ks, grid, lds, stream, half);
+        else if (pl.ng == 8) launch_gemv1_m<0, 8, 8>(p, mode, pl.ks, grid, lds, stream, half);
+        else if (pl.ng == 12) launch_gemv1_m<0, 12, 8>(p, mode, pl.ks, grid, lds, stream, half);
+        else launch_gemv1_m<0, 20, 8>(p, mode, pl.ks, grid, lds, stream, half);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.kr == 1) return e;

@@ -137,7 +137,7 @@ def test_prefill_gemm_t1024_down(kind, xtype):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M", [1, 9, 12, 16])
+@pytest.mark.parametrize("M", [1, 3, 4, 9, 12, 16])
 def test_gate_up_7b_multi(kind, M):
     """gate|up of one 7B layer in one iq_gemv_multi call (2 x 18944 x 3584)."""
     rng = np.random.default_rng(900 + 20 * kind + M)
@@ -152,7 +152,7 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 5, 9, 16])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 9, 16])
 def test_lm_head_int8(M):
     """The int8 lm_head 152064 x 3584 (9504 tiles)."""
     rng = np.random.default_rng(152064 + M)
