@@ -1112,7 +1112,8 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
 // M = 1, or 2..8 rows (a plan made for gemv1_rows(M)) of x at stride K;
 // part: the split-K partials (plans with kr > 1).
 hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* bias, float* const* y, int n,
-                        const G1Plan& pl, int mode, hipStream_t stream, int M = 1, float* part = nullptr) {
+                        const G1Plan& pl, int mode, hipStream_t stream, int M = 1, float* part = nullptr,
+                        bool reduce = true) {
     const int64_t K = W[0].cols, G = W[0].groups;
     GemvParams p{};
     int tiles = 0;
@@ -1162,7 +1163,7 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         else launch_gemv1_m<0, 20, 8>(p, mode, pl.ks, grid, lds, stream, half);
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || pl.kr == 1) return e;
+    if (e != hipSuccess || pl.kr == 1 || !reduce) return e;
     // the K ranges' sums, in range order, + bias
     GemvParams pr = p;
     pr.S = pl.kr;
@@ -2432,10 +2433,11 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
         if (e != hipSuccess) return e;
         if (launch_gemvs(W, bias, y, n, M, ws, stream, &e)) return e;
     }
-    // (and from 3 / 4 rows, int8 / int4, on long rows, G >= 128, which the
-    // 1-row kernel's 4-row instance splits over K ranges: 7B down 3584 x
-    // 18944 int8 at 3 / 4 rows 27.3 / 30.6 -> 24.1 / 24.2 us, int4 at 4 rows
-    // 22.1 -> 20.8; int4 at 2 / 3 rows 17.8 / 19.9 against 20.4 / 20.5)
+    // (and from 3 rows on long rows, G >= 128, which the 1-row kernel's
+    // 4-row instance splits over K ranges: 7B down 3584 x 18944 int8 at 3 /
+    // 4 rows 27.3 / 30.6 -> 24.1 / 24.2 us, int4 at 3 / 4 rows 22.5 / 22.1
+    // -> 19.9 / 20.8 (int4 step at 3 rows 1807 -> 1761 us); at 2 rows the
+    // 2-row instance stays ahead, int4 17.8 against 19.4)
     // ... and, since the cheaper int4 dequantisation and activation split,
     // from 4 rows on wide int4 calls and very wide calls of either kind
     // (7B at 4 rows: int4 gate|up 32.5 -> 27.3, lm_head int4 137 -> 118,
@@ -2444,7 +2446,7 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     // step measured the same either way, at 2 the 4-row instance is far
     // ahead
     const int tiles_all = total_tiles(W, n);
-    int m_lo = G >= 128 ? (W[0].kind == 0 ? 3 : 4) : 5;
+    int m_lo = G >= 128 ? 3 : 5;
     if (tiles_all >= 4096 || (W[0].kind == 1 && tiles_all >= 1024)) m_lo = m_lo < 4 ? m_lo : 4;
     if (M >= m_lo && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
         hipError_t e = hipSuccess;
@@ -2595,6 +2597,23 @@ int64_t chain_rows_partials(const QView* W, int n, int M, int64_t cap) {
 
 hipError_t launch_chain_rows(const QView* W, int n, int M, const RowsIn& in, float* part, int64_t part_floats,
                              int* S, hipStream_t stream) {
+    // 2 rows of a plain input (no RMSNorm, no gather: the down stage) on
+    // long rows: the 1-row kernel's K-split 2-row instance, its range sums
+    // into `part` for the epilogue (7B int4 decode chain at 2 sequences
+    // 1629 -> 1529 us; at 3 / 4 the 4-row instance lost to gemvr, 1900 /
+    // 2031 -> 1908 / 2105 us)
+    if (M == 2 && !in.norm && in.gqa_hd == 0 && in.xstride == W[0].cols) {
+        const int64_t K = W[0].cols, G = W[0].groups;
+        const int tiles = total_tiles(W, n);
+        const int mode = gemv1_mode(K, G, in.x);
+        const G1Plan pl = gemv1_plan(G, W[0].kind, mode, tiles, device_cu_count(), gemv1_rows(M));
+        if (pl.ng > 0 && pl.kr > 1 && int64_t(pl.kr) * M * tiles * 16 <= part_floats) {
+            const uint16_t* nb[kMaxMulti] = {};
+            float* ny[kMaxMulti] = {};
+            *S = pl.kr;
+            return launch_gemv1(in.x, W, nb, ny, n, pl, mode, stream, M, part, false);
+        }
+    }
     RowsSetup r = rows_setup(W, n, M, part_floats);
     if (!r.ok) return hipErrorInvalidValue;
     GemvParams& p = r.p;
