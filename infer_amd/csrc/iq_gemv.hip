@@ -1716,7 +1716,11 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
 template <int KIND, bool PK, int NG, bool PRO = false>
 __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvParams p) {
     constexpr int WPG = KIND == 1 ? 1 : 2;
-    constexpr int GB = PK ? kHGroupBytes / 2 : kHGroupBytes;  // operand bytes per group
+    // operand chunks of a group 65 16-byte slots apart (not 64): a row's
+    // 16-byte stores from the conversion spread over the bank groups
+    // instead of hitting one; the MFMA's reads stay contiguous
+    constexpr int CS = 65;
+    constexpr int GB = (PK ? 4 : 8) * CS * 16;  // operand bytes per group
     __shared__ __attribute__((aligned(16))) int8_t As[NG][GB];
     __shared__ __attribute__((aligned(16))) float4_t Fs[NG][4];
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, q = lane >> 4;
@@ -1805,11 +1809,11 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
         xh_split8<KIND == 1>(xv[u], ho, lo, fac);
         half8_t* dst = reinterpret_cast<half8_t*>(As[i]);
         if (PK) {
-            dst[jj * 64 + m + 16 * qq] = ho;
-            dst[jj * 64 + m + 8 + 16 * qq] = lo;
+            dst[jj * CS + m + 16 * qq] = ho;
+            dst[jj * CS + m + 8 + 16 * qq] = lo;
         } else {
-            dst[(jj * 2) * 64 + m + 16 * qq] = ho;
-            dst[(jj * 2 + 1) * 64 + m + 16 * qq] = lo;
+            dst[(jj * 2) * CS + m + 16 * qq] = ho;
+            dst[(jj * 2 + 1) * CS + m + 16 * qq] = lo;
         }
         if (j16 == 0) reinterpret_cast<float*>(Fs[i])[m] = fac;
     }
@@ -1845,10 +1849,10 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
         for (int j = 0; j < 4; j++) {
             if (PK) {
                 // one operand per k-chunk: A rows 0..7 the hi, 8..15 the lo terms
-                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[j * 64 + lane]), B[j], Dv);
+                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[j * CS + lane]), B[j], Dv);
             } else {
-                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[(2 * j) * 64 + lane]), B[j], Dv);
-                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[(2 * j + 1) * 64 + lane]), B[j], Dv);
+                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[(2 * j) * CS + lane]), B[j], Dv);
+                Dv = mfma16(__builtin_bit_cast(half8_t, Ai[(2 * j + 1) * CS + lane]), B[j], Dv);
             }
         }
         const float sc = __uint_as_float(uint32_t(sv[i]) << 16);
@@ -1896,7 +1900,10 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
 template <int KIND, int NG, int MB, bool LOOP, bool PRO = false>
 __global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
     constexpr int NW = KIND == 1 ? 2 : 4;  // 16-byte weight loads per lane and group
-    __shared__ __attribute__((aligned(16))) half8_t Aq[MB][NG][8][64];  // [block][group][chunk][lane]
+    // [block][group][chunk][lane], chunks 65 slots apart: the conversion's
+    // 16-byte stores of one row's 8 chunks then fall in 8 different bank
+    // groups (64 apart they all hit one), the MFMA's reads stay contiguous
+    __shared__ __attribute__((aligned(16))) half8_t Aq[MB][NG][8][65];
     __shared__ __attribute__((aligned(16))) float Fq[MB][NG][16];
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
