@@ -1714,7 +1714,11 @@ __global__ __launch_bounds__(512, 2) void gemvs_kernel(const GemvParams p) {
 // its weights by the range's operands group by group as they land.  S > 1
 // ranges write fp32 partial sums (gemvt_reduce_kernel).
 template <int KIND, bool PK, int NG, bool PRO = false>
-__global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvParams p) {
+// (the second bound is the minimum waves per SIMD: 4 caps the registers at
+// 128, two 8-wave workgroups per CU; the prologue's instances rose to 132
+// under a bound of 2, one workgroup per CU.  Not the int8 prologue
+// instance, which would spill.)
+__global__ __launch_bounds__(512, NG > 8 ? 1 : ((PRO && KIND == 0 && !PK) ? 2 : 4)) void gemvr_kernel(const GemvParams p) {
     constexpr int WPG = KIND == 1 ? 1 : 2;
     // operand chunks of a group 65 16-byte slots apart (not 64): a row's
     // 16-byte stores from the conversion spread over the bank groups
@@ -1898,7 +1902,9 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : 2) void gemvr_kernel(const GemvPa
 // chunk at a time) multiplied by every block's operand before the next
 // chunk, so the weights are read and converted once for all the rows.
 template <int KIND, int NG, int MB, bool LOOP, bool PRO = false>
-__global__ __launch_bounds__(512, 2) void gemvq_kernel(const GemvParams p) {
+// (bounds as gemvr_kernel's; the looped and int8 two-block prologue
+// instances keep 2, where 4 would spill)
+__global__ __launch_bounds__(512, (PRO && (LOOP || (KIND == 0 && MB == 2))) ? 2 : 4) void gemvq_kernel(const GemvParams p) {
     constexpr int NW = KIND == 1 ? 2 : 4;  // 16-byte weight loads per lane and group
     // [block][group][chunk][lane], chunks 65 slots apart: the conversion's
     // 16-byte stores of one row's 8 chunks then fall in 8 different bank
