@@ -121,6 +121,7 @@ struct HostStage {
     // B-row stages (rows > 1)
     int rows = 1;
     int fused_r = 1;  // > 1: one stage_kernel launch of the R-row instance (rows <= R)
+    bool hroute = false;  // B rows on a narrow stage: operand preparation + gemvh (no epilogue launch)
     QView W[kMaxStageMats];
     RowsIn in{};
     CEpi epi{};
@@ -621,6 +622,9 @@ struct Chain {
     float* rpart = nullptr;
     int64_t rpart_floats = 0;
     float* rssq = nullptr;
+    // narrow B-row stages: their prepared f16 operands (one stage at a time)
+    int8_t* hxq = nullptr;
+    float* hxmeta = nullptr;
 };
 
 int chain_create(const iq_stage* stages, int n, Chain** out) {
@@ -754,6 +758,10 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
             ep.swiglu = pair ? 1 : 0;
             ep.res = a.out_op == IQ_OUT_RESIDUAL ? a.residual : nullptr;
             ep.ncols = pair ? int32_t(W0.rows) : int32_t(ep.ld);
+            // narrow stages (q|k|v, o at 9..32 rows): the input transform
+            // into prepared f16 operands, then gemvh with bias, residual and
+            // per-tile sums of squares in its own epilogue
+            hs.hroute = !pair && (a.out_op != IQ_OUT_RESIDUAL || a.n == 1) && chain_h_applies(hs.W, a.n, rows);
             continue;
         }
         // slices of whole 4-group blocks (measured: fewer, fatter waves beat
@@ -839,7 +847,7 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         std::vector<int> producer(static_cast<size_t>(n), -1);
         auto ssq_count = [&](int e) {
             const HostStage& hp = prog[size_t(e)];
-            return hp.fused_r > 1 ? int((hp.st.mat[0].N + 15) / 16) : int((hp.epi.ncols + 255) / 256);
+            return (hp.fused_r > 1 || hp.hroute) ? int((hp.st.mat[0].N + 15) / 16) : int((hp.epi.ncols + 255) / 256);
         };
         for (const auto& l : links)
             if (rows_of(l.second) > 1 && ssq_count(l.first) <= 256) producer[size_t(l.second)] = l.first;
@@ -892,6 +900,19 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
             if (e != hipSuccess) return fail(e);
             ch->rpart_floats = part;
         }
+        size_t hxq = 0, hmeta = 0;
+        for (const HostStage& h : prog) {
+            if (!h.hroute) continue;
+            size_t xb = 0, mf = 0;
+            chain_h_bytes(h.W[0].groups, h.rows, &xb, &mf);
+            hxq = std::max(hxq, xb);
+            hmeta = std::max(hmeta, mf);
+        }
+        if (hxq) {
+            hipError_t e = hipMalloc(reinterpret_cast<void**>(&ch->hxq), hxq);
+            if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ch->hxmeta), hmeta * sizeof(float));
+            if (e != hipSuccess) return fail(e);
+        }
     }
     ch->stages = std::move(prog);
     *out = ch;
@@ -901,7 +922,14 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
 hipError_t chain_run(const Chain* ch, hipStream_t stream) {
     for (const HostStage& h : ch->stages) {
         hipError_t e;
-        if (h.rows > 1 && h.fused_r == 1) {
+        if (h.rows > 1 && h.fused_r == 1 && h.hroute) {
+            if (h.own_ssq) {
+                const int K = int(h.W[0].cols);
+                ssq_kernel<<<dim3(unsigned(h.in.ssq_n), unsigned(h.rows)), 256, 0, stream>>>(h.in.x, K, h.in.ssq_n, h.ssq);
+            }
+            e = launch_chain_h(h.W, h.st.nmat, h.rows, h.in, h.epi.bias, h.epi.y, h.epi.res, h.epi.ssq_out, ch->hxq,
+                               ch->hxmeta, stream);
+        } else if (h.rows > 1 && h.fused_r == 1) {
             e = run_rows_stage(h, ch->rpart, ch->rpart_floats, stream);
         } else {
             if (h.own_ssq) {
@@ -921,6 +949,8 @@ void chain_destroy(Chain* ch) {
     if (ch->partials) (void)hipFree(ch->partials);
     if (ch->rpart) (void)hipFree(ch->rpart);
     if (ch->rssq) (void)hipFree(ch->rssq);
+    if (ch->hxq) (void)hipFree(ch->hxq);
+    if (ch->hxmeta) (void)hipFree(ch->hxmeta);
     delete ch;
 }
 

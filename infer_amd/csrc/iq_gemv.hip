@@ -144,6 +144,11 @@ struct GemvParams {
     int ssq_n;
     float eps;
     int to_part;
+    // gemvh epilogue (chain stages): y = res + (sum + bias) when res, and
+    // the sum of squares of each 16-column tile of each output row into
+    // ssq_out[m * ntiles + tile] when ssq_out
+    const float* res;
+    float* ssq_out;
 };
 
 // ------------------------------------------------------------------ chain prologue
@@ -1433,6 +1438,64 @@ __global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x
     if (j16 == 0) xfx[(int64_t(b) * G + g) * 16 + i] = fac;
 }
 
+// xhprep_kernel's output (16-row blocks, not packed) from a chain stage's
+// input: activation row m read through the prologue's gather and RMSNorm
+// (pro_x_offset, pro_norm8).  Each wave takes one (row, 4 groups) and
+// computes its row's factor r_m itself, in ProScale's order (lane j < 16
+// adds partials j, j + 16, ... in double, then the 16 sums in order), so
+// the operands equal those the prologue instances make.
+template <bool PERM>
+__global__ __launch_bounds__(256) void xhprep_pro_kernel(const GemvParams p, int64_t quads, int nb,
+                                                         _Float16* __restrict__ xh, float* __restrict__ xfx) {
+    const int lane = threadIdx.x & 63, j16 = lane & 15;
+    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wave >= int64_t(nb) * 16 * quads) return;
+    const int M = p.M;
+    const int64_t G = p.G;
+    const int m = int(wave / quads);  // rows past M are written as zeros
+    const int64_t g = (wave % quads) * 4 + (lane >> 4);
+    const bool ok = g < G && m < M;
+    const int64_t c = (ok ? g : 0) * kGroup + j16 * 8;
+    const rsrc_t rx = make_rsrc(p.x, int64_t(M) * p.xstride * 4);
+    const uint32_t o = ok ? pro_x_offset(p, m, c) : kOob;
+    const float4_t a = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0));
+    const float4_t bq = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, o, 16, 0));
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        v[e] = a[e];
+        v[4 + e] = bq[e];
+    }
+    if (p.norm) {  // uniform
+        const rsrc_t rn = make_rsrc(p.norm, p.K * 2);
+        const uint4 nw = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rn, ok ? uint32_t(c) * 2 : kOob, 0, 0));
+        const rsrc_t rq = make_rsrc(p.ssq, int64_t(M) * p.ssq_n * 4);
+        double part = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int bb = lane + 16 * k;
+            const float sq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                           rq, (lane < 16 && m < M && bb < p.ssq_n) ? uint32_t(m * p.ssq_n + bb) * 4 : kOob, 0, 0));
+            part += double(sq);
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) ss += __shfl(part, j, 64);
+        const float r = 1.0f / __builtin_sqrtf(float(ss / double(p.K)) + p.eps);
+        pro_norm8(v, nw, r);
+    }
+    half8_t ho, lo2;
+    float fac;
+    xh_split8<PERM>(v, ho, lo2, fac);
+    if (g >= G) return;
+    const int b = m >> 4, i = m & 15, q = j16 >> 2, jj = j16 & 3;
+    _Float16* base = xh + ((int64_t(b) * G + g) * kHGroupBytes) / 2;
+    const int l = i + 16 * q;
+    *reinterpret_cast<half8_t*>(base + ((jj * 2 + 0) * 64 + l) * 8) = ho;
+    *reinterpret_cast<half8_t*>(base + ((jj * 2 + 1) * 64 + l) * 8) = lo2;
+    if (j16 == 0) xfx[(int64_t(b) * G + g) * 16 + i] = fac;
+}
+
 // Workgroup = T consecutive 16-row tiles (of any of the call's matrices) x
 // KS waves, wave w taking groups [w gs, w gs + gs) of every tile; per group a
 // wave loads the 8 prepared A operands once (contiguous 1 KiB each, from
@@ -1567,8 +1630,19 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
         }
         const TileSel ts = select_tile(p, tb + t);
         const int64_t row = ts.row0 + n;
-        if (row < ts.m.N)
-            ts.m.y[int64_t(m) * ts.m.N + row] = sum + (ts.m.bias ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
+        float v = sum + (ts.m.bias && row < ts.m.N ? bf16_to_f32(ts.m.bias[row]) : 0.0f);
+        if (p.res && row < ts.m.N) v = p.res[int64_t(m) * ts.m.N + row] + v;
+        if (row < ts.m.N) ts.m.y[int64_t(m) * ts.m.N + row] = v;
+        if (p.ssq_out) {
+            // (the 16 lanes n of (t, m) are one DPP row and take this branch
+            // together: m and t are the same for all of them)
+            float sq = row < ts.m.N ? v * v : 0.0f;
+            sq += __int_as_float(row_ror<8>(__float_as_int(sq)));
+            sq += __int_as_float(row_ror<4>(__float_as_int(sq)));
+            sq += __int_as_float(row_ror<2>(__float_as_int(sq)));
+            sq += __int_as_float(row_ror<1>(__float_as_int(sq)));
+            if (n == 0) p.ssq_out[int64_t(m) * p.ntiles + tb + t] = sq;
+        }
     }
 }
 
@@ -2294,8 +2368,12 @@ void launch_gemvh_t(const GemvParams& p, int ks, hipStream_t stream) {
 }
 
 // The n matrices (one kind and width) on the prepared f16 split activations.
-hipError_t launch_gemvh(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
-                        hipStream_t stream) {
+// gemvh over the prepared operands at xq / xmeta (16-row blocks), with the
+// chain epilogue's residual and per-tile sums of squares (res: one matrix,
+// [M][N]; ssq_out: [M][tiles]) when given.
+hipError_t launch_gemvh_on(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
+                           const int8_t* xq, const float* xmeta, const float* res, float* ssq_out,
+                           hipStream_t stream) {
     const int64_t K = W[0].cols, G = W[0].groups;
     const int tiles = total_tiles(W, n);
     // tiles per workgroup (measured, 7B shapes at 16 rows): the prepared
@@ -2317,8 +2395,10 @@ hipError_t launch_gemvh(const QView* W, const uint16_t* const* bias, float* cons
         p.nmat = n;
         p.K = K;
         p.G = G;
-        p.xq = ws->xq + int64_t(r0 / 16) * G * kHGroupBytes;
-        p.meta = reinterpret_cast<const int4*>(reinterpret_cast<const float*>(ws->xmeta) + int64_t(r0 / 16) * G * 16);
+        p.xq = xq + int64_t(r0 / 16) * G * kHGroupBytes;
+        p.meta = reinterpret_cast<const int4*>(xmeta + int64_t(r0 / 16) * G * 16);
+        p.res = res ? res + int64_t(r0) * W[0].rows : nullptr;
+        p.ssq_out = ssq_out ? ssq_out + int64_t(r0) * tiles : nullptr;
         p.M = M - r0 < 16 ? M - r0 : 16;
         p.gs = gs;
         p.S = M <= 8 ? 0 : 1;  // 0: the packed (M <= 8) preparation
@@ -2336,6 +2416,12 @@ hipError_t launch_gemvh(const QView* W, const uint16_t* const* bias, float* cons
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+hipError_t launch_gemvh(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M, Workspace* ws,
+                        hipStream_t stream) {
+    return launch_gemvh_on(W, bias, y, n, M, ws->xq, reinterpret_cast<const float*>(ws->xmeta), nullptr, nullptr,
+                           stream);
 }
 
 hipError_t launch_batched_multi(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
@@ -2667,6 +2753,43 @@ hipError_t launch_chain_rows(const QView* W, int n, int M, const RowsIn& in, flo
         }
     }
     return hipGetLastError();
+}
+
+void chain_h_bytes(int64_t G, int M, size_t* xq_bytes, size_t* meta_floats) {
+    const int64_t nb = (M + 15) / 16;
+    *xq_bytes = size_t(nb * G * kHGroupBytes);
+    *meta_floats = size_t(nb * G * 16);
+}
+
+bool chain_h_applies(const QView* W, int n, int M) {
+    return M >= 9 && M <= 16 && W[0].cols % kGroup == 0 && total_tiles(W, n) < 1024 && W[0].groups < 128;
+}
+
+hipError_t launch_chain_h(const QView* W, int n, int M, const RowsIn& in, const uint16_t* const* bias,
+                          float* const* y, const float* res, float* ssq_out, int8_t* xq, float* xmeta,
+                          hipStream_t stream) {
+    if (!chain_h_applies(W, n, M)) return hipErrorInvalidValue;
+    const int64_t K = W[0].cols, G = W[0].groups, quads = (G + 3) / 4;
+    const int nb = (M + 15) / 16;
+    GemvParams pp{};
+    pp.x = in.x;
+    pp.xstride = in.xstride;
+    pp.gqa_hd = in.gqa_hd;
+    pp.gqa_span = in.gqa_span;
+    pp.norm = in.norm;
+    pp.ssq = in.ssq;
+    pp.ssq_n = in.ssq_n;
+    pp.eps = in.eps;
+    pp.M = M;
+    pp.K = K;
+    pp.G = G;
+    const unsigned grid = unsigned((int64_t(nb) * 16 * quads + 3) / 4);
+    _Float16* xh = reinterpret_cast<_Float16*>(xq);
+    if (W[0].kind == 1) xhprep_pro_kernel<true><<<grid, 256, 0, stream>>>(pp, quads, nb, xh, xmeta);
+    else xhprep_pro_kernel<false><<<grid, 256, 0, stream>>>(pp, quads, nb, xh, xmeta);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_gemvh_on(W, bias, y, n, M, xq, xmeta, res, ssq_out, stream);
 }
 
 }  // namespace iq

@@ -124,6 +124,16 @@ struct RowsIn {
 int64_t chain_rows_partials(const QView* W, int n, int M, int64_t cap);
 hipError_t launch_chain_rows(const QView* W, int n, int M, const RowsIn& in, float* part, int64_t part_floats,
                              int* S, hipStream_t stream);
+// A narrow chain stage at 9..16 rows (under 1024 tiles, G < 128): the
+// input transform into f16 hi / lo operands at xq / xmeta (one 16-row
+// block: G * 8 KiB and G * 64 bytes), then gemvh storing y = (res +) sum +
+// bias and, when ssq_out, the sum of squares of each 16-column tile of each
+// row (ssq_out[m * tiles + tile]).
+bool chain_h_applies(const QView* W, int n, int M);
+void chain_h_bytes(int64_t G, int M, size_t* xq_bytes, size_t* meta_floats);
+hipError_t launch_chain_h(const QView* W, int n, int M, const RowsIn& in, const uint16_t* const* bias,
+                          float* const* y, const float* res, float* ssq_out, int8_t* xq, float* xmeta,
+                          hipStream_t stream);
 
 // A validated stage program on the device (iq_chain.hip).
 struct Chain;
