@@ -2373,7 +2373,7 @@ void launch_gemvh_t(const GemvParams& p, int ks, hipStream_t stream) {
 // [M][N]; ssq_out: [M][tiles]) when given.
 hipError_t launch_gemvh_on(const QView* W, const uint16_t* const* bias, float* const* y, int n, int M,
                            const int8_t* xq, const float* xmeta, const float* res, float* ssq_out,
-                           hipStream_t stream) {
+                           hipStream_t stream, bool packed = true) {
     const int64_t K = W[0].cols, G = W[0].groups;
     const int tiles = total_tiles(W, n);
     // tiles per workgroup (measured, 7B shapes at 16 rows): the prepared
@@ -2401,7 +2401,7 @@ hipError_t launch_gemvh_on(const QView* W, const uint16_t* const* bias, float* c
         p.ssq_out = ssq_out ? ssq_out + int64_t(r0) * tiles : nullptr;
         p.M = M - r0 < 16 ? M - r0 : 16;
         p.gs = gs;
-        p.S = M <= 8 ? 0 : 1;  // 0: the packed (M <= 8) preparation
+        p.S = M <= 8 && packed ? 0 : 1;  // 0: the packed (M <= 8) preparation
         p.ntiles = tiles;
         if (W[0].kind == 1) {
             if (T == 4) launch_gemvh_t<1, 4>(p, ks, stream);
@@ -2762,7 +2762,7 @@ void chain_h_bytes(int64_t G, int M, size_t* xq_bytes, size_t* meta_floats) {
 }
 
 bool chain_h_applies(const QView* W, int n, int M) {
-    return M >= 9 && M <= 16 && W[0].cols % kGroup == 0 && total_tiles(W, n) < 1024 && W[0].groups < 128;
+    return M >= 5 && M <= 16 && W[0].cols % kGroup == 0 && total_tiles(W, n) < 1024 && W[0].groups < 128;
 }
 
 hipError_t launch_chain_h(const QView* W, int n, int M, const RowsIn& in, const uint16_t* const* bias,
@@ -2789,7 +2789,9 @@ hipError_t launch_chain_h(const QView* W, int n, int M, const RowsIn& in, const 
     else xhprep_pro_kernel<false><<<grid, 256, 0, stream>>>(pp, quads, nb, xh, xmeta);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_gemvh_on(W, bias, y, n, M, xq, xmeta, res, ssq_out, stream);
+    // (the unpacked operand form at 5..8 rows too: rows 8..15 of each block
+    // are zero)
+    return launch_gemvh_on(W, bias, y, n, M, xq, xmeta, res, ssq_out, stream, false);
 }
 
 }  // namespace iq

@@ -124,7 +124,7 @@ struct RowsIn {
 int64_t chain_rows_partials(const QView* W, int n, int M, int64_t cap);
 hipError_t launch_chain_rows(const QView* W, int n, int M, const RowsIn& in, float* part, int64_t part_floats,
                              int* S, hipStream_t stream);
-// A narrow chain stage at 9..16 rows (under 1024 tiles, G < 128): the
+// A narrow chain stage at 5..16 rows (under 1024 tiles, G < 128): the
 // input transform into f16 hi / lo operands at xq / xmeta (one 16-row
 // block: G * 8 KiB and G * 64 bytes), then gemvh storing y = (res +) sum +
 // bias and, when ssq_out, the sum of squares of each 16-column tile of each

@@ -228,11 +228,12 @@ class RowView:
         self.logits = row(step.logits)
 
 
-@pytest.mark.parametrize("B", [2, 3, 4, 16, 32])
+@pytest.mark.parametrize("B", [2, 3, 4, 6, 16, 32])
 @pytest.mark.parametrize("kind,head_kind", [(1, 0), (0, 0)])
 def test_chain_rows_small_model_matches_forward(B, kind, head_kind):
     """B sequences of one token each: 2..4 rows on the fused R-row stages
-    (one launch per stage), more on the B-row stages (rows GEMV + epilogue);
+    (one launch per stage), more on the B-row stages (rows GEMV + epilogue;
+    at 5..16 rows the narrow ones on operand preparation + gemvh);
     every stage of every row against the oracle on the chain's own inputs,
     and every row's logits against the float64 forward of its token."""
     rng = np.random.default_rng(100 + B + 3 * kind + head_kind)
