@@ -563,7 +563,9 @@ __global__ __launch_bounds__(512) void gemm_xprep_kernel(const float* __restrict
 // rows each; 32x32 MFMA tiles; 64-column K steps double-buffered in LDS with
 // the step after next in registers), on the prepared fp16 operands (LO: hi
 // and lo, two MFMAs per weight operand).  K % 128 == 0.
-template <int KIND, bool LO, int NJ, int BM>
+// NR: K steps whose loads are in flight in registers (2, or 4 for short
+// T, where each workgroup's steps wait on memory rather than on the MFMAs)
+template <int KIND, bool LO, int NJ, int BM, int NR = 2>
 __global__ __launch_bounds__(BM >= 128 ? 2 * kThreads : kThreads, (BM == 256 || LO) ? 1 : 2) void gemmh_kernel(
     const GemmhParams p) {
     constexpr int BN = 64 * NJ;
@@ -600,7 +602,7 @@ __global__ __launch_bounds__(BM >= 128 ? 2 * kThreads : kThreads, (BM == 256 || 
         uint4 wr[WCH];
         uint32_t zr;
     };
-    Regs r0, r1;
+    Regs rr[NR];
 
     bool wok[WCH];
     int wcol[WCH];
@@ -712,10 +714,11 @@ __global__ __launch_bounds__(BM >= 128 ? 2 * kThreads : kThreads, (BM == 256 || 
     load_scales(0, s_cur);
     load_scales(1, s_nxt);
 
-    load_step(r0, 0);
-    store_step(r0, 0);
-    if (nk > 1) load_step(r1, 1);
-    if (nk > 2) load_step(r0, 2);
+    load_step(rr[0], 0);
+    store_step(rr[0], 0);
+#pragma unroll
+    for (int j = 1; j <= NR; j++)
+        if (nk > j) load_step(rr[j % NR], j);
     __syncthreads();
     auto step = [&](auto par, int kt, Regs& rnext) {
         constexpr int PAR = decltype(par)::value;
@@ -756,13 +759,20 @@ __global__ __launch_bounds__(BM >= 128 ? 2 * kThreads : kThreads, (BM == 256 || 
             load_scales(kt / 2 + 2, s_nxt);
         }
         if (kt + 1 < nk) store_step(rnext, buf ^ 1);
-        if (kt + 3 < nk) load_step(rnext, kt + 3);
+        if (kt + 1 + NR < nk) load_step(rnext, kt + 1 + NR);
         __syncthreads();
     };
-    // nk is even (K ranges are whole 128-column groups)
-    for (int kt = 0; kt < nk; kt += 2) {
-        step(std::integral_constant<int, 0>{}, kt, r1);
-        step(std::integral_constant<int, 1>{}, kt + 1, r0);
+    // nk is even (K ranges are whole 128-column groups); register set
+    // (kt + 1) % NR holds step kt + 1 while step kt runs
+    for (int kt = 0; kt < nk; kt += NR) {
+        step(std::integral_constant<int, 0>{}, kt, rr[1 % NR]);
+        step(std::integral_constant<int, 1>{}, kt + 1, rr[2 % NR]);
+        if constexpr (NR == 4) {
+            if (kt + 2 < nk) {
+                step(std::integral_constant<int, 0>{}, kt + 2, rr[3]);
+                step(std::integral_constant<int, 1>{}, kt + 3, rr[0]);
+            }
+        }
     }
 
     // Epilogue: lane holds rows m = 8*(r/4) + 4*(lane/32) + r%4 of each 32x32 tile.
@@ -938,8 +948,8 @@ hipError_t launch_gemmh_chunk(const float* x_f32, const QView& W, const uint16_t
         if (W.kind == 1) gemmh_kernel<1, true, 2, 128><<<ggrid, 2 * kThreads, 0, stream>>>(p);
         else gemmh_kernel<0, true, 2, 128><<<ggrid, 2 * kThreads, 0, stream>>>(p);
     } else {
-        if (W.kind == 1) gemmh_kernel<1, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
-        else gemmh_kernel<0, true, 2, 64><<<ggrid, kThreads, 0, stream>>>(p);
+        if (W.kind == 1) gemmh_kernel<1, true, 2, 64, 4><<<ggrid, kThreads, 0, stream>>>(p);
+        else gemmh_kernel<0, true, 2, 64, 4><<<ggrid, kThreads, 0, stream>>>(p);
     }
     if (p.splits > 1) {
         const int64_t n = p.T * p.N;
