@@ -204,11 +204,13 @@ typedef struct iq_stage {
 typedef struct iq_chain iq_chain;
 
 /* Validates the n stages and records their launch shapes for the current
- * device.  When an RMSNorm stage reads the output of an earlier stage, the
- * chain also allocates one small device array (a float per 16-row tile of
- * each such producer) for the per-tile sums of squares passed between them,
- * so create a chain outside graph capture, in code that may allocate;
- * iq_chain_destroy frees it.  iq_chain_run allocates nothing. */
+ * device.  The chain allocates its own device buffers here: the sums of
+ * squares passed from a stage to a later RMSNorm stage (a float per 16-row
+ * tile, or per row and tile / 256-column block with rows > 1), and for
+ * stages with rows > 1 the K-range partial sums of the rows GEMV and the
+ * prepared f16 operands of narrow stages (5..16 rows: G * 8 KiB).  So
+ * create a chain outside graph capture, in code that may allocate;
+ * iq_chain_destroy frees them.  iq_chain_run allocates nothing. */
 int iq_chain_create(const iq_stage* stages, int n, iq_chain** out);
 /* Enqueues one run of the whole program on `stream`. */
 int iq_chain_run(const iq_chain* chain, void* stream);
