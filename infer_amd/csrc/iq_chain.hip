@@ -362,17 +362,11 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
             xw[0][t][0] = a;
             xw[0][t][1] = c;
         }
-    } else if constexpr (norm) {
-#pragma unroll
-        for (int m = 0; m < R; m++) {
-            double part = 0.0;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                part += (R == 1 || 4 * lane + j < st.ssq_n) ? double(__uint_as_float(xc[m][j])) : 0.0;
-            const double ss = wave_sum(part);
-            scale[m] = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
-        }
     }
+    // (from the producer's sums, NORM 1, the factor r_m multiplies the
+    // output sums at the end instead: the limbs are made from x * w, so
+    // the conversion does not wait for the sums of squares to land and be
+    // added; (W (x w)) r and W ((x r) w) differ by fp32 rounding only)
 #pragma unroll
     for (int m = 0; m < R; m++)
 #pragma unroll
@@ -448,6 +442,20 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
         }
     }
 
+    // RMSNorm factors from the producer's per-tile sums (NORM 1), in double
+    // in a fixed order, every wave (wave_sum needs all 64 lanes)
+    if constexpr (NORM == 1) {
+#pragma unroll
+        for (int m = 0; m < R; m++) {
+            double part = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                part += (R == 1 || 4 * lane + j < st.ssq_n) ? double(__uint_as_float(xc[m][j])) : 0.0;
+            const double ss = wave_sum(part);
+            scale[m] = 1.0f / __builtin_sqrtf(float(ss / double(K)) + st.eps);
+        }
+    }
+
     // 5. Partials through LDS; the last wave adds them in wave order and
     //    applies the epilogue (and the per-tile sum of squares of the output
     //    for a consumer's RMSNorm).
@@ -467,6 +475,14 @@ __global__ __launch_bounds__(KIND == 1 ? 64 * kMaxWaves : 32 * kMaxWaves) void s
         for (int i = 0; i < nw; i++) sum[t] += red[i][t][lane];
     }
     const int64_t row = row0 + ln;
+    if constexpr (NORM == 1) {
+        // this lane's row: 0, or lane group kg (R > 1); no dynamic index
+        float rsc = scale[0];
+#pragma unroll
+        for (int m = 1; m < R; m++) rsc = kg == m ? scale[m] : rsc;
+#pragma unroll
+        for (int t = 0; t < TP; t++) sum[t] *= rsc;
+    }
     float v = sum[0] + __uint_as_float(addb[0] << 16);
     if (TP == 2) {
         // silu(g) * u  (kernels/ops/elementwise.cu:6-11)
