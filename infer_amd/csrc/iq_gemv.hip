@@ -1503,7 +1503,7 @@ __global__ __launch_bounds__(256) void xhprep_pro_kernel(const GemvParams p, int
 // in flight.  Slice sums are added through LDS in wave order
 // (deterministic).  p.M <= 16 rows of the block; p.xq / p.meta point at the
 // block's prepared operands and factors.
-template <int KIND, int T, bool PK>
+template <int KIND, int T, bool PK, bool D3 = false>
 __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvParams p) {
     extern __shared__ float hred[];  // [T][KS][4][64]
     constexpr int WPG = KIND == 1 ? 1 : 2;
@@ -1601,14 +1601,31 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void gemvh_kernel(const GemvPa
             for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(D[r], s * b.fx[r], acc[t][r]);
         }
     };
-    GB b0, b1;
-    if (g0 < g1) load(g0, b0);
-    for (int g = g0; g < g1; g += 2) {
-        if (g + 1 < g1) load(g + 1, b1);
-        compute(b0);
-        if (g + 1 >= g1) break;
-        if (g + 2 < g1) load(g + 2, b0);
-        compute(b1);
+    if constexpr (D3) {
+        // two groups in flight while one is multiplied
+        GB b0, b1, b2;
+        if (g0 < g1) load(g0, b0);
+        if (g0 + 1 < g1) load(g0 + 1, b1);
+        for (int g = g0; g < g1; g += 3) {
+            if (g + 2 < g1) load(g + 2, b2);
+            compute(b0);
+            if (g + 1 >= g1) break;
+            if (g + 3 < g1) load(g + 3, b0);
+            compute(b1);
+            if (g + 2 >= g1) break;
+            if (g + 4 < g1) load(g + 4, b1);
+            compute(b2);
+        }
+    } else {
+        GB b0, b1;
+        if (g0 < g1) load(g0, b0);
+        for (int g = g0; g < g1; g += 2) {
+            if (g + 1 < g1) load(g + 1, b1);
+            compute(b0);
+            if (g + 1 >= g1) break;
+            if (g + 2 < g1) load(g + 2, b0);
+            compute(b1);
+        }
     }
 
 #pragma unroll
@@ -2363,7 +2380,11 @@ template <int KIND, int T>
 void launch_gemvh_t(const GemvParams& p, int ks, hipStream_t stream) {
     const unsigned grid = unsigned((p.ntiles + T - 1) / T);
     const size_t lds = size_t(T) * ks * 4 * 64 * 4;
+    // (T = 2, 9..16 rows: two groups in flight per wave, 183 / 199 VGPRs on
+    // 8-wave workgroups; 7B q|k|v at 16 rows 13.8 -> 13.2 us with its
+    // preparation.  The 16-wave T = 1 instance would spill at 128.)
     if (p.M <= 8 && p.S == 0) gemvh_kernel<KIND, T, true><<<grid, 64 * ks, lds, stream>>>(p);
+    else if constexpr (T == 2) gemvh_kernel<KIND, T, false, true><<<grid, 64 * ks, lds, stream>>>(p);
     else gemvh_kernel<KIND, T, false><<<grid, 64 * ks, lds, stream>>>(p);
 }
 
