@@ -152,6 +152,24 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+@pytest.mark.parametrize("M", [9, 16])
+def test_qkv_7b_multi_gemvh(kind, M):
+    """q|k|v of one 7B layer (3584 + 512 + 512 rows x 3584, 288 tiles) in
+    one iq_gemv_multi call at 9..16 rows: the preparation launch and gemvh
+    on two tiles per workgroup, two groups in flight per wave."""
+    rng = np.random.default_rng(4600 + 20 * kind + M)
+    K = 3584
+    Ws = [Packed(rng, n, K, kind) for n in (3584, 512, 512)]
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("q|k|v 7B multi gemvh", kind, M)
+    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], None, M, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y) in enumerate(zip(Ws, ys)):
+        check_sampled(y, x, W, M, rng, f"q|k|v[{i}] kind={kind} M={M}")
+
+
 @pytest.mark.parametrize("M", [1, 3, 4, 5, 9, 16])
 def test_lm_head_int8(M):
     """The int8 lm_head 152064 x 3584 (9504 tiles)."""
