@@ -345,13 +345,16 @@ __device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParam
 // zero), so the same two MFMAs give row m's limb sums in D rows
 // 4m .. 4m + 3, i.e. registers 0..3 of lanes 16m .. 16m + 15.  Returns the
 // running sum of activation row l/16 (R = 4) or row 0 (R = 1, lanes 0..15).
-template <int KIND, int NG, int R>
-__device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_t* xs, const int4* ms,
-                                           const int8_t* xzero, int RS, int glo, int M, int gbeg, int gs, int ln,
-                                           int kg) {
+// TP slices (TP 16-row tiles of one workgroup, R = 1 only) share each
+// A operand read: acc[t] is tile t's sum.
+template <int KIND, int NG, int R, int TP = 1>
+__device__ __forceinline__ void slice_dot_tp(const Slice<KIND, NG> (&b)[TP], const int8_t* xs, const int4* ms,
+                                             const int8_t* xzero, int RS, int glo, int M, int gbeg, int gs, int ln,
+                                             int kg, float (&acc)[TP]) {
     // records of row m, group g at (m RS + g - glo) (RS records per row,
     // the first of them group glo)
-    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < TP; t++) acc[t] = 0.0f;
     const int am = R == 1 ? 0 : ln >> 2, aL = R == 1 ? ln : ln & 3;  // A row of this lane
     const bool alive = am < M;
     const int xoff = (am * RS - glo) * kLimbRec + aL * kGroup + kg * 16;
@@ -366,30 +369,44 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
             const int gl = 4 * q4 + e;
             const bool ok = gl < gs;
             const int g = gbeg + (ok ? gl : 0);
-            int4v_t a0, a1, b0, b1;
+            int4v_t a0, a1;
             {
                 const int8_t* pa = alive ? xs + (xoff + g * kLimbRec) : xzero;
                 a0 = *reinterpret_cast<const int4v_t*>(pa);
                 a1 = *reinterpret_cast<const int4v_t*>(pa + (alive ? 64 : 0));
             }
-            if (KIND == 1) {
-                const int4v_t v = b.w[gl][0];
-                b0 = v & 0x0F0F0F0F;
-                b1 = (v >> 4) & 0x0F0F0F0F;
-            } else {
-                b0 = b.w[gl][0];
-                b1 = b.w[gl][1];
+            const int4 md = ms[moff + g];
+#pragma unroll
+            for (int t = 0; t < TP; t++) {
+                int4v_t b0, b1;
+                if (KIND == 1) {
+                    const int4v_t v = b[t].w[gl][0];
+                    b0 = v & 0x0F0F0F0F;
+                    b1 = (v >> 4) & 0x0F0F0F0F;
+                } else {
+                    b0 = b[t].w[gl][0];
+                    b1 = b[t].w[gl][1];
+                }
+                int4v_t D = mfma_i8(a0, b0, int4v_t{0, 0, 0, 0});
+                D = mfma_i8(a1, b1, D);
+                const uint32_t sw = b[t].s[gl / 2];
+                const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+                const int z = KIND == 1 ? int((b[t].z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
+                const float nacc = combine(acc[t], D[0], D[1], D[2], D[3], z, md, sc);
+                acc[t] = ok ? nacc : acc[t];
             }
-            int4v_t D = mfma_i8(a0, b0, int4v_t{0, 0, 0, 0});
-            D = mfma_i8(a1, b1, D);
-            const uint32_t sw = b.s[gl / 2];
-            const float sc = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
-            const int z = KIND == 1 ? int((b.z[gl / 4] >> (8 * (gl & 3))) & 0xFF) : 0;
-            const float nacc = combine(acc, D[0], D[1], D[2], D[3], z, ms[moff + g], sc);
-            acc = ok ? nacc : acc;
         }
     }
-    return acc;
+}
+
+template <int KIND, int NG, int R>
+__device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_t* xs, const int4* ms,
+                                           const int8_t* xzero, int RS, int glo, int M, int gbeg, int gs, int ln,
+                                           int kg) {
+    float acc[1];
+    slice_dot_tp<KIND, NG, R, 1>(reinterpret_cast<const Slice<KIND, NG>(&)[1]>(b), xs, ms, xzero, RS, glo, M, gbeg,
+                                 gs, ln, kg, acc);
+    return acc[0];
 }
 
 // One activation row (the decode step).  Workgroup = KS waves (runtime,
@@ -401,7 +418,11 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // instead of every wave fetching the same lines for its slice.  The slice partials are added
 // through LDS by whichever wave finishes last (an LDS counter), in slice
 // order, so the sum is deterministic and no wave waits for the others.
-template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT, bool HALF = false>
+// TP = 2 (1 row, staged metadata, G <= 32): the workgroup owns tiles 2b
+// and 2b + 1 (wave t < 2 stages tile t's scales and zero points); each wave
+// requests both tiles' slices and multiplies them by the same activation
+// limbs, so one conversion of x and one LDS operand read serve 32 rows.
+template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT, bool HALF = false, int TP = 1>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // dynamic LDS: limbs [RR][G][512], meta [R][G] int4, then (staged) the
     // tile's scales [16][G] bf16 and zero points [16][G] u8.  R = 8, and R =
@@ -409,11 +430,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // records (each wave reuses its own groups' records; the weights stay
     // in registers): half the LDS of one block of R rows.
     static_assert(!HALF || (R == 4 && !KSPLIT), "two 2-row blocks: the 4-row instance, one K range");
+    static_assert(TP == 1 || (R == 1 && MODE == 2 && !KSPLIT), "two tiles: 1 row, staged metadata");
     constexpr int RR = HALF ? R / 2 : (R < 4 ? R : 4);  // rows per block
     constexpr int RB = R / RR;                          // blocks
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
     __shared__ __attribute__((aligned(16))) int8_t xzero[16];
-    __shared__ float red[MAXW][RB][16 * RR];
+    __shared__ float red[MAXW][RB * TP][16 * RR];
     __shared__ int arrived;
     const int tid = threadIdx.x, lane = tid & 63, ln = lane & 15, kg = lane >> 4, wave = tid >> 6;
     const int KS = int(blockDim.x) >> 6;
@@ -427,9 +449,14 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     const int M = R == 1 ? 1 : p.M;  // activation rows (R = 4: 1..4, R = 8: 5..8)
     int4* ms1 = reinterpret_cast<int4*>(xs1 + RR * RS * kLimbRec);
     int8_t* tmeta = xs1 + (RR * kLimbRec + R * 16) * RS;
-    const int tile = KSPLIT ? int(blockIdx.x) / kr : int(blockIdx.x);
-    const TileSel ts = select_tile(p, tile);
-    const bool staged = MODE == 2 && p.S == 2;  // (only with kr == 1)
+    const int tile = KSPLIT ? int(blockIdx.x) / kr : int(blockIdx.x) * TP;
+    // (TP = 2, odd tile count: the last workgroup's second tile starts past
+    // its matrix's rows, so its loads read zero and nothing is stored)
+    TileSel tsv[TP];
+#pragma unroll
+    for (int t = 0; t < TP; t++) tsv[t] = select_tile(p, tile + t);
+    const TileSel& ts = tsv[0];
+    const bool staged = MODE == 2 && (TP > 1 || p.S == 2);  // (only with kr == 1)
 
     // 1. This wave's activations: pass t converts groups gbeg + 4t + kg,
     //    16 lanes (one DPP row) per group, 8 columns per lane.  Every wave
@@ -438,11 +465,13 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     //    CU's weight misses would arrive only after them.
     //    The bias of the rows this lane may store goes first (lanes 0..15 of
     //    every wave: any wave may be the one that finishes the tile).
-    uint32_t bias;
-    {
-        const rsrc_t rb = make_rsrc(ts.m.bias, ts.m.bias ? ts.m.N * 2 : 0);
-        bias = __builtin_amdgcn_raw_buffer_load_b16(rb, lane < 16 * (M < 4 ? M : 4) ? uint32_t(ts.row0 + ln) * 2 : kOob,
-                                                    0, 0);
+    uint32_t bias = 0;
+#pragma unroll
+    for (int t = 0; t < TP; t++) {
+        // (TP = 2: lanes 16t .. 16t + 15 take tile t's; the others read zero)
+        const rsrc_t rb = make_rsrc(tsv[t].m.bias, tsv[t].m.bias ? tsv[t].m.N * 2 : 0);
+        const bool mine = TP == 1 ? lane < 16 * (M < 4 ? M : 4) : kg == t;
+        bias |= __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(tsv[t].row0 + ln) * 2 : kOob, 0, 0);
     }
     constexpr int XP = NG / 4;
     float xv[R][XP][8];
@@ -466,21 +495,28 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     //    The staged loads are unconditional (not staged, or threads past
     //    the block: an empty range, reading zero): under a branch the
     //    compiler waited for every earlier load before the weights went out.
+    //    TP = 2: wave t < 2 stages tile t's blocks (2 G <= 64).
     int4v_t mv_s = {0, 0, 0, 0}, mv_z = {0, 0, 0, 0};
-    const int64_t trows = ts.m.N - ts.row0 < 16 ? ts.m.N - ts.row0 : 16;
     if constexpr (MODE == 2) {
-        const rsrc_t rs = make_rsrc(ts.m.scales + ts.row0 * G, staged ? trows * G * 2 : 0);
+        const int wt = TP == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave < TP ? wave : 0);
+        const TileSel tw = (TP > 1 && wt) ? tsv[TP - 1] : tsv[0];
+        int64_t trows = tw.m.N - tw.row0 < 16 ? tw.m.N - tw.row0 : 16;
+        trows = trows > 0 ? trows : 0;
+        const int sl = TP == 1 ? tid : (wave < TP ? lane : 64);  // 16-byte chunk of this thread
+        const rsrc_t rs = make_rsrc(tw.m.scales + tw.row0 * G, staged ? trows * G * 2 : 0);
         mv_s = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rs, tid < 2 * G ? uint32_t(tid) * 16 : kOob, 0, 0));
+                                               rs, sl < 2 * G ? uint32_t(sl) * 16 : kOob, 0, 0));
         if (KIND == 1) {
-            const rsrc_t rz = make_rsrc(ts.m.zeros + ts.row0 * G, staged ? trows * G : 0);
+            const rsrc_t rz = make_rsrc(tw.m.zeros + tw.row0 * G, staged ? trows * G : 0);
             mv_z = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   rz, tid < G ? uint32_t(tid) * 16 : kOob, 0, 0));
+                                                   rz, sl < G ? uint32_t(sl) * 16 : kOob, 0, 0));
         }
     }
-    Slice<KIND, NG> b;
+    Slice<KIND, NG> bt[TP];
+    Slice<KIND, NG>& b = bt[0];
     if (!staged) load_meta<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln);
-    load_weights<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln, kg);
+#pragma unroll
+    for (int t = 0; t < TP; t++) load_weights<KIND, NG, MODE>(bt[t], p, tsv[t], gbeg, gs, ln, kg);
     // rows [m0, m0 + RR) into the limb records (row m at record row m - m0)
     auto convert_rows = [&](int m0) {
 #pragma unroll
@@ -501,24 +537,55 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     convert_rows(0);
     // (each wave reads only its own limb records; the zero block is shared)
     if (staged) {
-        if (wave * 64 < 2 * G) {
-            if (tid < 2 * G) reinterpret_cast<int4v_t*>(tmeta)[tid] = mv_s;
-            if (KIND == 1 && tid < G) reinterpret_cast<int4v_t*>(tmeta + 32 * G)[tid] = mv_z;
+        if (TP == 1) {
+            if (wave * 64 < 2 * G) {
+                if (tid < 2 * G) reinterpret_cast<int4v_t*>(tmeta)[tid] = mv_s;
+                if (KIND == 1 && tid < G) reinterpret_cast<int4v_t*>(tmeta + 32 * G)[tid] = mv_z;
+            }
+        } else if (wave < TP) {
+            int8_t* tm = tmeta + wave * 48 * G;
+            if (lane < 2 * G) reinterpret_cast<int4v_t*>(tm)[lane] = mv_s;
+            if (KIND == 1 && lane < G) reinterpret_cast<int4v_t*>(tm + 32 * G)[lane] = mv_z;
         }
         __syncthreads();
         // this wave's words: rows ln, groups gbeg .. gbeg + NG (gbeg % 4 == 0)
 #pragma unroll
-        for (int q4 = 0; q4 < NG / 4; q4++) {
-            const int g = 4 * q4 < gs ? gbeg + 4 * q4 : gbeg;
-            const uint2 sv = *reinterpret_cast<const uint2*>(tmeta + (ln * G + g) * 2);
-            b.s[2 * q4] = sv.x;
-            b.s[2 * q4 + 1] = sv.y;
-            b.z[q4] = KIND == 1 ? *reinterpret_cast<const uint32_t*>(tmeta + 32 * G + ln * G + g) : 0u;
+        for (int t = 0; t < TP; t++) {
+            const int8_t* tm = tmeta + t * 48 * G;
+#pragma unroll
+            for (int q4 = 0; q4 < NG / 4; q4++) {
+                const int g = 4 * q4 < gs ? gbeg + 4 * q4 : gbeg;
+                const uint2 sv = *reinterpret_cast<const uint2*>(tm + (ln * G + g) * 2);
+                bt[t].s[2 * q4] = sv.x;
+                bt[t].s[2 * q4 + 1] = sv.y;
+                bt[t].z[q4] = KIND == 1 ? *reinterpret_cast<const uint32_t*>(tm + 32 * G + ln * G + g) : 0u;
+            }
         }
     }
 
     // 3. The slice as it lands; partials through LDS, the last wave to
     //    arrive adds them in slice order (rows k >= KS were never written).
+    if constexpr (TP > 1) {
+        float acc2[TP];
+        slice_dot_tp<KIND, NG, 1, TP>(bt, xs1, ms1, xzero, RS, glo, 1, gbeg, gs, ln, kg, acc2);
+#pragma unroll
+        for (int t = 0; t < TP; t++)
+            if (lane < 16) red[wave][t][lane] = acc2[t];
+        int prior = 0;
+        if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        prior = __builtin_amdgcn_readfirstlane(prior);
+        if (prior != KS - 1 || kg >= TP) return;
+        // lanes 16t .. 16t + 15: tile t
+        float sum = red[0][kg][ln];
+#pragma unroll
+        for (int k = 1; k < MAXW; k++) {
+            const float v = red[k][kg][ln];
+            sum += k < KS ? v : 0.0f;
+        }
+        const TileSel& tt = (TP > 1 && kg) ? tsv[TP - 1] : tsv[0];
+        if (tt.row0 + ln < tt.m.N) tt.m.y[tt.row0 + ln] = sum + __uint_as_float(bias << 16);
+        return;
+    }
     float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, RS, glo, M < RR ? M : RR, gbeg, gs, ln, kg);
     if (lane < 16 * RR) red[wave][0][lane] = acc;
     if constexpr (RB == 2) {
@@ -1066,12 +1133,13 @@ G1Plan gemv1_plan(int64_t G, int kind, int mode, int ntiles, int cus, int R) {
 
 template <int KIND, int NG, int MAXW>
 void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t lds, hipStream_t stream,
-                    bool half = false) {
-#define IQ_G1H(MODE_, R_, KSPLIT_, HALF_)                                                          \
-    do {                                                                                           \
-        allow_big_lds<gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_, HALF_>>();                  \
-        gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_, HALF_><<<grid, 64 * ks, lds, stream>>>(p); \
+                    bool half = false, int tp = 1) {
+#define IQ_G1X(MODE_, R_, KSPLIT_, HALF_, TP_)                                                          \
+    do {                                                                                                \
+        allow_big_lds<gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_, HALF_, TP_>>();                  \
+        gemv1_kernel<KIND, NG, MODE_, MAXW, R_, KSPLIT_, HALF_, TP_><<<grid, 64 * ks, lds, stream>>>(p); \
     } while (0)
+#define IQ_G1H(MODE_, R_, KSPLIT_, HALF_) IQ_G1X(MODE_, R_, KSPLIT_, HALF_, 1)
 #define IQ_G1(MODE_, R_, KSPLIT_) IQ_G1H(MODE_, R_, KSPLIT_, false)
     if (p.M > 4) {
         if constexpr (NG <= 4) IQ_G1(2, 8, false);
@@ -1106,11 +1174,14 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
         }
         return;
     }
-    if (mode == 2) IQ_G1(2, 1, false);
+    if (mode == 2 && tp == 2) {
+        if constexpr (NG == 4 && KIND == 1) IQ_G1X(2, 1, false, false, 2);
+    } else if (mode == 2) IQ_G1(2, 1, false);
     else if (mode == 1) IQ_G1(1, 1, false);
     else IQ_G1(0, 1, false);
 #undef IQ_G1
 #undef IQ_G1H
+#undef IQ_G1X
 }
 
 // The 1-row kernel on n <= kMaxMulti matrices of one kind and width.
@@ -1156,13 +1227,22 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         p.S = 2;
         lds = staged;
     }
-    const unsigned grid = unsigned(pl.grid);
+    // int4, 1 row, staged, 4-group slices: two tiles per workgroup (TP =
+    // 2; 7B gate|up 16.4 -> 15.7 us).  Not int8 (lm_head 88 -> 92-98 us:
+    // two tiles' int8 words take the instance to 97 VGPRs, five waves per
+    // SIMD)
+    int tp = 1;
+    if (W[0].kind == 1 && M == 1 && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 2) {
+        tp = 2;
+        lds += size_t(G) * 48;
+    }
+    const unsigned grid = unsigned(tp == 2 ? (pl.grid + 1) / 2 : pl.grid);
     if (W[0].kind == 1) {
-        if (pl.ng == 4) launch_gemv1_m<1, 4, 16>(p, mode, pl.ks, grid, lds, stream, half);
+        if (pl.ng == 4) launch_gemv1_m<1, 4, 16>(p, mode, pl.ks, grid, lds, stream, half, tp);
         else if (pl.ng == 8) launch_gemv1_m<1, 8, 16>(p, mode, pl.ks, grid, lds, stream, half);
         else launch_gemv1_m<1, 12, 16>(p, mode, pl.ks, grid, lds, stream, half);
     } else {
-        if (pl.ng == 4) launch_gemv1_m<0, 4, 8>(p, mode, pl.ks, grid, lds, stream, half);
+        if (pl.ng == 4) launch_gemv1_m<0, 4, 8>(p, mode, pl.ks, grid, lds, stream, half, tp);
         else if (pl.ng == 8) launch_gemv1_m<0, 8, 8>(p, mode, pl.ks, grid, lds, stream, half);
         else if (pl.ng == 12) launch_gemv1_m<0, 12, 8>(p, mode, pl.ks, grid, lds, stream, half);
         else launch_gemv1_m<0, 20, 8>(p, mode, pl.ks, grid, lds, stream, half);

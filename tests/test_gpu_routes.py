@@ -152,6 +152,26 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
+def test_one_row_two_tiles_per_workgroup():
+    """int4 at 1 row on a wide call (over 4 workgroups per CU, G = 12): two
+    16-row tiles per workgroup.  Matrices of 1025 (ragged), 20, 3 and 1
+    tiles in one call with biases: tile pairs that straddle two matrices,
+    and an odd tile count, so the last workgroup's second tile is past
+    every matrix."""
+    rng = np.random.default_rng(2525)
+    K = 1536
+    Ws = [Packed(rng, N, K, 1) for N in (16389, 309, 48, 5)]
+    bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
+    bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    ys = [out_buffer(1, W.rows) for W in Ws]
+    say("1 row, two tiles per workgroup")
+    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, 1, K, ys)
+    torch.cuda.synchronize()
+    for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
+        check_sampled(y, x, W, 1, rng, f"two tiles[{i}]", bias_bits=bb)
+
+
 @pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [9, 16])
 def test_qkv_7b_multi_gemvh(kind, M):
