@@ -833,16 +833,30 @@ void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, int bm, hipStrea
 // 18944 at T = 80 / 200, fp32 activations: 76.8 / 140.6 -> 60.7 / 111.0
 // us; bf16 activations 50.1 / 94.9 -> 36.6 / 69.4 us; 7B gate 18944 x 3584
 // with bf16 activations at T = 17..48, on the three-term kernel's one
-// workgroup per CU: 29.5..32.6 -> 24.1..27.0 us).
+// workgroup per CU: 29.5..32.6 -> 24.1..27.0 us).  The exception: tiles
+// that fill only half to two thirds of one round, on rows of at least 24
+// groups, take 3 ranges (two full rounds of shorter workgroups; 7B gate at
+// T = 65 / 96 / 128, int8, fp32 activations 78.0 / 72.9 / 73.3 -> 66.4 /
+// 64.9 / 68.7 us, bf16 activations 49.6 / 49.7 / 50.2 -> 41.8 / 43.8 /
+// 46.5 us, int4 8-16 % faster; 1.5B gate 8960 x 1536, 12 groups, at T =
+// 256 lost 38.2 -> 44.5 us).  part_floats: the workspace's partial-sum
+// capacity.
+int pick_splits(int tiles, int slots, int64_t G, int64_t T, int64_t N, int64_t part_floats) {
+    if (tiles >= slots || G < 2) return 1;
+    int S = slots / tiles;
+    S = S > 16 ? 16 : S;
+    while (S > 1 && int64_t(S) * T * N > part_floats) S--;
+    if (S == 1 && 3 * tiles <= 2 * slots && G >= 24 && 3 * T * N <= part_floats) S = 3;
+    return S;
+}
+
 void plan_splits(GemmParams& p, bool fast, int64_t part_floats, int per_cu) {
     p.splits = 1;
     p.kchunk = p.K;
     const int tiles = p.tiles_m * p.tiles_n, want = per_cu * device_cu_count();
     if (!fast || !p.part || tiles >= want) return;
-    int S = want / tiles;
-    S = S > 16 ? 16 : S;
-    while (S > 1 && int64_t(S) * p.T * p.N > part_floats) S--;
     const int64_t G = p.K / kGroup;
+    const int S = pick_splits(tiles, want, G, p.T, p.N, part_floats);
     if (S < 2 || G < 2) return;
     const int64_t gch = (G + S - 1) / S;
     p.kchunk = gch * kGroup;
@@ -850,7 +864,7 @@ void plan_splits(GemmParams& p, bool fast, int64_t part_floats, int per_cu) {
 }
 
 template <int KIND, bool XF32>
-void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t stream) {
+void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, int64_t part_floats, hipStream_t stream) {
     // 128-wide tiles unless they leave CUs without two workgroups to run;
     // with 64-row tiles (short T) always, the K split filling the CUs: each
     // workgroup then re-reads the activations for twice the columns (7B int8
@@ -867,11 +881,11 @@ void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t s
     const bool nj2_rounds = 2 * ((t128 + slots - 1) / slots) <= (t64 + slots - 1) / slots;
     if (t128 >= 2 * device_cu_count() || bm == 64 || nj2_rounds) {
         p.tiles_n = int((p.N + 127) / 128);
-        plan_splits(p, fastw && fastx, kPartialFloats, per_cu);
+        plan_splits(p, fastw && fastx, part_floats, per_cu);
         launch_gemm_t<KIND, XF32, 2>(p, fastw, fastx, bm, stream);
     } else {
         p.tiles_n = int((p.N + 63) / 64);
-        plan_splits(p, fastw && fastx, kPartialFloats, per_cu);
+        plan_splits(p, fastw && fastx, part_floats, per_cu);
         launch_gemm_t<KIND, XF32, 1>(p, fastw, fastx, bm, stream);
     }
     if (p.splits > 1) {
@@ -933,9 +947,7 @@ hipError_t launch_gemmh_chunk(const float* x_f32, const QView& W, const uint16_t
         const int tiles = p.tiles_m * p.tiles_n, want = (bm == 128 ? 1 : 2) * device_cu_count();
         const int64_t G = K / kGroup;
         if (tiles < want && G >= 2) {
-            int S = want / tiles;
-            S = S > 16 ? 16 : S;
-            while (S > 1 && int64_t(S) * T * p.N > kPartialFloats) S--;
+            const int S = pick_splits(tiles, want, G, T, p.N, ws->part_floats);
             if (S >= 2) {
                 const int64_t gch = (G + S - 1) / S;
                 p.kchunk = gch * kGroup;
@@ -1031,11 +1043,11 @@ hipError_t launch_gemm(const float* x_f32, const uint16_t* x_bf16, const QView& 
     const int bm = (short_t && fastw && fastx) ? 64 : (big ? 256 : 128);
     p.tiles_m = int((T + bm - 1) / bm);
     if (x_f32) {
-        if (W.kind == 1) launch_gemm_nj<1, true>(p, fastw, fastx, bm, stream);
-        else launch_gemm_nj<0, true>(p, fastw, fastx, bm, stream);
+        if (W.kind == 1) launch_gemm_nj<1, true>(p, fastw, fastx, bm, ws->part_floats, stream);
+        else launch_gemm_nj<0, true>(p, fastw, fastx, bm, ws->part_floats, stream);
     } else {
-        if (W.kind == 1) launch_gemm_nj<1, false>(p, fastw, fastx, bm, stream);
-        else launch_gemm_nj<0, false>(p, fastw, fastx, bm, stream);
+        if (W.kind == 1) launch_gemm_nj<1, false>(p, fastw, fastx, bm, ws->part_floats, stream);
+        else launch_gemm_nj<0, false>(p, fastw, fastx, bm, ws->part_floats, stream);
     }
     return hipGetLastError();
 }

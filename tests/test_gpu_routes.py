@@ -338,6 +338,29 @@ def test_gemm_t_boundaries(kind):
             check_sampled(y, O.bf16_to_f32(xb), W, T, rng, f"iq_gemm_bf16x {N}x{K} T={T} kind={kind}")
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+def test_gemm_three_k_ranges(kind):
+    """Tiles that fill half to two thirds of one round of workgroup slots,
+    on rows of >= 24 groups, take three K ranges: 7B gate (18944 x 3584) at
+    T = 65 and 128, and a ragged 18000 x 3072 at T = 100, both activation
+    types."""
+    rng = np.random.default_rng(6565 + kind)
+    for N, K, Ts in ((18944, 3584, (65, 128)), (18000, 3072, (100,))):
+        W = Packed(rng, N, K, kind)
+        for T in Ts:
+            x = rng.standard_normal((T, K), dtype=np.float32)
+            say("gemm three K ranges", kind, N, K, T)
+            y = out_buffer(T, N)
+            ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, None, T, K, N, y)
+            torch.cuda.synchronize()
+            check_sampled(y, x, W, T, rng, f"iq_gemm {N}x{K} T={T} kind={kind}")
+            xb = O.f32_to_bf16(x)
+            y = out_buffer(T, N)
+            ops.launch_gemm_bf16x(torch.from_numpy(xb.view(np.int16)).cuda(), W.view, None, T, K, N, y)
+            torch.cuda.synchronize()
+            check_sampled(y, O.bf16_to_f32(xb), W, T, rng, f"iq_gemm_bf16x {N}x{K} T={T} kind={kind}")
+
+
 def test_gemvq_looped_k_ranges():
     """gemvq where one K range per workgroup would need more partial sums
     than the workspace holds, so each workgroup loops over several ranges:
