@@ -839,10 +839,17 @@ void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, int bm, hipStrea
 // T = 65 / 96 / 128, int8, fp32 activations 78.0 / 72.9 / 73.3 -> 66.4 /
 // 64.9 / 68.7 us, bf16 activations 49.6 / 49.7 / 50.2 -> 41.8 / 43.8 /
 // 46.5 us, int4 8-16 % faster; 1.5B gate 8960 x 1536, 12 groups, at T =
-// 256 lost 38.2 -> 44.5 us).  part_floats: the workspace's partial-sum
+// 256 lost 38.2 -> 44.5 us), and so do tiles that fill one round up to 2.5
+// rounds (7B gate at T = 256, int8 / int4: fp32 activations 125.9 / 119.8
+// -> 116.3 / 107.5 us, bf16 84.9 / 95.9 -> 81.8 / 88.9 us; wider ones
+// overrun the partial sums).  part_floats: the workspace's partial-sum
 // capacity.
 int pick_splits(int tiles, int slots, int64_t G, int64_t T, int64_t N, int64_t part_floats) {
-    if (tiles >= slots || G < 2) return 1;
+    if (G < 2) return 1;
+    if (tiles >= slots) {
+        if (2 * tiles < 5 * slots && G >= 24 && 3 * T * N <= part_floats) return 3;
+        return 1;
+    }
     int S = slots / tiles;
     S = S > 16 ? 16 : S;
     while (S > 1 && int64_t(S) * T * N > part_floats) S--;
@@ -854,7 +861,7 @@ void plan_splits(GemmParams& p, bool fast, int64_t part_floats, int per_cu) {
     p.splits = 1;
     p.kchunk = p.K;
     const int tiles = p.tiles_m * p.tiles_n, want = per_cu * device_cu_count();
-    if (!fast || !p.part || tiles >= want) return;
+    if (!fast || !p.part) return;
     const int64_t G = p.K / kGroup;
     const int S = pick_splits(tiles, want, G, p.T, p.N, part_floats);
     if (S < 2 || G < 2) return;
@@ -938,15 +945,15 @@ hipError_t launch_gemmh_chunk(const float* x_f32, const QView& W, const uint16_t
     const int bm = wide_t ? 128 : 64;
     p.tiles_m = int((T + bm - 1) / bm);
     p.tiles_n = int((p.N + 127) / 128);
-    // K ranges when the tiles leave CUs without two workgroups
+    // K ranges (pick_splits)
     p.splits = 1;
     p.kchunk = K;
     {
-        // (one round of workgroup slots, as plan_splits: 1.5B o 1536 x
-        // 1536 at T = 80 / 256 18.5 / 23.0 -> 13.6 / 16.5 us)
+        // (as plan_splits: 1.5B o 1536 x 1536 at T = 80 / 256 18.5 / 23.0
+        // -> 13.6 / 16.5 us)
         const int tiles = p.tiles_m * p.tiles_n, want = (bm == 128 ? 1 : 2) * device_cu_count();
         const int64_t G = K / kGroup;
-        if (tiles < want && G >= 2) {
+        if (G >= 2) {
             const int S = pick_splits(tiles, want, G, T, p.N, ws->part_floats);
             if (S >= 2) {
                 const int64_t gch = (G + S - 1) / S;

@@ -341,11 +341,11 @@ def test_gemm_t_boundaries(kind):
 @pytest.mark.parametrize("kind", [0, 1])
 def test_gemm_three_k_ranges(kind):
     """Tiles that fill half to two thirds of one round of workgroup slots,
-    on rows of >= 24 groups, take three K ranges: 7B gate (18944 x 3584) at
-    T = 65 and 128, and a ragged 18000 x 3072 at T = 100, both activation
-    types."""
+    or one to 2.5 rounds, on rows of >= 24 groups, take three K ranges: 7B
+    gate (18944 x 3584) at T = 65, 128 and 256, and a ragged 18000 x 3072
+    at T = 100 and 250, both activation types."""
     rng = np.random.default_rng(6565 + kind)
-    for N, K, Ts in ((18944, 3584, (65, 128)), (18000, 3072, (100,))):
+    for N, K, Ts in ((18944, 3584, (65, 128, 256)), (18000, 3072, (100, 250))):
         W = Packed(rng, N, K, kind)
         for T in Ts:
             x = rng.standard_normal((T, K), dtype=np.float32)
