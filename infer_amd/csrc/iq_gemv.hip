@@ -191,14 +191,16 @@ struct ProScale {
     }
 };
 
-// bf16 norm weights of columns [c, c + 8) applied to v (PRO with norm).
-__device__ __forceinline__ void pro_norm8(float (&v)[8], uint4 nw, float r) {
+// bf16 norm weights of columns [c, c + 8) applied to v (PRO with norm; the
+// row factor r_m multiplies the group factors of the split operands
+// instead, so the conversion need not wait for it).
+__device__ __forceinline__ void pro_norm8(float (&v)[8], uint4 nw) {
     const uint32_t w4[4] = {nw.x, nw.y, nw.z, nw.w};
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const uint32_t h = w4[i >> 1];
         const float wn = __uint_as_float((i & 1) ? (h & 0xFFFF0000u) : (h << 16));
-        v[i] = (v[i] * r) * wn;
+        v[i] = v[i] * wn;
     }
 }
 
@@ -1522,8 +1524,9 @@ __global__ __launch_bounds__(256) void xhprep_kernel(const float* __restrict__ x
 // input: activation row m read through the prologue's gather and RMSNorm
 // (pro_x_offset, pro_norm8).  Each wave takes one (row, 4 groups) and
 // computes its row's factor r_m itself, in ProScale's order (lane j < 16
-// adds partials j, j + 16, ... in double, then the 16 sums in order), so
-// the operands equal those the prologue instances make.
+// adds partials j, j + 16, ... in double, then the 16 sums in order), and
+// multiplies the group factor by it after the split, so the operands and
+// factors equal those the prologue instances make.
 template <bool PERM>
 __global__ __launch_bounds__(256) void xhprep_pro_kernel(const GemvParams p, int64_t quads, int nb,
                                                          _Float16* __restrict__ xh, float* __restrict__ xfx) {
@@ -1546,6 +1549,7 @@ __global__ __launch_bounds__(256) void xhprep_pro_kernel(const GemvParams p, int
         v[e] = a[e];
         v[4 + e] = bq[e];
     }
+    float r = 1.0f;
     if (p.norm) {  // uniform
         const rsrc_t rn = make_rsrc(p.norm, p.K * 2);
         const uint4 nw = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rn, ok ? uint32_t(c) * 2 : kOob, 0, 0));
@@ -1558,15 +1562,17 @@ __global__ __launch_bounds__(256) void xhprep_pro_kernel(const GemvParams p, int
                                                            rq, (lane < 16 && m < M && bb < p.ssq_n) ? uint32_t(m * p.ssq_n + bb) * 4 : kOob, 0, 0));
             part += double(sq);
         }
+        // the operands split x w; r_m joins the group factor after the split
+        pro_norm8(v, nw);
         double ss = 0.0;
 #pragma unroll
         for (int j = 0; j < 16; j++) ss += __shfl(part, j, 64);
-        const float r = 1.0f / __builtin_sqrtf(float(ss / double(p.K)) + p.eps);
-        pro_norm8(v, nw, r);
+        r = 1.0f / __builtin_sqrtf(float(ss / double(p.K)) + p.eps);
     }
     half8_t ho, lo2;
     float fac;
     xh_split8<PERM>(v, ho, lo2, fac);
+    fac *= r;
     if (g >= G) return;
     const int b = m >> 4, i = m & 15, q = j16 >> 2, jj = j16 & 3;
     _Float16* base = xh + ((int64_t(b) * G + g) * kHGroupBytes) / 2;
@@ -1966,18 +1972,17 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : ((PRO && KIND == 0 && !PK) ? 2 : 
     }
     // 2. the operands and factors of the range (all 16 lanes of each
     //    (row, group) together), then one barrier
+    //    (with RMSNorm: the operands split x w, and the row factor r_m joins
+    //    the group factor once the producer's sums of squares are added)
     __shared__ double rsp[PRO ? kMaxRowsGemv : 1][16];
     __shared__ float rsc[PRO ? kMaxRowsGemv : 1];
-    if constexpr (PRO) {
-        if (p.norm) psc.finish(p, tid, rsp, rsc);  // workgroup-uniform
-    }
 #pragma unroll
     for (int u = 0; u < NX; u++) {
         const int t = tid + 512 * u, j16 = t & 15, pr = t >> 4;
         const int m = PK ? pr & 7 : pr & 15, i = PK ? pr >> 3 : pr >> 4;
         const int qq = j16 >> 2, jj = j16 & 3;
         if constexpr (PRO) {
-            if (p.norm) pro_norm8(xv[u], nwv[u], rsc[m < p.M ? m : 0]);
+            if (p.norm) pro_norm8(xv[u], nwv[u]);
         }
         half8_t ho, lo;
         float fac;
@@ -1991,6 +1996,18 @@ __global__ __launch_bounds__(512, NG > 8 ? 1 : ((PRO && KIND == 0 && !PK) ? 2 : 
             dst[(jj * 2 + 1) * CS + m + 16 * qq] = lo;
         }
         if (j16 == 0) reinterpret_cast<float*>(Fs[i])[m] = fac;
+    }
+    if constexpr (PRO) {
+        if (p.norm) {  // workgroup-uniform
+            psc.finish(p, tid, rsp, rsc);
+            // (each factor rescaled by the thread that stored it)
+#pragma unroll
+            for (int u = 0; u < NX; u++) {
+                const int t = tid + 512 * u, j16 = t & 15, pr = t >> 4;
+                const int m = PK ? pr & 7 : pr & 15, i = PK ? pr >> 3 : pr >> 4;
+                if (j16 == 0) reinterpret_cast<float*>(Fs[i])[m] *= rsc[m < p.M ? m : 0];
+            }
+        }
     }
     __syncthreads();
 
@@ -2179,16 +2196,15 @@ __global__ __launch_bounds__(512, (PRO && (LOOP || (KIND == 0 && MB == 2))) ? 2 
 
         // 2. the range's operands and factors (16 lanes per (row, group)):
         //    octet j16 = 8 h' + c of row m goes to chunk c, lanes m + 32 h'
-        //    (hi) and m + 16 + 32 h' (lo); then one barrier
-        if constexpr (PRO) {
-            if (it == 0 && p.norm) psc.finish(p, tid, rsp, rsc);  // workgroup-uniform
-        }
+        //    (hi) and m + 16 + 32 h' (lo); then one barrier.  With RMSNorm
+        //    the operands split x w and the row factor r_m joins the group
+        //    factor afterwards, so the conversion does not wait for the
+        //    producer's sums of squares.
 #pragma unroll
         for (int u = 0; u < NX; u++) {
             const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG, b = (t >> 8) / NG;
             if constexpr (PRO) {
-                const int row = 16 * b + m;
-                if (p.norm) pro_norm8(xv[u], nwv[u], rsc[row < p.M ? row : 0]);
+                if (p.norm) pro_norm8(xv[u], nwv[u]);
             }
             half8_t ho, lo;
             float fac;
@@ -2196,6 +2212,18 @@ __global__ __launch_bounds__(512, (PRO && (LOOP || (KIND == 0 && MB == 2))) ? 2 
             Aq[b][i][j16 & 7][m + 32 * (j16 >> 3)] = ho;
             Aq[b][i][j16 & 7][m + 16 + 32 * (j16 >> 3)] = lo;
             if (j16 == 0) Fq[b][i][m] = fac;
+        }
+        if constexpr (PRO) {
+            if (p.norm) {  // workgroup-uniform
+                if (it == 0) psc.finish(p, tid, rsp, rsc);
+                // (each factor rescaled by the thread that stored it)
+#pragma unroll
+                for (int u = 0; u < NX; u++) {
+                    const int t = tid + 512 * u, j16 = t & 15, m = (t >> 4) & 15, i = (t >> 8) % NG, b = (t >> 8) / NG;
+                    const int row = 16 * b + m;
+                    if (j16 == 0) Fq[b][i][m] *= rsc[row < p.M ? row : 0];
+                }
+            }
         }
         __syncthreads();
 
