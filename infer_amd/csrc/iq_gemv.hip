@@ -129,13 +129,15 @@ struct GemvParams {
     float* part;
     int M, S, gs, nrb;
     int ntiles;  // 1-row kernel: 16-row tiles over all matrices
+    int th;      // 1-row kernel, one row: rows per tile (8..16; 0: 16)
     int kr, gr;  // 1-row kernel: K ranges (workgroups per tile) and groups per range;
                  // gemvq: kr consecutive K ranges per workgroup
     // Chain prologue (gemvr / gemvq instances with PRO): activation row m,
     // column c is x[m * xstride + c], or with gqa_span > 0 the value row of
     // c's key/value head, x[m * xstride + (c / gqa_span) * gqa_hd + c % gqa_hd];
-    // with norm, RMSNorm'd: (x * r_m) * norm[c], r_m = 1 / sqrt(sum_b
-    // ssq[m][b] / K + eps) over the ssq_n partial sums of squares of row m.
+    // with norm, RMSNorm'd: x * norm[c] is split into the operands and r_m =
+    // 1 / sqrt(sum_b ssq[m][b] / K + eps), over the ssq_n partial sums of
+    // squares of row m, multiplies the group factors.
     // to_part: K-range partial sums are written even when S == 1.
     int64_t xstride;
     int gqa_hd, gqa_span;
@@ -247,12 +249,12 @@ struct TileSel {
     int64_t row0;
 };
 
-__device__ __forceinline__ TileSel select_tile(const GemvParams& p, int tile) {
+__device__ __forceinline__ TileSel select_tile(const GemvParams& p, int tile, int th = 16) {
     MatRef m = p.mat[0];
 #pragma unroll
     for (int i = 1; i < kMaxMulti; i++)
         if (i < p.nmat && tile >= p.mat[i].tile0) m = p.mat[i];
-    return TileSel{m, int64_t(tile - m.tile0) * 16};
+    return TileSel{m, int64_t(tile - m.tile0) * th};
 }
 
 // The loads of one wave's slice [gbeg, gbeg + gs) of the tile at row0
@@ -267,7 +269,7 @@ __device__ __forceinline__ TileSel select_tile(const GemvParams& p, int tile) {
 // workgroup stages the tile's scales and zero points in LDS.
 template <int KIND, int NG, int MODE>
 __device__ __forceinline__ void load_meta(Slice<KIND, NG>& b, const GemvParams& p, const TileSel& ts, int gbeg,
-                                          int gs, int ln) {
+                                          int gs, int ln, bool live = true) {
     const int G = int(p.G);
     const MatRef& mr = ts.m;
     const int64_t row = ts.row0 + ln;
@@ -283,7 +285,7 @@ __device__ __forceinline__ void load_meta(Slice<KIND, NG>& b, const GemvParams& 
     if (MODE == 2) {
 #pragma unroll
         for (int q4 = 0; q4 < NG / 4; q4++) {
-            const uint32_t ok = 4 * q4 < gs ? 0u : kOob;
+            const uint32_t ok = (4 * q4 < gs && live) ? 0u : kOob;
             const auto sv = __builtin_amdgcn_raw_buffer_load_b64(rs, vs + ok, q4 * 8, 0);
             b.s[2 * q4] = sv[0];
             b.s[2 * q4 + 1] = sv[1];
@@ -293,7 +295,7 @@ __device__ __forceinline__ void load_meta(Slice<KIND, NG>& b, const GemvParams& 
         uint32_t sh[NG], zb[NG];
 #pragma unroll
         for (int gl = 0; gl < NG; gl++) {
-            const uint32_t ok = gl < gs ? 0u : kOob;
+            const uint32_t ok = (gl < gs && live) ? 0u : kOob;
             sh[gl] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs + ok, gl * 2, 0);
             zb[gl] = KIND == 1 ? __builtin_amdgcn_raw_buffer_load_b8(rz, vz + ok, gl, 0) : 0u;
         }
@@ -307,7 +309,7 @@ __device__ __forceinline__ void load_meta(Slice<KIND, NG>& b, const GemvParams& 
 
 template <int KIND, int NG, int MODE>
 __device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParams& p, const TileSel& ts, int gbeg,
-                                             int gs, int ln, int kg) {
+                                             int gs, int ln, int kg, bool live = true) {
     constexpr int WPG = Slice<KIND, NG>::WPG;
     const int row_bytes = int(KIND == 1 ? p.K / 2 : p.K);
     const MatRef& mr = ts.m;
@@ -330,7 +332,7 @@ __device__ __forceinline__ void load_weights(Slice<KIND, NG>& b, const GemvParam
         const uint32_t vq = uint32_t(row * row_bytes) + uint32_t(gbeg * (KIND == 1 ? 64 : 128) + kg * 16);
 #pragma unroll
         for (int gl = 0; gl < NG; gl++) {
-            const uint32_t vo = vq + (gl < gs ? 0u : kOob);
+            const uint32_t vo = vq + ((gl < gs && live) ? 0u : kOob);
 #pragma unroll
             for (int h = 0; h < WPG; h++)
                 b.w[gl][h] = __builtin_bit_cast(int4v_t, __builtin_amdgcn_raw_buffer_load_b128(
@@ -452,11 +454,16 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     int4* ms1 = reinterpret_cast<int4*>(xs1 + RR * RS * kLimbRec);
     int8_t* tmeta = xs1 + (RR * kLimbRec + R * 16) * RS;
     const int tile = KSPLIT ? int(blockIdx.x) / kr : int(blockIdx.x) * TP;
+    // rows per tile: th (1 row, one tile per workgroup, 16-byte rows: p.th
+    // when set, so that narrow matrices fill every CU), else 16; lanes
+    // ln >= th read nothing and store nothing
+    const int th = (R == 1 && TP == 1 && !KSPLIT && MODE == 2 && p.th) ? p.th : 16;
+    const bool live = ln < th;
     // (TP = 2, odd tile count: the last workgroup's second tile starts past
     // its matrix's rows, so its loads read zero and nothing is stored)
     TileSel tsv[TP];
 #pragma unroll
-    for (int t = 0; t < TP; t++) tsv[t] = select_tile(p, tile + t);
+    for (int t = 0; t < TP; t++) tsv[t] = select_tile(p, tile + t, th);
     const TileSel& ts = tsv[0];
     const bool staged = MODE == 2 && (TP > 1 || p.S == 2);  // (only with kr == 1)
 
@@ -472,7 +479,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     for (int t = 0; t < TP; t++) {
         // (TP = 2: lanes 16t .. 16t + 15 take tile t's; the others read zero)
         const rsrc_t rb = make_rsrc(tsv[t].m.bias, tsv[t].m.bias ? tsv[t].m.N * 2 : 0);
-        const bool mine = TP == 1 ? lane < 16 * (M < 4 ? M : 4) : kg == t;
+        const bool mine = (TP == 1 ? lane < 16 * (M < 4 ? M : 4) : kg == t) && live;
         bias |= __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(tsv[t].row0 + ln) * 2 : kOob, 0, 0);
     }
     constexpr int XP = NG / 4;
@@ -502,7 +509,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     if constexpr (MODE == 2) {
         const int wt = TP == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave < TP ? wave : 0);
         const TileSel tw = (TP > 1 && wt) ? tsv[TP - 1] : tsv[0];
-        int64_t trows = tw.m.N - tw.row0 < 16 ? tw.m.N - tw.row0 : 16;
+        int64_t trows = tw.m.N - tw.row0 < th ? tw.m.N - tw.row0 : th;
         trows = trows > 0 ? trows : 0;
         const int sl = TP == 1 ? tid : (wave < TP ? lane : 64);  // 16-byte chunk of this thread
         const rsrc_t rs = make_rsrc(tw.m.scales + tw.row0 * G, staged ? trows * G * 2 : 0);
@@ -516,9 +523,9 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     }
     Slice<KIND, NG> bt[TP];
     Slice<KIND, NG>& b = bt[0];
-    if (!staged) load_meta<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln);
+    if (!staged) load_meta<KIND, NG, MODE>(b, p, ts, gbeg, gs, ln, live);
 #pragma unroll
-    for (int t = 0; t < TP; t++) load_weights<KIND, NG, MODE>(bt[t], p, tsv[t], gbeg, gs, ln, kg);
+    for (int t = 0; t < TP; t++) load_weights<KIND, NG, MODE>(bt[t], p, tsv[t], gbeg, gs, ln, kg, live);
     // rows [m0, m0 + RR) into the limb records (row m at record row m - m0)
     auto convert_rows = [&](int m0) {
 #pragma unroll
@@ -613,7 +620,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
             const float v = red[k][rb][lane];
             sum += k < KS ? v : 0.0f;
         }
-        if (ts.row0 + ln >= ts.m.N) continue;
+        if (ts.row0 + ln >= ts.m.N || !live) continue;
         if (kr == 1) ts.m.y[int64_t(m) * ts.m.N + ts.row0 + ln] = sum + __uint_as_float(bias << 16);
         else p.part[(int64_t(range) * M + m) * (int64_t(p.ntiles) * 16) + int64_t(tile) * 16 + ln] = sum;
     }
@@ -1238,7 +1245,28 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         tp = 2;
         lds += size_t(G) * 48;
     }
-    const unsigned grid = unsigned(tp == 2 ? (pl.grid + 1) / 2 : pl.grid);
+    unsigned grid = unsigned(tp == 2 ? (pl.grid + 1) / 2 : pl.grid);
+    // 1 row on fewer 16-row tiles than CUs (one tile per workgroup, 16-byte
+    // rows): the tallest tiles of 8..15 rows that give every CU one (7B
+    // down and o, 224 tiles of 16 rows: 256 of 14; down 11.95 -> 11.78 us,
+    // step 1188 -> 1179 us; the 1.5B set, 96..128 tiles, unchanged)
+    p.th = 0;
+    if (M == 1 && tp == 1 && pl.kr == 1 && mode == 2 && tiles < device_cu_count()) {
+        int th = 15;
+        auto count = [&](int h) {
+            int t = 0;
+            for (int i = 0; i < n; i++) t += int((W[i].rows + h - 1) / h);
+            return t;
+        };
+        while (th > 8 && count(th) < device_cu_count()) th--;
+        int t0 = 0;
+        for (int i = 0; i < n; i++) {
+            p.mat[i].tile0 = t0;
+            t0 += int((W[i].rows + th - 1) / th);
+        }
+        p.th = th;
+        grid = unsigned(t0);
+    }
     if (W[0].kind == 1) {
         if (pl.ng == 4) launch_gemv1_m<1, 4, 16>(p, mode, pl.ks, grid, lds, stream, half, tp);
         else if (pl.ng == 8) launch_gemv1_m<1, 8, 16>(p, mode, pl.ks, grid, lds, stream, half);

@@ -173,6 +173,26 @@ def test_one_row_two_tiles_per_workgroup():
 
 
 @pytest.mark.parametrize("kind", [0, 1])
+def test_one_row_short_tiles(kind):
+    """1 row on fewer 16-row tiles than CUs: tiles of 8..15 rows, one per
+    workgroup.  Ragged matrices in one call with biases (1530 + 250 + 250
+    rows, K = 1536: 8-row tiles) and 7B down alone (3584 x 18944: 14-row
+    tiles)."""
+    rng = np.random.default_rng(1414 + kind)
+    for K, Ns in ((1536, (1530, 250, 250)), (18944, (3584,))):
+        Ws = [Packed(rng, N, K, kind) for N in Ns]
+        bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
+        bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+        x = rng.standard_normal((1, K), dtype=np.float32)
+        ys = [out_buffer(1, W.rows) for W in Ws]
+        say("1 row, short tiles", kind, K, Ns)
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, 1, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
+            check_sampled(y, x, W, 1, rng, f"short tiles[{i}] K={K} kind={kind}", bias_bits=bb)
+
+
+@pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [9, 16])
 def test_qkv_7b_multi_gemvh(kind, M):
     """q|k|v of one 7B layer (3584 + 512 + 512 rows x 3584, 288 tiles) in
