@@ -454,10 +454,10 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     int4* ms1 = reinterpret_cast<int4*>(xs1 + RR * RS * kLimbRec);
     int8_t* tmeta = xs1 + (RR * kLimbRec + R * 16) * RS;
     const int tile = KSPLIT ? int(blockIdx.x) / kr : int(blockIdx.x) * TP;
-    // rows per tile: th (1 row, one tile per workgroup, 16-byte rows: p.th
+    // rows per tile: th (1 row, one tile per workgroup, whole groups: p.th
     // when set, so that narrow matrices fill every CU), else 16; lanes
     // ln >= th read nothing and store nothing
-    const int th = (R == 1 && TP == 1 && !KSPLIT && MODE == 2 && p.th) ? p.th : 16;
+    const int th = (R == 1 && TP == 1 && !KSPLIT && MODE >= 1 && p.th) ? p.th : 16;
     const bool live = ln < th;
     // (TP = 2, odd tile count: the last workgroup's second tile starts past
     // its matrix's rows, so its loads read zero and nothing is stored)
@@ -1252,12 +1252,12 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         lds += size_t(G) * 48;
     }
     unsigned grid = unsigned(tp == 2 ? (pl.grid + 1) / 2 : pl.grid);
-    // 1 row on fewer 16-row tiles than CUs (one tile per workgroup, 16-byte
-    // rows): the tallest tiles of 8..15 rows that give every CU one (7B
+    // 1 row on fewer 16-row tiles than CUs (one tile per workgroup, whole
+    // groups): the tallest tiles of 8..15 rows that give every CU one (7B
     // down and o, 224 tiles of 16 rows: 256 of 14; down 11.95 -> 11.78 us,
-    // step 1188 -> 1179 us; the 1.5B set, 96..128 tiles, unchanged)
+    // step 1188 -> 1179 us; 1.5B down, 96 tiles: 192 of 8, 8.5 -> 7.7 us)
     p.th = 0;
-    if (M == 1 && tp == 1 && pl.kr == 1 && mode == 2 && tiles < device_cu_count()) {
+    if (M == 1 && tp == 1 && pl.kr == 1 && mode >= 1 && tiles < device_cu_count()) {
         int th = 15;
         auto count = [&](int h) {
             int t = 0;

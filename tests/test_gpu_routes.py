@@ -176,10 +176,11 @@ def test_one_row_two_tiles_per_workgroup():
 def test_one_row_short_tiles(kind):
     """1 row on fewer 16-row tiles than CUs: tiles of 8..15 rows, one per
     workgroup.  Ragged matrices in one call with biases (1530 + 250 + 250
-    rows, K = 1536: 8-row tiles) and 7B down alone (3584 x 18944: 14-row
-    tiles)."""
+    rows, K = 1536: 8-row tiles), 7B down alone (3584 x 18944: 14-row
+    tiles) and 1.5B down (1536 x 8960, 70 groups: per-group metadata loads,
+    8-row tiles)."""
     rng = np.random.default_rng(1414 + kind)
-    for K, Ns in ((1536, (1530, 250, 250)), (18944, (3584,))):
+    for K, Ns in ((1536, (1530, 250, 250)), (18944, (3584,)), (8960, (1536,))):
         Ws = [Packed(rng, N, K, kind) for N in Ns]
         bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
         bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
