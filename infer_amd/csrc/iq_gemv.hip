@@ -1242,12 +1242,13 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         p.S = 2;
         lds = staged;
     }
-    // int4, 1 row, staged, 4-group slices: two tiles per workgroup (TP =
-    // 2; 7B gate|up 16.4 -> 15.7 us).  Not int8 (lm_head 88 -> 92-98 us:
-    // two tiles' int8 words take the instance to 97 VGPRs, five waves per
-    // SIMD)
+    // int4, 1 row, staged, 4-group slices, >= 6 waves: two tiles per
+    // workgroup (TP = 2; 7B gate|up, 7 waves, 16.4 -> 15.7 us; 1.5B
+    // gate|up, 3 waves, lost: 6.2 -> 6.7 us).  Not int8 (lm_head 88 ->
+    // 92-98 us: two tiles' int8 words take the instance to 97 VGPRs, five
+    // waves per SIMD)
     int tp = 1;
-    if (W[0].kind == 1 && M == 1 && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 2) {
+    if (W[0].kind == 1 && M == 1 && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 6) {
         tp = 2;
         lds += size_t(G) * 48;
     }

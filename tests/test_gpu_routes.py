@@ -153,13 +153,13 @@ def test_gate_up_7b_multi(kind, M):
 
 
 def test_one_row_two_tiles_per_workgroup():
-    """int4 at 1 row on a wide call (over 4 workgroups per CU, G = 12): two
-    16-row tiles per workgroup.  Matrices of 1025 (ragged), 20, 3 and 1
-    tiles in one call with biases: tile pairs that straddle two matrices,
-    and an odd tile count, so the last workgroup's second tile is past
-    every matrix."""
+    """int4 at 1 row on a wide call (over 4 workgroups per CU, G = 24: six
+    waves of 4 groups): two 16-row tiles per workgroup.  Matrices of 1025
+    (ragged), 20, 3 and 1 tiles in one call with biases: tile pairs that
+    straddle two matrices, and an odd tile count, so the last workgroup's
+    second tile is past every matrix."""
     rng = np.random.default_rng(2525)
-    K = 1536
+    K = 3072
     Ws = [Packed(rng, N, K, 1) for N in (16389, 309, 48, 5)]
     bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
     bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
