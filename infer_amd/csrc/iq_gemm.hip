@@ -564,7 +564,8 @@ __global__ __launch_bounds__(512) void gemm_xprep_kernel(const float* __restrict
 // the step after next in registers), on the prepared fp16 operands (LO: hi
 // and lo, two MFMAs per weight operand).  K % 128 == 0.
 // NR: K steps whose loads are in flight in registers (2, or 4 for short
-// T, where each workgroup's steps wait on memory rather than on the MFMAs)
+// T, where each workgroup's steps wait on memory rather than on the MFMAs,
+// and for int8 on 128-row tiles)
 template <int KIND, bool LO, int NJ, int BM, int NR = 2>
 __global__ __launch_bounds__(BM >= 128 ? 2 * kThreads : kThreads, (BM == 256 || LO) ? 1 : 2) void gemmh_kernel(
     const GemmhParams p) {
@@ -964,8 +965,11 @@ hipError_t launch_gemmh_chunk(const float* x_f32, const QView& W, const uint16_t
     }
     const unsigned ggrid = unsigned(p.tiles_m * p.tiles_n * p.splits);
     if (bm == 128) {
+        // (int8 with four K steps in flight, int4 with two: 7B at T = 512 /
+        // 1024 / 2048, int8 gate|up 392 / 789 / 1526 -> 374 / 748 / 1446 us,
+        // down 212 / 374 / 756 -> 199 / 352 / 714 us; int4 3-5 % slower so)
         if (W.kind == 1) gemmh_kernel<1, true, 2, 128><<<ggrid, 2 * kThreads, 0, stream>>>(p);
-        else gemmh_kernel<0, true, 2, 128><<<ggrid, 2 * kThreads, 0, stream>>>(p);
+        else gemmh_kernel<0, true, 2, 128, 4><<<ggrid, 2 * kThreads, 0, stream>>>(p);
     } else {
         if (W.kind == 1) gemmh_kernel<1, true, 2, 64, 4><<<ggrid, kThreads, 0, stream>>>(p);
         else gemmh_kernel<0, true, 2, 64, 4><<<ggrid, kThreads, 0, stream>>>(p);
