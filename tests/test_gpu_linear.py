@@ -32,6 +32,26 @@ def test_reference_shapes(kind, T, bias):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
+def test_tiny_shapes_every_row_count(kind):
+    """Matrices smaller than one 16-row tile or one 4-group block (1, 7 and
+    33 output rows; 128, 256 and ragged 130 / 640 columns) at every row
+    count 1..32 through the reference's linear_b routing (GEMV to 32 rows),
+    with a bias: every route's ragged edge, the short 1-row tiles on
+    matrices of a tile or two, and K of one group."""
+    rng = np.random.default_rng(31337 + kind)
+    for N, K in ((1, 128), (7, 256), (33, 130), (33, 640), (17, 384)):
+        W = QFix(rng, N, K, kind)
+        bb, bd = bias_of(rng, N)
+        for M in range(1, 33):
+            x = rng.standard_normal((M, K), dtype=np.float32)
+            y = out_buffer(M, N)
+            say("tiny shapes", kind, N, K, M)
+            ops.launch_linear_q(torch.from_numpy(x).cuda(), W.view, bd, M, K, N, y)
+            torch.cuda.synchronize()
+            check_linear(y, x, W, bb, M, f"tiny kind={kind} {N}x{K} M={M}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 12, 16, 17, 32])
 def test_gemv_15b_mlp_shapes(kind, M):
     rng = np.random.default_rng(77 + M)
