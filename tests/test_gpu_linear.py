@@ -52,6 +52,30 @@ def test_tiny_shapes_every_row_count(kind):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
+def test_tiny_shapes_prefill(kind):
+    """The prefill GEMM on matrices smaller than one output tile (1, 7 and
+    33 rows; K of one group, ragged 130 and 640) at T = 33, 64, 65, 128,
+    129 and 300, fp32 activations through linear_b and bf16 activations
+    through iq_gemm_bf16x, with a bias on the fp32 calls."""
+    rng = np.random.default_rng(4242 + kind)
+    for N, K in ((1, 128), (7, 256), (33, 130), (33, 640)):
+        W = QFix(rng, N, K, kind)
+        bb, bd = bias_of(rng, N)
+        for T in (33, 64, 65, 128, 129, 300):
+            x = rng.standard_normal((T, K), dtype=np.float32)
+            y = out_buffer(T, N)
+            say("tiny prefill", kind, N, K, T)
+            ops.launch_linear_q(torch.from_numpy(x).cuda(), W.view, bd, T, K, N, y)
+            torch.cuda.synchronize()
+            check_linear(y, x, W, bb, T, f"tiny prefill kind={kind} {N}x{K} T={T}")
+            xb = O.f32_to_bf16(x)
+            y = out_buffer(T, N)
+            ops.launch_gemm_bf16x(torch.from_numpy(xb.view(np.int16)).cuda(), W.view, None, T, K, N, y)
+            torch.cuda.synchronize()
+            check_linear(y, O.bf16_to_f32(xb), W, None, T, f"tiny prefill bf16 kind={kind} {N}x{K} T={T}")
+
+
+@pytest.mark.parametrize("kind", [0, 1])
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 12, 16, 17, 32])
 def test_gemv_15b_mlp_shapes(kind, M):
     rng = np.random.default_rng(77 + M)
