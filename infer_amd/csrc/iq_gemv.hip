@@ -422,10 +422,11 @@ __device__ __forceinline__ float slice_dot(const Slice<KIND, NG>& b, const int8_
 // instead of every wave fetching the same lines for its slice.  The slice partials are added
 // through LDS by whichever wave finishes last (an LDS counter), in slice
 // order, so the sum is deterministic and no wave waits for the others.
-// TP = 2 (1 row, staged metadata, G <= 32): the workgroup owns tiles 2b
-// and 2b + 1 (wave t < 2 stages tile t's scales and zero points); each wave
-// requests both tiles' slices and multiplies them by the same activation
-// limbs, so one conversion of x and one LDS operand read serve 32 rows.
+// TP = 2 (1 or 2 rows, staged metadata, G <= 32): the workgroup owns tiles
+// 2b and 2b + 1 (wave t < 2 stages tile t's scales and zero points); each
+// wave requests both tiles' slices and multiplies them by the same
+// activation limbs, so one conversion of x and one LDS operand read serve
+// 32 rows.
 template <int KIND, int NG, int MODE, int MAXW, int R, bool KSPLIT, bool HALF = false, int TP = 1>
 __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // dynamic LDS: limbs [RR][G][512], meta [R][G] int4, then (staged) the
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // records (each wave reuses its own groups' records; the weights stay
     // in registers): half the LDS of one block of R rows.
     static_assert(!HALF || (R == 4 && !KSPLIT), "two 2-row blocks: the 4-row instance, one K range");
-    static_assert(TP == 1 || (R == 1 && MODE == 2 && !KSPLIT), "two tiles: 1 row, staged metadata");
+    static_assert(TP == 1 || (R <= 2 && MODE == 2 && !KSPLIT), "two tiles: 1 or 2 rows, staged metadata");
     constexpr int RR = HALF ? R / 2 : (R < 4 ? R : 4);  // rows per block
     constexpr int RB = R / RR;                          // blocks
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     for (int t = 0; t < TP; t++) {
         // (TP = 2: lanes 16t .. 16t + 15 take tile t's; the others read zero)
         const rsrc_t rb = make_rsrc(tsv[t].m.bias, tsv[t].m.bias ? tsv[t].m.N * 2 : 0);
-        const bool mine = (TP == 1 ? lane < 16 * (M < 4 ? M : 4) : kg == t) && live;
+        const bool mine = (TP == 1 ? lane < 16 * (M < 4 ? M : 4) : kg / RR == t) && live;
         bias |= __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(tsv[t].row0 + ln) * 2 : kOob, 0, 0);
     }
     constexpr int XP = NG / 4;
@@ -576,23 +577,24 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     //    arrive adds them in slice order (rows k >= KS were never written).
     if constexpr (TP > 1) {
         float acc2[TP];
-        slice_dot_tp<KIND, NG, 1, TP>(bt, xs1, ms1, xzero, RS, glo, 1, gbeg, gs, ln, kg, acc2);
+        slice_dot_tp<KIND, NG, RR, TP>(bt, xs1, ms1, xzero, RS, glo, M < RR ? M : RR, gbeg, gs, ln, kg, acc2);
 #pragma unroll
         for (int t = 0; t < TP; t++)
-            if (lane < 16) red[wave][t][lane] = acc2[t];
+            if (lane < 16 * RR) red[wave][t][lane] = acc2[t];
         int prior = 0;
         if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
         prior = __builtin_amdgcn_readfirstlane(prior);
-        if (prior != KS - 1 || kg >= TP) return;
-        // lanes 16t .. 16t + 15: tile t
-        float sum = red[0][kg][ln];
+        // lane group kg = RR t + m: tile t, activation row m
+        const int tq = kg / RR, m = kg % RR;
+        if (prior != KS - 1 || tq >= TP || m >= M) return;
+        float sum = red[0][tq][16 * m + ln];
 #pragma unroll
         for (int k = 1; k < MAXW; k++) {
-            const float v = red[k][kg][ln];
+            const float v = red[k][tq][16 * m + ln];
             sum += k < KS ? v : 0.0f;
         }
-        const TileSel& tt = (TP > 1 && kg) ? tsv[TP - 1] : tsv[0];
-        if (tt.row0 + ln < tt.m.N) tt.m.y[tt.row0 + ln] = sum + __uint_as_float(bias << 16);
+        const TileSel& tt = (TP > 1 && tq) ? tsv[TP - 1] : tsv[0];
+        if (tt.row0 + ln < tt.m.N) tt.m.y[int64_t(m) * tt.m.N + tt.row0 + ln] = sum + __uint_as_float(bias << 16);
         return;
     }
     float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, RS, glo, M < RR ? M : RR, gbeg, gs, ln, kg);
@@ -1162,7 +1164,9 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
     }
     if (p.M == 2) {
         if constexpr (NG <= (KIND == 1 ? 4 : 8)) {
-            if (mode == 2) {
+            if (mode == 2 && tp == 2) {
+                if constexpr (NG == 4 && KIND == 1) IQ_G1X(2, 2, false, false, 2);
+            } else if (mode == 2) {
                 if (p.kr > 1) IQ_G1(2, 2, true);
                 else IQ_G1(2, 2, false);
             } else {
@@ -1242,13 +1246,13 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         p.S = 2;
         lds = staged;
     }
-    // int4, 1 row, staged, 4-group slices, >= 6 waves: two tiles per
-    // workgroup (TP = 2; 7B gate|up, 7 waves, 16.4 -> 15.7 us; 1.5B
-    // gate|up, 3 waves, lost: 6.2 -> 6.7 us).  Not int8 (lm_head 88 ->
-    // 92-98 us: two tiles' int8 words take the instance to 97 VGPRs, five
-    // waves per SIMD)
+    // int4, 1 or 2 rows, staged, 4-group slices, >= 6 waves: two tiles per
+    // workgroup (TP = 2; 7B gate|up, 7 waves, 16.4 -> 15.7 us at 1 row,
+    // 21.3 -> 17.9 us at 2 (2-row step 1488 -> 1439 us); 1.5B gate|up, 3
+    // waves, lost: 6.2 -> 6.7 us).  Not int8 (lm_head 88 -> 92-98 us: two
+    // tiles' int8 words take the instance to 97 VGPRs, five waves per SIMD)
     int tp = 1;
-    if (W[0].kind == 1 && M == 1 && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 6) {
+    if (W[0].kind == 1 && M <= 2 && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 6) {
         tp = 2;
         lds += size_t(G) * 48;
     }

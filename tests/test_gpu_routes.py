@@ -137,7 +137,7 @@ def test_prefill_gemm_t1024_down(kind, xtype):
 
 
 @pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M", [1, 3, 4, 9, 12, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 9, 12, 16])
 def test_gate_up_7b_multi(kind, M):
     """gate|up of one 7B layer in one iq_gemv_multi call (2 x 18944 x 3584)."""
     rng = np.random.default_rng(900 + 20 * kind + M)
@@ -152,24 +152,25 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
-def test_one_row_two_tiles_per_workgroup():
-    """int4 at 1 row on a wide call (over 4 workgroups per CU, G = 24: six
+@pytest.mark.parametrize("M", [1, 2])
+def test_one_row_two_tiles_per_workgroup(M):
+    """int4 at 1 and 2 rows on a wide call (over 4 workgroups per CU, G = 24: six
     waves of 4 groups): two 16-row tiles per workgroup.  Matrices of 1025
     (ragged), 20, 3 and 1 tiles in one call with biases: tile pairs that
     straddle two matrices, and an odd tile count, so the last workgroup's
     second tile is past every matrix."""
-    rng = np.random.default_rng(2525)
+    rng = np.random.default_rng(2525 + M)
     K = 3072
     Ws = [Packed(rng, N, K, 1) for N in (16389, 309, 48, 5)]
     bias_bits = [O.seeded_bf16(rng, (W.rows,), 0.5) for W in Ws]
     bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
-    x = rng.standard_normal((1, K), dtype=np.float32)
-    ys = [out_buffer(1, W.rows) for W in Ws]
-    say("1 row, two tiles per workgroup")
-    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, 1, K, ys)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    ys = [out_buffer(M, W.rows) for W in Ws]
+    say("two tiles per workgroup", M)
+    ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, M, K, ys)
     torch.cuda.synchronize()
     for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
-        check_sampled(y, x, W, 1, rng, f"two tiles[{i}]", bias_bits=bb)
+        check_sampled(y, x, W, M, rng, f"two tiles[{i}] M={M}", bias_bits=bb)
 
 
 @pytest.mark.parametrize("kind", [0, 1])
