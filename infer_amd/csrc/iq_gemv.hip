@@ -435,7 +435,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     // records (each wave reuses its own groups' records; the weights stay
     // in registers): half the LDS of one block of R rows.
     static_assert(!HALF || (R == 4 && !KSPLIT), "two 2-row blocks: the 4-row instance, one K range");
-    static_assert(TP == 1 || (R <= 2 && MODE == 2 && !KSPLIT), "two tiles: 1 or 2 rows, staged metadata");
+    static_assert(TP == 1 || (R <= 4 && !HALF && MODE == 2 && !KSPLIT), "two tiles: 1..4 rows, staged metadata");
     constexpr int RR = HALF ? R / 2 : (R < 4 ? R : 4);  // rows per block
     constexpr int RB = R / RR;                          // blocks
     extern __shared__ __attribute__((aligned(16))) int8_t xs1[];
@@ -475,14 +475,15 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
     //    CU's weight misses would arrive only after them.
     //    The bias of the rows this lane may store goes first (lanes 0..15 of
     //    every wave: any wave may be the one that finishes the tile).
-    uint32_t bias = 0;
+    uint32_t biasv[TP];
 #pragma unroll
     for (int t = 0; t < TP; t++) {
-        // (TP = 2: lanes 16t .. 16t + 15 take tile t's; the others read zero)
+        // (TP = 2: every lane takes row ln of both tiles)
         const rsrc_t rb = make_rsrc(tsv[t].m.bias, tsv[t].m.bias ? tsv[t].m.N * 2 : 0);
-        const bool mine = (TP == 1 ? lane < 16 * (M < 4 ? M : 4) : kg / RR == t) && live;
-        bias |= __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(tsv[t].row0 + ln) * 2 : kOob, 0, 0);
+        const bool mine = (TP == 1 ? lane < 16 * (M < 4 ? M : 4) : true) && live;
+        biasv[t] = __builtin_amdgcn_raw_buffer_load_b16(rb, mine ? uint32_t(tsv[t].row0 + ln) * 2 : kOob, 0, 0);
     }
+    const uint32_t bias = biasv[0];
     constexpr int XP = NG / 4;
     float xv[R][XP][8];
 #pragma unroll
@@ -584,17 +585,22 @@ __global__ __launch_bounds__(64 * MAXW) void gemv1_kernel(const GemvParams p) {
         int prior = 0;
         if (lane == 0) prior = __hip_atomic_fetch_add(&arrived, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
         prior = __builtin_amdgcn_readfirstlane(prior);
-        // lane group kg = RR t + m: tile t, activation row m
-        const int tq = kg / RR, m = kg % RR;
-        if (prior != KS - 1 || tq >= TP || m >= M) return;
-        float sum = red[0][tq][16 * m + ln];
+        if (prior != KS - 1) return;
+        // (tile t, activation row m) pairs RR t + m = kg + 4 j
 #pragma unroll
-        for (int k = 1; k < MAXW; k++) {
-            const float v = red[k][tq][16 * m + ln];
-            sum += k < KS ? v : 0.0f;
+        for (int j = 0; j < (TP * RR + 3) / 4; j++) {
+            const int pr = kg + 4 * j, tq = pr / RR, m = pr % RR;
+            if (tq >= TP || m >= M) break;
+            float sum = red[0][tq][16 * m + ln];
+#pragma unroll
+            for (int k = 1; k < MAXW; k++) {
+                const float v = red[k][tq][16 * m + ln];
+                sum += k < KS ? v : 0.0f;
+            }
+            const TileSel& tt = (TP > 1 && tq) ? tsv[TP - 1] : tsv[0];
+            const uint32_t bv = (TP > 1 && tq) ? biasv[TP - 1] : biasv[0];
+            if (tt.row0 + ln < tt.m.N) tt.m.y[int64_t(m) * tt.m.N + tt.row0 + ln] = sum + __uint_as_float(bv << 16);
         }
-        const TileSel& tt = (TP > 1 && tq) ? tsv[TP - 1] : tsv[0];
-        if (tt.row0 + ln < tt.m.N) tt.m.y[int64_t(m) * tt.m.N + tt.row0 + ln] = sum + __uint_as_float(bias << 16);
         return;
     }
     float acc = slice_dot<KIND, NG, RR>(b, xs1, ms1, xzero, RS, glo, M < RR ? M : RR, gbeg, gs, ln, kg);
@@ -1183,6 +1189,8 @@ void launch_gemv1_m(const GemvParams& p, int mode, int ks, unsigned grid, size_t
                     if (mode == 2) IQ_G1H(2, 4, false, true);
                     else IQ_G1H(1, 4, false, true);
                 }
+            } else if (mode == 2 && tp == 2) {
+                if constexpr (NG == 4 && KIND == 1) IQ_G1X(2, 4, false, false, 2);
             } else if (mode == 2) {
                 if (p.kr > 1) IQ_G1(2, 4, true);
                 else IQ_G1(2, 4, false);
@@ -1246,13 +1254,15 @@ hipError_t launch_gemv1(const float* x, const QView* W, const uint16_t* const* b
         p.S = 2;
         lds = staged;
     }
-    // int4, 1 or 2 rows, staged, 4-group slices, >= 6 waves: two tiles per
-    // workgroup (TP = 2; 7B gate|up, 7 waves, 16.4 -> 15.7 us at 1 row,
-    // 21.3 -> 17.9 us at 2 (2-row step 1488 -> 1439 us); 1.5B gate|up, 3
-    // waves, lost: 6.2 -> 6.7 us).  Not int8 (lm_head 88 -> 92-98 us: two
-    // tiles' int8 words take the instance to 97 VGPRs, five waves per SIMD)
+    // int4, 1..4 rows, staged, 4-group slices, >= 6 waves: two tiles per
+    // workgroup (TP = 2; 7B gate|up, 7 waves: 16.4 -> 15.7 us at 1 row,
+    // 21.3 -> 17.9 at 2, 28.0 -> 21.4 at 3 rows; at 4 rows 22.8 us against
+    // 27.5 on gemvr; steps at 2 / 3 / 4 rows 1488 / 1774 / 1835 -> 1439 /
+    // 1630 / 1717 us; 1.5B gate|up, 3 waves, lost: 6.2 -> 6.7 us at 1 row).
+    // Not int8 (lm_head 88 -> 92-98 us: two tiles' int8 words take the
+    // instance to 97 VGPRs, five waves per SIMD)
     int tp = 1;
-    if (W[0].kind == 1 && M <= 2 && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 6) {
+    if (W[0].kind == 1 && M <= 4 && !half && p.S == 2 && pl.ng == 4 && 2 * G <= 64 && pl.ks >= 6) {
         tp = 2;
         lds += size_t(G) * 48;
     }
@@ -2715,6 +2725,10 @@ hipError_t launch_gemv_multi(const float* x, const QView* W, const uint16_t* con
     const int tiles_all = total_tiles(W, n);
     int m_lo = G >= 128 ? 3 : 5;
     if (tiles_all >= 4096 || (W[0].kind == 1 && tiles_all >= 1024)) m_lo = m_lo < 4 ? m_lo : 4;
+    // ... except wide int4 calls whose rows the 1-row kernel's 4-row
+    // instance takes two tiles per workgroup (6..8 waves of 4 groups: 7B
+    // gate|up at 4 rows 27.5 -> 22.8 us)
+    if (W[0].kind == 1 && tiles_all < 4096 && G >= 21 && G <= 32 && G % 4 == 0) m_lo = 5;
     if (M >= m_lo && M <= 8 && K % kGroup == 0 && (total_tiles(W, n) >= 1024 || G >= 128)) {
         hipError_t e = hipSuccess;
         if (launch_gemvr(x, W, bias, y, n, M, ws, stream, &e)) return e;

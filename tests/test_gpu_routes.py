@@ -152,9 +152,9 @@ def test_gate_up_7b_multi(kind, M):
         check_sampled(y, x, W, M, rng, f"gate|up[{i}] kind={kind} M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_one_row_two_tiles_per_workgroup(M):
-    """int4 at 1 and 2 rows on a wide call (over 4 workgroups per CU, G = 24: six
+    """int4 at 1..4 rows on a wide call (over 4 workgroups per CU, G = 24: six
     waves of 4 groups): two 16-row tiles per workgroup.  Matrices of 1025
     (ragged), 20, 3 and 1 tiles in one call with biases: tile pairs that
     straddle two matrices, and an odd tile count, so the last workgroup's
