@@ -730,11 +730,11 @@ int chain_create(const iq_stage* stages, int n, Chain** out) {
         hs.kind = W0.kind;
         const bool i4 = W0.kind == IQ_INT4;
         const int maxw = i4 ? kMaxWaves : kMaxWaves / 2;
-        // (4 rows of a very wide stage, the lm_head: the B-row route, as the
-        // bare GEMV takes gemvr there; 7B chain at 4 sequences 1985 -> 1965
-        // us; a SwiGLU pair stays fused, 26.7 us against 29.2 for gemvr and
-        // its range sums on 7B gate|up)
-        const bool wide4 = rows == 4 && !pair && tiles >= 4096;
+        // (3..4 rows of a very wide stage, the lm_head: the B-row route; 7B
+        // chain at 3 / 4 sequences 1904 / 1985 -> 1885 / 1965 us; a SwiGLU
+        // pair stays fused, 26.7 us against 29.2 for gemvr and its range
+        // sums on 7B gate|up at 4 rows)
+        const bool wide4 = rows >= 3 && rows <= 4 && !pair && tiles >= 4096;
         if (rows > 1 && rows <= 4 && !wide4 && G <= int64_t(4) * maxw &&
             size_t(rows <= 2 ? 2 : 4) * size_t(G) * (kLimbRec + 16) <= 160 * 1024) {
             // 2..4 rows on short rows: one fused launch (the R-row

@@ -261,8 +261,8 @@ def test_chain_rows_small_model_matches_forward(B, kind, head_kind):
 @pytest.mark.parametrize("B", [2, 3, 4, 16, 32])
 def test_chain_rows_7b_shapes_sampled(B):
     """The 7B program (28 int4 layers, int8 lm_head) at B rows: at 2..4 rows
-    q|k|v, o, gate|up and (2..3 rows) the head on fused R-row stages, down
-    (K = 18944) and the head at 4 rows on the B-row stages (at 2 rows the
+    q|k|v, o, gate|up and (2 rows) the head on fused R-row stages, down
+    (K = 18944) and the head at 3..4 rows on the B-row stages (at 2 rows the
     1-row kernel's K-split instance writing the epilogue's range sums); at
     16 / 32 gate|up on the 32-row tile kernel; stage by stage on sampled
     output rows of a few layers and sequences."""
