@@ -809,6 +809,37 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
     y[i] = sum + (bias ? bf16_to_f32(bias[i % N]) : 0.0f);
 }
 
+// The same, four consecutive outputs per thread (N % 4 == 0: they share a
+// row; y 16-byte aligned): one 16-byte load per range, the ranges added in
+// the same order, so the sums are gemm_reduce_kernel's bit for bit (7B gate
+// at T = 256: 117.6 -> 113.9 us with fp32, 83.9 -> 80.6 with bf16
+// activations; where the partial sums are small, no change).
+__global__ __launch_bounds__(256) void gemm_reduce4_kernel(const float* __restrict__ part, int S, int64_t T,
+                                                           int64_t N, const uint16_t* __restrict__ bias,
+                                                           float* __restrict__ y) {
+    const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= T * N) return;
+    const int64_t stride = T * N;
+    const rsrc_t r = make_rsrc(part, int64_t(S) * stride * 4);
+    float4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        float4_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t off = s0 + j < S ? uint32_t((int64_t(s0 + j) * stride + i) * 4) : kOob;
+            v[j] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (s0 + j < S) sum += v[j];
+    }
+    const int64_t n = i % N;
+    float4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = sum[e] + (bias ? bf16_to_f32(bias[n + e]) : 0.0f);
+    *reinterpret_cast<float4_t*>(y + i) = o;
+}
+
 template <int KIND, bool XF32, int NJ>
 void launch_gemm_t(const GemmParams& p, bool fastw, bool fastx, int bm, hipStream_t stream) {
     const unsigned grid = unsigned(p.tiles_m * p.tiles_n * p.splits);
@@ -898,7 +929,10 @@ void launch_gemm_nj(GemmParams& p, bool fastw, bool fastx, int bm, int64_t part_
     }
     if (p.splits > 1) {
         const int64_t n = p.T * p.N;
-        gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
+        if (p.N % 4 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0)
+            gemm_reduce4_kernel<<<unsigned((n / 4 + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
+        else
+            gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
     }
 }
 
@@ -976,7 +1010,10 @@ hipError_t launch_gemmh_chunk(const float* x_f32, const QView& W, const uint16_t
     }
     if (p.splits > 1) {
         const int64_t n = p.T * p.N;
-        gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
+        if (p.N % 4 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0)
+            gemm_reduce4_kernel<<<unsigned((n / 4 + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
+        else
+            gemm_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(p.part, p.splits, p.T, p.N, p.bias, p.y);
     }
     return hipGetLastError();
 }
