@@ -383,6 +383,43 @@ def test_gemm_three_k_ranges(kind):
             check_sampled(y, O.bf16_to_f32(xb), W, T, rng, f"iq_gemm_bf16x {N}x{K} T={T} kind={kind}")
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+def test_random_shapes_across_routes(kind):
+    """A seeded sweep over the routing space: 24 random (rows, columns,
+    activation rows) with whole-group or ragged K, one to three matrices
+    per call below 33 rows (iq_gemv_multi) and the GEMM past it, with
+    biases, on sampled output rows against the oracle."""
+    rng = np.random.default_rng(8800 + kind)
+    for case in range(24):
+        G = int(rng.integers(1, 160))
+        K = 128 * G if rng.random() < 0.8 else 128 * G + 2 * int(rng.integers(1, 63))
+        N = int(rng.integers(1, 40000 if K <= 4096 else 6000))
+        M = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 24, 32, 33, 64, 65, 128, 200]))
+        if M > 32:
+            W = Packed(rng, N, K, kind)
+            x = rng.standard_normal((M, K), dtype=np.float32)
+            bb = O.seeded_bf16(rng, (N,), 0.5)
+            y = out_buffer(M, N)
+            say("random shapes", kind, case, N, K, M)
+            ops.launch_gemm_tiled_q(torch.from_numpy(x).cuda(), W.view, torch.from_numpy(bb.view(np.int16)).cuda(),
+                                    M, K, N, y)
+            torch.cuda.synchronize()
+            check_sampled(y, x, W, M, rng, f"random gemm {N}x{K} M={M} kind={kind}", bias_bits=bb)
+            continue
+        n = int(rng.integers(1, 4))
+        Ns = [N] + [int(rng.integers(1, 5000)) for _ in range(n - 1)]
+        Ws = [Packed(rng, Ni, K, kind) for Ni in Ns]
+        bias_bits = [O.seeded_bf16(rng, (Ni,), 0.5) for Ni in Ns]
+        bias = [torch.from_numpy(b.view(np.int16)).cuda() for b in bias_bits]
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        ys = [out_buffer(M, Ni) for Ni in Ns]
+        say("random shapes", kind, case, Ns, K, M)
+        ops.gemv_multi(torch.from_numpy(x).cuda(), [W.view for W in Ws], bias, M, K, ys)
+        torch.cuda.synchronize()
+        for i, (W, y, bb) in enumerate(zip(Ws, ys, bias_bits)):
+            check_sampled(y, x, W, M, rng, f"random {Ns[i]}x{K} M={M} kind={kind} [{i}]", bias_bits=bb)
+
+
 def test_gemvq_looped_k_ranges():
     """gemvq where one K range per workgroup would need more partial sums
     than the workspace holds, so each workgroup loops over several ranges:
